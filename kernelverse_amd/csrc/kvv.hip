@@ -1,0 +1,516 @@
+// libkvv: MI355X verdict library -- C ABI entry points (include/kvv.h),
+// planning (dimension coalescing, layout and access choice, workspace
+// layout) and the launch sequence of the verdict kernels.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kvv.h"
+#include "kvv_kernels.h"
+
+namespace kvv {
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define KVV_HIP(call)                                                                   \
+  do {                                                                                  \
+    hipError_t e_ = (call);                                                             \
+    if (e_ != hipSuccess) return fail(KVV_E_HIP, std::string(#call) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+constexpr int64_t kMaxNumel = int64_t(1) << 40;
+constexpr int64_t kMaxSamplesCap = int64_t(1) << 24;
+
+int elem_size(int dt) {
+  switch (dt) {
+    case KVV_F32: case KVV_I32: return 4;
+    case KVV_F16: case KVV_BF16: case KVV_I16: return 2;
+    case KVV_F64: case KVV_I64: return 8;
+    case KVV_F8E4M3FN: case KVV_F8E5M2: case KVV_I8: case KVV_U8: case KVV_BOOL: return 1;
+    default: return 0;
+  }
+}
+
+int item_elems_for(int dt) { return kBlock * (16 / elem_size(dt)) * kUnroll; }
+
+int device_cus() {
+  static thread_local int cached_dev = -1, cached_cus = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev != cached_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached_dev = dev;
+    cached_cus = cus;
+  }
+  return cached_cus;
+}
+
+// Coalesces the joint (size, gen stride, ref stride) dims and picks the layout.
+int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, SegDesc& d) {
+  if (!g || !r || !p) return fail(KVV_E_INVALID, "null tensor or policy");
+  if (g->dtype != r->dtype) return fail(KVV_E_INVALID, "generated and reference dtypes differ");
+  const int es = elem_size(r->dtype);
+  if (es == 0) return fail(KVV_E_INVALID, "unknown dtype code " + std::to_string(r->dtype));
+  if (g->ndim != r->ndim || r->ndim < 0 || r->ndim > KVV_MAX_DIMS)
+    return fail(KVV_E_INVALID, "ndim mismatch or out of range");
+  int64_t n = 1;
+  for (int i = 0; i < r->ndim; ++i) {
+    if (g->sizes[i] != r->sizes[i]) return fail(KVV_E_INVALID, "shapes differ");
+    if (r->sizes[i] < 0) return fail(KVV_E_INVALID, "negative size");
+    if (r->sizes[i] > 0 && n > kMaxNumel / r->sizes[i]) return fail(KVV_E_UNSUPPORTED, "more than 2^40 elements");
+    n *= r->sizes[i];
+  }
+  if (n > kMaxNumel) return fail(KVV_E_UNSUPPORTED, "more than 2^40 elements");
+  if (p->mode != KVV_MODE_ISCLOSE && p->mode != KVV_MODE_MAX_ABS_DIFF) return fail(KVV_E_INVALID, "bad mode");
+  if (p->mode == KVV_MODE_MAX_ABS_DIFF && (p->max_abs_diff < INT32_MIN || p->max_abs_diff > INT32_MAX))
+    return fail(KVV_E_INVALID, "max_abs_diff does not fit int32");
+  if (p->max_samples < 2 || p->max_samples > kMaxSamplesCap)
+    return fail(KVV_E_INVALID, "max_samples must be in [2, 2^24]");
+  if (n > 0 && (!g->data || !r->data)) return fail(KVV_E_INVALID, "null data pointer");
+
+  std::memset(&d, 0, sizeof(d));
+  d.g = g->data;
+  d.r = r->data;
+  d.n = n;
+  d.max_samples = p->max_samples;
+  d.m = n < p->max_samples ? n : p->max_samples;
+  d.mode = p->mode;
+  d.flags = p->flags;
+  d.rtol = (float)p->rtol;
+  d.atol = (float)p->atol;
+  d.zero_tol = (p->rtol == 0.0 && p->atol == 0.0) ? 1 : 0;
+  d.max_abs_diff = (int32_t)p->max_abs_diff;
+  d.nz_abs = (float)p->near_zero_abs;
+  d.nz_bad = (float)p->near_zero_bad_abs;
+  d.dtype = r->dtype;
+  d.item_elems = item_elems_for(r->dtype);
+
+  // joint coalescing: drop size-1 dims, merge i into i+1 when both strides chain
+  int64_t sz[KVV_MAX_DIMS], gs[KVV_MAX_DIMS], rs[KVV_MAX_DIMS];
+  int nd = 0;
+  for (int i = 0; i < r->ndim; ++i) {
+    if (r->sizes[i] == 1) continue;
+    if (nd > 0 && gs[nd - 1] == g->strides[i] * r->sizes[i] && rs[nd - 1] == r->strides[i] * r->sizes[i]) {
+      sz[nd - 1] *= r->sizes[i];
+      gs[nd - 1] = g->strides[i];
+      rs[nd - 1] = r->strides[i];
+    } else {
+      sz[nd] = r->sizes[i];
+      gs[nd] = g->strides[i];
+      rs[nd] = r->strides[i];
+      ++nd;
+    }
+  }
+  const int V = 16 / es;
+  const bool aligned = (reinterpret_cast<uintptr_t>(g->data) % 16 == 0) && (reinterpret_cast<uintptr_t>(r->data) % 16 == 0);
+  if (n == 0 || nd == 0 || (nd == 1 && gs[0] == 1 && rs[0] == 1)) {
+    d.layout = L_CONTIG;
+    d.vec = aligned;
+  } else if (gs[nd - 1] == 1 && rs[nd - 1] == 1) {
+    d.layout = L_ROWS;
+    d.row_len = sz[nd - 1];
+    d.dims.ndim = nd - 1;
+    bool ok = aligned && (d.row_len % V == 0);
+    for (int i = 0; i < nd - 1; ++i) {
+      d.dims.sizes[i] = sz[i];
+      d.dims.gstr[i] = gs[i];
+      d.dims.rstr[i] = rs[i];
+      ok = ok && ((gs[i] * es) % 16 == 0) && ((rs[i] * es) % 16 == 0);
+    }
+    d.vec = ok;
+  } else {
+    d.layout = L_GENERIC;
+    d.dims.ndim = nd;
+    for (int i = 0; i < nd; ++i) {
+      d.dims.sizes[i] = sz[i];
+      d.dims.gstr[i] = gs[i];
+      d.dims.rstr[i] = rs[i];
+    }
+    d.vec = 0;
+  }
+  d.item_count = (n + d.item_elems - 1) / d.item_elems;
+  d.chunk_count = (d.m + kSelChunk - 1) / kSelChunk;
+  return KVV_OK;
+}
+
+// ------------------------------------------------------------ kernel tables
+using ScanFn = void (*)(ScanArgs);
+using NearFn = void (*)(NearArgs);
+
+template <int DT>
+struct Kern {
+  static ScanFn scan(int mode) {
+    return mode == KVV_MODE_ISCLOSE ? (ScanFn)scan_kernel<DT, KVV_MODE_ISCLOSE> : (ScanFn)scan_kernel<DT, KVV_MODE_MAX_ABS_DIFF>;
+  }
+  static NearFn near(int mode) {
+    return mode == KVV_MODE_ISCLOSE ? (NearFn)near_kernel<DT, KVV_MODE_ISCLOSE> : (NearFn)near_kernel<DT, KVV_MODE_MAX_ABS_DIFF>;
+  }
+};
+
+void kernels_for(int dt, int mode, ScanFn& s, NearFn& nr) {
+  switch (dt) {
+#define KVV_CASE(X) case X: s = Kern<X>::scan(mode); nr = Kern<X>::near(mode); return;
+    KVV_CASE(KVV_F32) KVV_CASE(KVV_F16) KVV_CASE(KVV_BF16) KVV_CASE(KVV_F64) KVV_CASE(KVV_F8E4M3FN)
+    KVV_CASE(KVV_F8E5M2) KVV_CASE(KVV_I8) KVV_CASE(KVV_U8) KVV_CASE(KVV_I16) KVV_CASE(KVV_I32)
+    KVV_CASE(KVV_I64) KVV_CASE(KVV_BOOL)
+#undef KVV_CASE
+    default: s = nullptr; nr = nullptr;
+  }
+}
+
+// ------------------------------------------------------------ workspace
+struct WsLayout {
+  size_t runs, run_valid, sample_abs, sample_rel, hist, nan_cnt, item_near, item_near_off, item_near_sum, near_sample,
+      table, chunk_seg, total;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+WsLayout workspace_layout(int64_t items, int64_t samples, int64_t nseg, int64_t chunks, bool near, bool batch) {
+  WsLayout L{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off += align256(bytes);
+    return at;
+  };
+  L.runs = take((size_t)items * sizeof(RunRec));
+  L.run_valid = take((size_t)items * 4);
+  L.sample_abs = take((size_t)samples * 4);
+  L.sample_rel = take((size_t)samples * 4);
+  L.hist = take((size_t)nseg * kHistPerSeg * 4);
+  L.nan_cnt = take((size_t)nseg * kArrays * 4);
+  if (near) {
+    L.item_near = take((size_t)items * 4);
+    L.item_near_off = take((size_t)items * 8);
+    L.item_near_sum = take((size_t)items * 8);
+    L.near_sample = take((size_t)samples * 4);
+  }
+  if (batch) {
+    L.table = take((size_t)nseg * sizeof(SegDesc));
+    L.chunk_seg = take((size_t)chunks * 8);
+  }
+  L.total = off + 256;
+  return L;
+}
+
+template <typename T>
+T* at(void* ws, size_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
+}
+
+int64_t blocks_target() { return (int64_t)device_cus() * 4; }
+
+// ------------------------------------------------------------ one verdict
+int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st,
+               hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr) {
+  SegDesc d = d0;
+  d.item_begin = 0;
+  d.sample_off = 0;
+  d.chunk_begin = 0;
+  const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
+  const WsLayout L = workspace_layout(d.item_count, d.m, 1, d.chunk_count, near, false);
+  if (!ws) return fail(KVV_E_WORKSPACE, "workspace is null");
+  if (ws_bytes < L.total) return fail(KVV_E_WORKSPACE, "workspace too small: need " + std::to_string(L.total));
+  if (reinterpret_cast<uintptr_t>(ws) % 256) return fail(KVV_E_WORKSPACE, "workspace must be 256-byte aligned");
+  if (!out) return fail(KVV_E_INVALID, "null result pointer");
+  ScanFn scan;
+  NearFn nearfn;
+  kernels_for(d.dtype, d.mode, scan, nearfn);
+  if (!scan) return fail(KVV_E_INVALID, "no kernel for dtype");
+
+  if (d.item_count > 0) {
+    ScanArgs a{};
+    a.seg0 = d;
+    a.table = nullptr;
+    a.nseg = 1;
+    a.item_lo = 0;
+    a.items = d.item_count;
+    const int64_t target = blocks_target();
+    a.items_per_block = (d.item_count + target - 1) / target;
+    a.runs = at<RunRec>(ws, L.runs);
+    a.run_valid = at<uint32_t>(ws, L.run_valid);
+    a.sample_abs = at<float>(ws, L.sample_abs);
+    a.sample_rel = at<float>(ws, L.sample_rel);
+    a.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
+    const int64_t grid = (d.item_count + a.items_per_block - 1) / a.items_per_block;
+    if (ev_begin) KVV_HIP(hipEventRecord(ev_begin, st));
+    hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
+    KVV_HIP(hipGetLastError());
+    if (ev_end) KVV_HIP(hipEventRecord(ev_end, st));
+  }
+  ReduceArgs ra{};
+  ra.seg0 = d;
+  ra.table = nullptr;
+  ra.runs = at<RunRec>(ws, L.runs);
+  ra.run_valid = at<uint32_t>(ws, L.run_valid);
+  ra.out = out;
+  ra.hist = at<uint32_t>(ws, L.hist);
+  ra.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
+  ra.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
+  ra.item_near_off = near ? at<uint64_t>(ws, L.item_near_off) : nullptr;
+  hipLaunchKernelGGL(reduce_kernel, dim3(1), dim3(kReduceBlock), 0, st, ra);
+  KVV_HIP(hipGetLastError());
+
+  if (near && d.item_count > 0) {
+    NearArgs na{};
+    na.seg0 = d;
+    na.table = nullptr;
+    na.nseg = 1;
+    na.item_lo = 0;
+    na.items = d.item_count;
+    na.res = out;
+    na.item_near_off = at<uint64_t>(ws, L.item_near_off);
+    na.item_near = at<uint32_t>(ws, L.item_near);
+    na.near_sample = at<float>(ws, L.near_sample);
+    na.item_near_sum = at<double>(ws, L.item_near_sum);
+    hipLaunchKernelGGL(nearfn, dim3((unsigned)d.item_count), dim3(kBlock), 0, st, na);
+    KVV_HIP(hipGetLastError());
+  }
+  const int narr = near ? 3 : 2;
+  if (d.chunk_count > 0) {
+    SelectArgs sa{};
+    sa.seg0 = d;
+    sa.table = nullptr;
+    sa.chunk_seg = nullptr;
+    sa.nseg = 1;
+    sa.narrays = narr;
+    sa.total_chunks = d.chunk_count;
+    sa.res = out;
+    sa.arr[0] = at<float>(ws, L.sample_abs);
+    sa.arr[1] = at<float>(ws, L.sample_rel);
+    sa.arr[2] = near ? at<float>(ws, L.near_sample) : nullptr;
+    sa.hist = at<uint32_t>(ws, L.hist);
+    sa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
+    for (int pass = 0; pass < kSelPasses; ++pass) {
+      sa.pass = pass;
+      hipLaunchKernelGGL(select_kernel, dim3((unsigned)(narr * d.chunk_count)), dim3(kBlock), 0, st, sa);
+      KVV_HIP(hipGetLastError());
+    }
+  }
+  FinalArgs fa{};
+  fa.seg0 = d;
+  fa.table = nullptr;
+  fa.narrays = narr;
+  fa.res = out;
+  fa.hist = at<uint32_t>(ws, L.hist);
+  fa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
+  fa.item_near_sum = near ? at<double>(ws, L.item_near_sum) : nullptr;
+  hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(64), 0, st, fa);
+  KVV_HIP(hipGetLastError());
+  return KVV_OK;
+}
+
+// ------------------------------------------------------------ batch
+struct BatchPlan {
+  std::vector<SegDesc> table;       // sorted by (dtype, mode) group, then input order
+  std::vector<int64_t> chunk_seg;
+  struct Group { int dt, mode; int seg_lo, seg_hi; int64_t item_lo, items; };
+  std::vector<Group> groups;
+  int64_t items = 0, samples = 0, chunks = 0;
+  bool near = false;
+};
+
+int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, const kvv_policy* pols, BatchPlan& bp) {
+  if (count < 0) return fail(KVV_E_INVALID, "negative count");
+  if (count > 0 && (!gens || !refs || !pols)) return fail(KVV_E_INVALID, "null batch arrays");
+  std::vector<SegDesc> segs((size_t)count);
+  std::vector<int> order((size_t)count);
+  for (int i = 0; i < count; ++i) {
+    int rc = plan_segment(&gens[i], &refs[i], &pols[i], segs[i]);
+    if (rc) return fail(rc, "pair " + std::to_string(i) + ": " + g_err);
+    segs[i].out_index = i;
+    order[i] = i;
+  }
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+    const int ka = segs[a].dtype * 2 + segs[a].mode, kb = segs[b].dtype * 2 + segs[b].mode;
+    return ka < kb;
+  });
+  bp.table.clear();
+  for (int i : order) bp.table.push_back(segs[i]);
+  int64_t item = 0, sample = 0, chunk = 0;
+  for (size_t s = 0; s < bp.table.size(); ++s) {
+    SegDesc& d = bp.table[s];
+    d.item_begin = item;
+    d.sample_off = sample;
+    d.chunk_begin = chunk;
+    item += d.item_count;
+    sample += d.m;
+    for (int64_t c = 0; c < d.chunk_count; ++c) bp.chunk_seg.push_back((int64_t)s);
+    chunk += d.chunk_count;
+    bp.near = bp.near || (d.flags & KVV_FLAG_NEAR_ZERO);
+    if (bp.groups.empty() || bp.groups.back().dt != d.dtype || bp.groups.back().mode != d.mode) {
+      bp.groups.push_back({d.dtype, d.mode, (int)s, (int)s + 1, d.item_begin, d.item_count});
+    } else {
+      bp.groups.back().seg_hi = (int)s + 1;
+      bp.groups.back().items += d.item_count;
+    }
+  }
+  bp.items = item;
+  bp.samples = sample;
+  bp.chunks = chunk;
+  return KVV_OK;
+}
+
+int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st) {
+  const int nseg = (int)bp.table.size();
+  if (nseg == 0) return KVV_OK;
+  const WsLayout L = workspace_layout(bp.items, bp.samples, nseg, bp.chunks, bp.near, true);
+  if (!ws) return fail(KVV_E_WORKSPACE, "workspace is null");
+  if (ws_bytes < L.total) return fail(KVV_E_WORKSPACE, "workspace too small: need " + std::to_string(L.total));
+  if (reinterpret_cast<uintptr_t>(ws) % 256) return fail(KVV_E_WORKSPACE, "workspace must be 256-byte aligned");
+  if (!out) return fail(KVV_E_INVALID, "null result pointer");
+  SegDesc* dtable = at<SegDesc>(ws, L.table);
+  int64_t* dchunk = at<int64_t>(ws, L.chunk_seg);
+  KVV_HIP(hipMemcpyAsync(dtable, bp.table.data(), nseg * sizeof(SegDesc), hipMemcpyHostToDevice, st));
+  if (bp.chunks) KVV_HIP(hipMemcpyAsync(dchunk, bp.chunk_seg.data(), bp.chunks * 8, hipMemcpyHostToDevice, st));
+  const int64_t target = blocks_target();
+  for (const auto& gr : bp.groups) {
+    if (gr.items == 0) continue;
+    ScanFn scan;
+    NearFn nearfn;
+    kernels_for(gr.dt, gr.mode, scan, nearfn);
+    ScanArgs a{};
+    a.table = dtable + gr.seg_lo;
+    a.nseg = gr.seg_hi - gr.seg_lo;
+    a.item_lo = gr.item_lo;
+    a.items = gr.items;
+    a.items_per_block = (gr.items + target - 1) / target;
+    a.runs = at<RunRec>(ws, L.runs);
+    a.run_valid = at<uint32_t>(ws, L.run_valid);
+    a.sample_abs = at<float>(ws, L.sample_abs);
+    a.sample_rel = at<float>(ws, L.sample_rel);
+    a.item_near = bp.near ? at<uint32_t>(ws, L.item_near) : nullptr;
+    const int64_t grid = (gr.items + a.items_per_block - 1) / a.items_per_block;
+    hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
+    KVV_HIP(hipGetLastError());
+  }
+  ReduceArgs ra{};
+  ra.table = dtable;
+  ra.runs = at<RunRec>(ws, L.runs);
+  ra.run_valid = at<uint32_t>(ws, L.run_valid);
+  ra.out = out;
+  ra.hist = at<uint32_t>(ws, L.hist);
+  ra.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
+  ra.item_near = bp.near ? at<uint32_t>(ws, L.item_near) : nullptr;
+  ra.item_near_off = bp.near ? at<uint64_t>(ws, L.item_near_off) : nullptr;
+  hipLaunchKernelGGL(reduce_kernel, dim3(nseg), dim3(kReduceBlock), 0, st, ra);
+  KVV_HIP(hipGetLastError());
+  if (bp.near) {
+    for (const auto& gr : bp.groups) {
+      if (gr.items == 0) continue;
+      ScanFn scan;
+      NearFn nearfn;
+      kernels_for(gr.dt, gr.mode, scan, nearfn);
+      NearArgs na{};
+      na.table = dtable + gr.seg_lo;
+      na.nseg = gr.seg_hi - gr.seg_lo;
+      na.item_lo = gr.item_lo;
+      na.items = gr.items;
+      na.res = out;
+      na.item_near_off = at<uint64_t>(ws, L.item_near_off);
+      na.item_near = at<uint32_t>(ws, L.item_near);
+      na.near_sample = at<float>(ws, L.near_sample);
+      na.item_near_sum = at<double>(ws, L.item_near_sum);
+      hipLaunchKernelGGL(nearfn, dim3((unsigned)gr.items), dim3(kBlock), 0, st, na);
+      KVV_HIP(hipGetLastError());
+    }
+  }
+  const int narr = bp.near ? 3 : 2;
+  if (bp.chunks > 0) {
+    SelectArgs sa{};
+    sa.table = dtable;
+    sa.chunk_seg = dchunk;
+    sa.nseg = nseg;
+    sa.narrays = narr;
+    sa.total_chunks = bp.chunks;
+    sa.res = out;
+    sa.arr[0] = at<float>(ws, L.sample_abs);
+    sa.arr[1] = at<float>(ws, L.sample_rel);
+    sa.arr[2] = bp.near ? at<float>(ws, L.near_sample) : nullptr;
+    sa.hist = at<uint32_t>(ws, L.hist);
+    sa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
+    for (int pass = 0; pass < kSelPasses; ++pass) {
+      sa.pass = pass;
+      hipLaunchKernelGGL(select_kernel, dim3((unsigned)(narr * bp.chunks)), dim3(kBlock), 0, st, sa);
+      KVV_HIP(hipGetLastError());
+    }
+  }
+  FinalArgs fa{};
+  fa.table = dtable;
+  fa.narrays = narr;
+  fa.res = out;
+  fa.hist = at<uint32_t>(ws, L.hist);
+  fa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
+  fa.item_near_sum = bp.near ? at<double>(ws, L.item_near_sum) : nullptr;
+  hipLaunchKernelGGL(finalize_kernel, dim3(nseg), dim3(64), 0, st, fa);
+  KVV_HIP(hipGetLastError());
+  return KVV_OK;
+}
+
+}  // namespace
+}  // namespace kvv
+
+// ================================================================ C ABI
+extern "C" {
+
+int kvv_abi_version(void) { return KVV_ABI_VERSION; }
+
+const char* kvv_last_error(void) { return kvv::g_err.c_str(); }
+
+int kvv_workspace_size(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy, size_t* bytes) {
+  if (!bytes) return kvv::fail(KVV_E_INVALID, "null bytes pointer");
+  kvv::SegDesc d;
+  int rc = kvv::plan_segment(gen, ref, policy, d);
+  if (rc) return rc;
+  *bytes = kvv::workspace_layout(d.item_count, d.m, 1, d.chunk_count, (d.flags & KVV_FLAG_NEAR_ZERO) != 0, false).total;
+  return KVV_OK;
+}
+
+int kvv_verdict(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy, kvv_result* out,
+                void* workspace, size_t workspace_bytes, void* stream) {
+  kvv::SegDesc d;
+  int rc = kvv::plan_segment(gen, ref, policy, d);
+  if (rc) return rc;
+  return kvv::run_single(d, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int kvv_verdict_timed(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy, kvv_result* out,
+                      void* workspace, size_t workspace_bytes, void* stream, void* main_begin, void* main_end) {
+  kvv::SegDesc d;
+  int rc = kvv::plan_segment(gen, ref, policy, d);
+  if (rc) return rc;
+  return kvv::run_single(d, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                         static_cast<hipEvent_t>(main_begin), static_cast<hipEvent_t>(main_end));
+}
+
+int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs,
+                             const kvv_policy* policies, size_t* bytes) {
+  if (!bytes) return kvv::fail(KVV_E_INVALID, "null bytes pointer");
+  kvv::BatchPlan bp;
+  int rc = kvv::plan_batch(count, gens, refs, policies, bp);
+  if (rc) return rc;
+  *bytes = kvv::workspace_layout(bp.items, bp.samples, (int64_t)bp.table.size(), bp.chunks, bp.near, true).total;
+  return KVV_OK;
+}
+
+int kvv_verdict_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, const kvv_policy* policies,
+                      kvv_result* out, void* workspace, size_t workspace_bytes, void* stream) {
+  kvv::BatchPlan bp;
+  int rc = kvv::plan_batch(count, gens, refs, policies, bp);
+  if (rc) return rc;
+  return kvv::run_batch(bp, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

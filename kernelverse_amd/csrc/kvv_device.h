@@ -1,0 +1,230 @@
+// Device-side element decoding, ordering keys and wave/block reductions for
+// the verdict kernels.  Compiled for gfx950 only (wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kvv.h"
+
+namespace kvv {
+
+constexpr int kBlock = 256;           // threads per block (4 waves of 64)
+constexpr int kWaves = kBlock / 64;
+constexpr int kBuckets = KVV_HIST_BUCKETS;
+constexpr uint64_t kNone = ~0ull;     // "no index yet"
+
+// Per-thread LDS counters (one column per thread, so increments never collide).
+enum LdsCounter {
+  LC_VIOL = 0, LC_NAN_G, LC_NAN_R, LC_PINF_G, LC_PINF_R, LC_NINF_G, LC_NINF_R, LC_NANPAIR,
+  LC_NEAR, LC_FARMM, LC_NEARBAD,
+  LC_HIST0,  // + bucket
+  LC_COUNT = LC_HIST0 + kBuckets
+};
+
+// ---------------------------------------------------------------- float keys
+// Monotone map float -> uint32 (NaN is above +inf): ascending key == ascending value.
+__device__ __forceinline__ uint32_t fkey(float x) {
+  uint32_t b = __float_as_uint(x);
+  if (__builtin_isnan(x)) return 0xFFFFFFFFu;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__host__ __device__ inline float fkey_value(uint32_t k) {
+  if (k == 0xFFFFFFFFu) return __builtin_nanf("");
+  uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  float f;
+  __builtin_memcpy(&f, &b, 4);
+  return f;
+}
+// Monotone map int32 -> uint32.
+__device__ __forceinline__ uint32_t ikey(int32_t x) { return (uint32_t)x ^ 0x80000000u; }
+__host__ __device__ inline int32_t ikey_value(uint32_t k) { return (int32_t)(k ^ 0x80000000u); }
+
+// x86 semantics of float -> int32 truncation (cvttss2si / cvttsd2si): NaN and
+// out-of-range values give INT32_MIN.  torch-CPU's Tensor.to(torch.int32) runs that.
+__device__ __forceinline__ int32_t x86_trunc_i32(double x) {
+  if (!(x > -2147483649.0 && x < 2147483648.0)) return INT32_MIN;
+  return (int32_t)x;
+}
+
+// Bucket of a ULP / integer distance: 0 for 0, else min(bit_length(d), 15).
+__device__ __forceinline__ int ulp_bucket(uint64_t d) {
+  if (d == 0) return 0;
+  int bl = 64 - __clzll(d);
+  return bl < kBuckets - 1 ? bl : kBuckets - 1;
+}
+
+// ------------------------------------------------------------ element traits
+// T is the raw storage type; decoding never rounds except where torch rounds
+// too (float64 -> float32, int64 -> float32).
+template <int DT> struct Elem;
+
+struct FloatElemBase { static constexpr bool is_float = true; };
+struct IntElemBase { static constexpr bool is_float = false; };
+
+template <> struct Elem<KVV_F32> : FloatElemBase {
+  using T = uint32_t;
+  static constexpr int width = 32;
+  __device__ static float f32(T c) { return __uint_as_float(c); }
+  __device__ static double f64(T c) { return (double)__uint_as_float(c); }
+  __device__ static int32_t i32(T c) { return x86_trunc_i32((double)__uint_as_float(c)); }
+  __device__ static bool isnan(T c) { return (c & 0x7FFFFFFFu) > 0x7F800000u; }
+  __device__ static bool isinf(T c) { return (c & 0x7FFFFFFFu) == 0x7F800000u; }
+  __device__ static bool sign(T c) { return c >> 31; }
+  __device__ static uint64_t mag(T c) { return c & 0x7FFFFFFFu; }
+};
+
+template <> struct Elem<KVV_BF16> : FloatElemBase {
+  using T = uint16_t;
+  static constexpr int width = 16;
+  __device__ static float f32(T c) { return __uint_as_float((uint32_t)c << 16); }
+  __device__ static double f64(T c) { return (double)f32(c); }
+  __device__ static int32_t i32(T c) { return x86_trunc_i32((double)f32(c)); }
+  __device__ static bool isnan(T c) { return (c & 0x7FFFu) > 0x7F80u; }
+  __device__ static bool isinf(T c) { return (c & 0x7FFFu) == 0x7F80u; }
+  __device__ static bool sign(T c) { return c >> 15; }
+  __device__ static uint64_t mag(T c) { return c & 0x7FFFu; }
+};
+
+template <> struct Elem<KVV_F16> : FloatElemBase {
+  using T = uint16_t;
+  static constexpr int width = 16;
+  __device__ static float f32(T c) { return (float)__builtin_bit_cast(_Float16, c); }
+  __device__ static double f64(T c) { return (double)f32(c); }
+  __device__ static int32_t i32(T c) { return x86_trunc_i32((double)f32(c)); }
+  __device__ static bool isnan(T c) { return (c & 0x7FFFu) > 0x7C00u; }
+  __device__ static bool isinf(T c) { return (c & 0x7FFFu) == 0x7C00u; }
+  __device__ static bool sign(T c) { return c >> 15; }
+  __device__ static uint64_t mag(T c) { return c & 0x7FFFu; }
+};
+
+template <> struct Elem<KVV_F64> : FloatElemBase {
+  using T = uint64_t;
+  static constexpr int width = 64;
+  __device__ static double f64(T c) { return __longlong_as_double((long long)c); }
+  __device__ static float f32(T c) { return (float)f64(c); }
+  __device__ static int32_t i32(T c) { return x86_trunc_i32(f64(c)); }
+  __device__ static bool isnan(T c) { return (c & 0x7FFFFFFFFFFFFFFFull) > 0x7FF0000000000000ull; }
+  __device__ static bool isinf(T c) { return (c & 0x7FFFFFFFFFFFFFFFull) == 0x7FF0000000000000ull; }
+  __device__ static bool sign(T c) { return c >> 63; }
+  __device__ static uint64_t mag(T c) { return c & 0x7FFFFFFFFFFFFFFFull; }
+};
+
+// OCP float8 e4m3fn: bias 7, no infinities, S.1111.111 is NaN, max 448.
+template <> struct Elem<KVV_F8E4M3FN> : FloatElemBase {
+  using T = uint8_t;
+  static constexpr int width = 8;
+  __device__ static float f32(T c) {
+    const uint32_t s = (uint32_t)(c >> 7) << 31;
+    const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+    if (e == 15u && m == 7u) return __uint_as_float(s | 0x7FC00000u);
+    if (e == 0u) {
+      float v = (float)m * 0x1p-9f;  // exact
+      return __uint_as_float(s | __float_as_uint(v));
+    }
+    return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+  }
+  __device__ static double f64(T c) { return (double)f32(c); }
+  __device__ static int32_t i32(T c) { return x86_trunc_i32((double)f32(c)); }
+  __device__ static bool isnan(T c) { return (c & 0x7Fu) == 0x7Fu; }
+  __device__ static bool isinf(T) { return false; }
+  __device__ static bool sign(T c) { return c >> 7; }
+  __device__ static uint64_t mag(T c) { return c & 0x7Fu; }
+};
+
+// float8 e5m2 is the high byte of an IEEE half.
+template <> struct Elem<KVV_F8E5M2> : FloatElemBase {
+  using T = uint8_t;
+  static constexpr int width = 8;
+  __device__ static float f32(T c) { return (float)__builtin_bit_cast(_Float16, (uint16_t)((uint16_t)c << 8)); }
+  __device__ static double f64(T c) { return (double)f32(c); }
+  __device__ static int32_t i32(T c) { return x86_trunc_i32((double)f32(c)); }
+  __device__ static bool isnan(T c) { return (c & 0x7Fu) > 0x7Cu; }
+  __device__ static bool isinf(T c) { return (c & 0x7Fu) == 0x7Cu; }
+  __device__ static bool sign(T c) { return c >> 7; }
+  __device__ static uint64_t mag(T c) { return c & 0x7Fu; }
+};
+
+template <typename Raw, typename Signed>
+struct IntElem : IntElemBase {
+  using T = Raw;
+  static constexpr int width = 8 * sizeof(Raw);
+  __device__ static int64_t v(T c) { return (int64_t)(Signed)c; }
+  __device__ static float f32(T c) { return (float)v(c); }     // RNE, as torch's int -> float32
+  __device__ static double f64(T c) { return (double)v(c); }
+  __device__ static int32_t i32(T c) { return (int32_t)(uint32_t)(uint64_t)v(c); }  // wraps like .to(int32)
+  __device__ static bool isnan(T) { return false; }
+  __device__ static bool isinf(T) { return false; }
+};
+template <> struct Elem<KVV_I8> : IntElem<uint8_t, int8_t> {};
+template <> struct Elem<KVV_U8> : IntElem<uint8_t, uint8_t> {};
+template <> struct Elem<KVV_I16> : IntElem<uint16_t, int16_t> {};
+template <> struct Elem<KVV_I32> : IntElem<uint32_t, int32_t> {};
+template <> struct Elem<KVV_I64> : IntElem<uint64_t, int64_t> {};
+template <> struct Elem<KVV_BOOL> : IntElemBase {
+  using T = uint8_t;
+  static constexpr int width = 8;
+  __device__ static int64_t v(T c) { return c != 0; }
+  __device__ static float f32(T c) { return c != 0 ? 1.0f : 0.0f; }
+  __device__ static double f64(T c) { return c != 0 ? 1.0 : 0.0; }
+  __device__ static int32_t i32(T c) { return c != 0; }
+  __device__ static bool isnan(T) { return false; }
+  __device__ static bool isinf(T) { return false; }
+};
+
+// ULP / integer distance of a pair (never called for NaN pairs).
+template <int DT>
+__device__ __forceinline__ uint64_t pair_distance(typename Elem<DT>::T g, typename Elem<DT>::T r) {
+  using E = Elem<DT>;
+  if constexpr (E::is_float) {
+    const uint64_t mg = E::mag(g), mr = E::mag(r);
+    if (E::sign(g) == E::sign(r)) return mg > mr ? mg - mr : mr - mg;
+    return mg + mr;  // opposite signs: distance through zero (+0 and -0 coincide)
+  } else {
+    const int64_t a = E::v(g), b = E::v(r);
+    return a > b ? (uint64_t)a - (uint64_t)b : (uint64_t)b - (uint64_t)a;
+  }
+}
+
+// ----------------------------------------------------------------- reductions
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    T w = __shfl_xor(v, o);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_min(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    T w = __shfl_xor(v, o);
+    v = w < v ? w : v;
+  }
+  return v;
+}
+// (key, index) argmax: larger key wins, equal keys -> smaller index.
+__device__ __forceinline__ void wave_argmax(uint32_t& key, uint64_t& idx) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t k = __shfl_xor(key, o);
+    uint64_t i = __shfl_xor(idx, o);
+    if (k > key || (k == key && i < idx)) {
+      key = k;
+      idx = i;
+    }
+  }
+}
+__device__ __forceinline__ bool better(uint32_t k, uint64_t i, uint32_t bk, uint64_t bi) {
+  return k > bk || (k == bk && i < bi);
+}
+
+}  // namespace kvv

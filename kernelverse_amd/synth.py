@@ -1,0 +1,208 @@
+"""Seeded synthetic tensor pairs for the verdict workloads.
+
+Every generator draws from numpy's PCG64 (bit-identical across machines for a
+given numpy version) and casts with torch on the CPU, so a (seed, size) pair
+always yields the same bytes here and on the GPU box.  ``*_device`` variants
+build the same *kind* of pair directly on a GPU with torch's device generator
+(fast, for benchmarking; not byte-identical to the CPU variants).
+
+Workload shapes follow the five benchmark configurations of the verdict:
+
+* ``fp32_noise_pair``   fp32, ref ~ N(0,1), cand = ref + N(0,1e-6), 0.1% of
+  positions pushed by +U(1e-3, 1e-1).
+* ``code_flip_pair``    bf16 / fp16 / fp8: cand = ref with same-sign +-k code
+  steps at seeded positions (so the ULP distance of each step is exactly k).
+* ``fp16_nonfinite_pair``  fp16 U(-60000, 60000) with seeded NaN/+-Inf and a
+  given number of finite-pattern breaks, as a strided (row-pitched) view.
+* ``int8_pair``         int8 U[-128,127], cand differs at exactly k positions.
+* ``ragged_batch``      list of fp32/bf16 pairs with log-uniform sizes.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import List, Tuple
+
+import numpy as np
+import torch
+
+_CODE_INFO = {
+    # dtype: (int view dtype, numpy unsigned dtype, magnitude mask, first non-finite magnitude)
+    torch.bfloat16: (torch.int16, np.uint16, 0x7FFF, 0x7F80),
+    torch.float16: (torch.int16, np.uint16, 0x7FFF, 0x7C00),
+    torch.float8_e4m3fn: (torch.int8, np.uint8, 0x7F, 0x7F),
+    torch.float8_e5m2: (torch.int8, np.uint8, 0x7F, 0x7C),
+}
+
+
+def _rng(seed: int) -> np.random.Generator:
+    return np.random.default_rng(seed)
+
+
+def _distinct_positions(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
+    """k distinct positions in [0, n), sorted."""
+    k = min(k, n)
+    if k == 0:
+        return np.zeros(0, dtype=np.int64)
+    if k * 4 >= n:
+        return np.sort(rng.permutation(n)[:k]).astype(np.int64)
+    pos = np.unique(rng.integers(0, n, size=int(k * 1.3) + 16))
+    while pos.size < k:
+        pos = np.unique(np.concatenate([pos, rng.integers(0, n, size=k)]))
+    return np.sort(rng.permutation(pos)[:k]).astype(np.int64)
+
+
+def fp32_noise_pair(n: int, seed: int, noise: float = 1e-6, frac: float = 1e-3,
+                    lo: float = 1e-3, hi: float = 1e-1) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(cand, ref) fp32: ref ~ N(0,1); cand = ref + N(0,noise); frac of positions get +U(lo,hi)."""
+    rng = _rng(seed)
+    ref = rng.standard_normal(n, dtype=np.float32)
+    cand = ref + (rng.standard_normal(n, dtype=np.float32) * np.float32(noise))
+    pos = _distinct_positions(rng, n, int(round(n * frac)))
+    cand[pos] += rng.uniform(lo, hi, size=pos.size).astype(np.float32)
+    return torch.from_numpy(cand), torch.from_numpy(ref)
+
+
+def step_codes(ref: torch.Tensor, positions: np.ndarray, steps: np.ndarray, rng: np.random.Generator) -> torch.Tensor:
+    """Copy of ``ref`` whose codes at ``positions`` move by ``steps`` code units of magnitude.
+
+    The sign bit is kept and the direction is random but chosen so that the
+    new magnitude stays finite and non-negative: the ULP distance of every
+    moved element to its original is exactly its step.
+    """
+    view, npu, mag_mask, nonfinite = _CODE_INFO[ref.dtype]
+    codes = ref.contiguous().view(view).numpy().view(npu).copy()
+    c = codes[positions].astype(np.int64)
+    sign = c & ~mag_mask
+    mag = c & mag_mask
+    up = rng.integers(0, 2, size=positions.size).astype(bool)
+    new_up = mag + steps
+    new_dn = mag - steps
+    go_up = np.where(up, new_up < nonfinite, new_dn < 0)
+    go_up &= new_up < nonfinite
+    new = np.where(go_up, new_up, new_dn)
+    codes[positions] = (sign | new).astype(npu)
+    out = torch.from_numpy(codes.view(np.int16 if npu == np.uint16 else np.int8).copy()).view(ref.dtype)
+    return out.reshape(ref.shape)
+
+
+def code_flip_pair(n: int, seed: int, dtype: torch.dtype = torch.bfloat16, std: float = 2.0,
+                   p1: float = 0.05, p3: float = 1e-4, clamp: float = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(cand, ref): ref = dtype(N(0,std)); cand moves disjoint positions by 1 code (fraction p1) or 3 codes (p3)."""
+    rng = _rng(seed)
+    x = rng.standard_normal(n, dtype=np.float32) * np.float32(std)
+    if clamp is not None:
+        np.clip(x, -clamp, clamp, out=x)
+    ref = torch.from_numpy(x).to(dtype)
+    k1 = int(round(n * p1))
+    k3 = int(round(n * p3))
+    pos = _distinct_positions(rng, n, k1 + k3)
+    perm = rng.permutation(pos.size)
+    steps = np.ones(pos.size, dtype=np.int64)
+    steps[perm[:k3]] = 3
+    cand = step_codes(ref, pos, steps, rng)
+    return cand, ref
+
+
+def fp16_nonfinite_pair(rows: int, cols: int, row_stride: int, seed: int, p_nan: float = 5e-4,
+                        p_inf: float = 5e-4, breaks: int = 17) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(cand, ref) fp16 views of shape (rows, cols) with strides (row_stride, 1).
+
+    ref ~ U(-60000, 60000) with seeded NaN and +-Inf; cand copies ref (pattern
+    included) except at ``breaks`` seeded positions whose finite/NaN/Inf class
+    is changed.  The padding columns hold values that must never be read.
+    """
+    rng = _rng(seed)
+    n = rows * cols
+    vals = rng.uniform(-60000.0, 60000.0, size=n).astype(np.float32)
+    k_nan = int(round(n * p_nan))
+    k_inf = int(round(n * p_inf))
+    pos = _distinct_positions(rng, n, k_nan + k_inf)
+    perm = rng.permutation(pos.size)
+    nan_pos = pos[perm[:k_nan]]
+    inf_pos = pos[perm[k_nan:]]
+    vals[nan_pos] = np.nan
+    vals[inf_pos] = np.where(rng.integers(0, 2, size=inf_pos.size) == 1, np.inf, -np.inf)
+    ref_logical = vals.astype(np.float16)
+    cand_logical = ref_logical.copy()
+    bpos = _distinct_positions(rng, n, breaks)
+    for j, p in enumerate(bpos):
+        v = ref_logical[p]
+        if np.isnan(v):
+            cand_logical[p] = np.float16(1.0) if j % 2 else np.float16(np.inf)
+        elif np.isinf(v):
+            cand_logical[p] = np.float16(np.nan) if j % 2 else -v
+        else:
+            cand_logical[p] = np.float16(np.nan) if j % 2 else np.float16(np.inf)
+    out = []
+    for logical, pad_val in ((cand_logical, 7.0), (ref_logical, -7.0)):
+        base = np.full((rows, row_stride), pad_val, dtype=np.float16)
+        base[:, :cols] = logical.reshape(rows, cols)
+        t = torch.from_numpy(base.reshape(-1).copy())
+        out.append(t.as_strided((rows, cols), (row_stride, 1)))
+    return out[0], out[1]
+
+
+def int8_pair(n: int, seed: int, changed: int = 1000) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(cand, ref) int8: ref ~ U[-128,127]; cand differs from ref at exactly ``changed`` positions."""
+    rng = _rng(seed)
+    ref = rng.integers(-128, 128, size=n, dtype=np.int16).astype(np.int8)
+    cand = ref.copy()
+    pos = _distinct_positions(rng, n, changed)
+    delta = rng.integers(1, 256, size=pos.size)
+    cand[pos] = ((ref[pos].astype(np.int16) + 128 + delta) % 256 - 128).astype(np.int8)
+    return torch.from_numpy(cand), torch.from_numpy(ref)
+
+
+def fp8_pair(n: int, seed: int, p: float = 0.02, std: float = 4.0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(cand, ref) float8_e4m3fn: ref = e4m3(clamp(N(0,std), +-448)); cand moves a fraction p by one code."""
+    return code_flip_pair(n, seed, dtype=torch.float8_e4m3fn, std=std, p1=p, p3=0.0, clamp=448.0)
+
+
+def ragged_sizes(count: int, seed: int, lo: int = 1024, hi: int = 1 << 20) -> List[int]:
+    """Log-uniform integer sizes in [lo, hi]."""
+    rng = _rng(seed)
+    u = rng.uniform(math.log(lo), math.log(hi), size=count)
+    return [int(min(hi, max(lo, round(math.exp(v))))) for v in u]
+
+
+RAGGED_TOLERANCES = ({"rtol": 1e-5, "atol": 1e-5}, {"rtol": 1.6e-2, "atol": 1e-2},
+                     {"rtol": 1e-3, "atol": 1e-4}, {"rtol": 5e-4, "atol": 5e-4})
+
+
+def ragged_batch(count: int, seed: int, lo: int = 1024, hi: int = 1 << 20):
+    """List of (cand, ref, tolerance) with dtype alternating fp32 / bf16 and the fp32 noise model."""
+    sizes = ragged_sizes(count, seed, lo, hi)
+    out = []
+    for i, n in enumerate(sizes):
+        cand, ref = fp32_noise_pair(n, seed * 100003 + i)
+        if i % 2:
+            cand, ref = cand.to(torch.bfloat16), ref.to(torch.bfloat16)
+        out.append((cand, ref, dict(RAGGED_TOLERANCES[i % len(RAGGED_TOLERANCES)])))
+    return out
+
+
+# ------------------------------------------------------------ device variants
+def code_flip_pair_device(n: int, seed: int, device, dtype=torch.bfloat16, std: float = 2.0,
+                          p1: float = 0.05, p3: float = 1e-4, clamp: float = None):
+    """Device-side analogue of ``code_flip_pair`` (same statistics, different bytes)."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    x = torch.randn(n, generator=gen, device=device, dtype=torch.float32) * std
+    if clamp is not None:
+        x.clamp_(-clamp, clamp)
+    ref = x.to(dtype)
+    del x
+    view, _, mag_mask, nonfinite = _CODE_INFO[dtype]
+    u = torch.rand(n, generator=gen, device=device)
+    steps = torch.where(u < p3, 3, torch.where(u < p3 + p1, 1, 0)).to(torch.int32)
+    del u
+    codes = ref.view(view).to(torch.int32) & ((mag_mask << 1) | 1)
+    sign = codes & ~mag_mask
+    mag = codes & mag_mask
+    up = mag + steps
+    new = torch.where(up < nonfinite, up, mag - steps)
+    cand_codes = (sign | new)
+    cand_codes = torch.where(cand_codes > mag_mask, cand_codes - (2 * (mag_mask + 1)), cand_codes)
+    cand = cand_codes.to(view).view(dtype)
+    return cand, ref
