@@ -93,6 +93,10 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
   d.max_abs_diff = (int32_t)p->max_abs_diff;
   d.nz_abs = (float)p->near_zero_abs;
   d.nz_bad = (float)p->near_zero_bad_abs;
+  // A bit-identical finite pair is a non-mismatch with abs_diff 0 -- unless the integer
+  // threshold is negative (0 > t) or a negative near-zero "bad" threshold counts 0 as bad.
+  d.fast = !(p->mode == KVV_MODE_MAX_ABS_DIFF && p->max_abs_diff < 0) &&
+           !((p->flags & KVV_FLAG_NEAR_ZERO) && d.nz_bad < 0.0f);
   d.dtype = r->dtype;
   d.item_elems = item_elems_for(r->dtype);
 
@@ -210,7 +214,12 @@ T* at(void* ws, size_t off) {
   return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
 }
 
-int64_t blocks_target() { return (int64_t)device_cus() * 4; }
+// Persistent-style grid: a few blocks per CU, each streaming a contiguous range of
+// items.  Capped so that a segment never has more runs than reduce_kernel lists.
+int64_t blocks_target() {
+  const int64_t b = (int64_t)device_cus() * 4;
+  return b < 2048 ? b : 2048;
+}
 
 // ------------------------------------------------------------ one verdict
 int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st,
@@ -307,7 +316,7 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   fa.hist = at<uint32_t>(ws, L.hist);
   fa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
   fa.item_near_sum = near ? at<double>(ws, L.item_near_sum) : nullptr;
-  hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(64), 0, st, fa);
+  hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kBlock), 0, st, fa);
   KVV_HIP(hipGetLastError());
   return KVV_OK;
 }
@@ -454,7 +463,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   fa.hist = at<uint32_t>(ws, L.hist);
   fa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
   fa.item_near_sum = bp.near ? at<double>(ws, L.item_near_sum) : nullptr;
-  hipLaunchKernelGGL(finalize_kernel, dim3(nseg), dim3(64), 0, st, fa);
+  hipLaunchKernelGGL(finalize_kernel, dim3(nseg), dim3(kBlock), 0, st, fa);
   KVV_HIP(hipGetLastError());
   return KVV_OK;
 }

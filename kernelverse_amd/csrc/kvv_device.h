@@ -70,6 +70,7 @@ template <> struct Elem<KVV_F32> : FloatElemBase {
   __device__ static int32_t i32(T c) { return x86_trunc_i32((double)__uint_as_float(c)); }
   __device__ static bool isnan(T c) { return (c & 0x7FFFFFFFu) > 0x7F800000u; }
   __device__ static bool isinf(T c) { return (c & 0x7FFFFFFFu) == 0x7F800000u; }
+  __device__ static bool finite(T c) { return (c & 0x7F800000u) != 0x7F800000u; }
   __device__ static bool sign(T c) { return c >> 31; }
   __device__ static uint64_t mag(T c) { return c & 0x7FFFFFFFu; }
 };
@@ -82,6 +83,7 @@ template <> struct Elem<KVV_BF16> : FloatElemBase {
   __device__ static int32_t i32(T c) { return x86_trunc_i32((double)f32(c)); }
   __device__ static bool isnan(T c) { return (c & 0x7FFFu) > 0x7F80u; }
   __device__ static bool isinf(T c) { return (c & 0x7FFFu) == 0x7F80u; }
+  __device__ static bool finite(T c) { return (c & 0x7F80u) != 0x7F80u; }
   __device__ static bool sign(T c) { return c >> 15; }
   __device__ static uint64_t mag(T c) { return c & 0x7FFFu; }
 };
@@ -94,6 +96,7 @@ template <> struct Elem<KVV_F16> : FloatElemBase {
   __device__ static int32_t i32(T c) { return x86_trunc_i32((double)f32(c)); }
   __device__ static bool isnan(T c) { return (c & 0x7FFFu) > 0x7C00u; }
   __device__ static bool isinf(T c) { return (c & 0x7FFFu) == 0x7C00u; }
+  __device__ static bool finite(T c) { return (c & 0x7C00u) != 0x7C00u; }
   __device__ static bool sign(T c) { return c >> 15; }
   __device__ static uint64_t mag(T c) { return c & 0x7FFFu; }
 };
@@ -106,6 +109,7 @@ template <> struct Elem<KVV_F64> : FloatElemBase {
   __device__ static int32_t i32(T c) { return x86_trunc_i32(f64(c)); }
   __device__ static bool isnan(T c) { return (c & 0x7FFFFFFFFFFFFFFFull) > 0x7FF0000000000000ull; }
   __device__ static bool isinf(T c) { return (c & 0x7FFFFFFFFFFFFFFFull) == 0x7FF0000000000000ull; }
+  __device__ static bool finite(T c) { return (c & 0x7FF0000000000000ull) != 0x7FF0000000000000ull; }
   __device__ static bool sign(T c) { return c >> 63; }
   __device__ static uint64_t mag(T c) { return c & 0x7FFFFFFFFFFFFFFFull; }
 };
@@ -128,6 +132,7 @@ template <> struct Elem<KVV_F8E4M3FN> : FloatElemBase {
   __device__ static int32_t i32(T c) { return x86_trunc_i32((double)f32(c)); }
   __device__ static bool isnan(T c) { return (c & 0x7Fu) == 0x7Fu; }
   __device__ static bool isinf(T) { return false; }
+  __device__ static bool finite(T c) { return (c & 0x7Fu) != 0x7Fu; }
   __device__ static bool sign(T c) { return c >> 7; }
   __device__ static uint64_t mag(T c) { return c & 0x7Fu; }
 };
@@ -141,6 +146,7 @@ template <> struct Elem<KVV_F8E5M2> : FloatElemBase {
   __device__ static int32_t i32(T c) { return x86_trunc_i32((double)f32(c)); }
   __device__ static bool isnan(T c) { return (c & 0x7Fu) > 0x7Cu; }
   __device__ static bool isinf(T c) { return (c & 0x7Fu) == 0x7Cu; }
+  __device__ static bool finite(T c) { return (c & 0x7Cu) != 0x7Cu; }
   __device__ static bool sign(T c) { return c >> 7; }
   __device__ static uint64_t mag(T c) { return c & 0x7Fu; }
 };
@@ -155,6 +161,7 @@ struct IntElem : IntElemBase {
   __device__ static int32_t i32(T c) { return (int32_t)(uint32_t)(uint64_t)v(c); }  // wraps like .to(int32)
   __device__ static bool isnan(T) { return false; }
   __device__ static bool isinf(T) { return false; }
+  __device__ static bool finite(T) { return true; }
 };
 template <> struct Elem<KVV_I8> : IntElem<uint8_t, int8_t> {};
 template <> struct Elem<KVV_U8> : IntElem<uint8_t, uint8_t> {};
@@ -170,6 +177,7 @@ template <> struct Elem<KVV_BOOL> : IntElemBase {
   __device__ static int32_t i32(T c) { return c != 0; }
   __device__ static bool isnan(T) { return false; }
   __device__ static bool isinf(T) { return false; }
+  __device__ static bool finite(T) { return true; }
 };
 
 // ULP / integer distance of a pair (never called for NaN pairs).

@@ -50,12 +50,12 @@ struct SegDesc {
   int32_t mode;           // enum kvv_mode
   uint32_t flags;
   int32_t zero_tol;       // rtol == atol == 0: isclose is plain equality
+  int32_t fast;           // bit-identical finite pairs may take the short path
   int32_t max_abs_diff;
   float rtol, atol, nz_abs, nz_bad;
   int32_t dtype;
   int32_t item_elems;
   int32_t out_index;      // position of this pair's kvv_result in the caller's array
-  int32_t pad;
   int64_t row_len;        // L_ROWS: contiguous inner length
   Dims dims;              // L_ROWS: outer dims; L_GENERIC: all dims
 };
@@ -89,15 +89,22 @@ struct Acc {
   uint32_t mism;
   uint32_t mm_abs, mm_rel;
   uint32_t gabs_k, grel_k;
+  uint32_t nfast;          // bit-identical finite pairs (ULP bucket 0, never a mismatch)
+  uint32_t nnear_fast;     // ... of which near zero
   uint64_t first_mm, first_viol;
   uint64_t gabs_i, grel_i;
-  double s[7];
+  uint64_t first_fast;     // lowest index of such a pair (an abs/rel argmax candidate of value 0)
+  double e_sq;             // sum of g*g over those pairs (there g == r, so it feeds gg, rr and gr)
+  double s[7];             // full path: gg rr gr dd | sampled gg rr gr
   __device__ void init() {
     mism = 0;
     mm_abs = mm_rel = 0;
     gabs_k = grel_k = 0;
+    nfast = nnear_fast = 0;
     first_mm = first_viol = kNone;
     gabs_i = grel_i = kNone;
+    first_fast = kNone;
+    e_sq = 0.0;
 #pragma unroll
     for (int i = 0; i < 7; ++i) s[i] = 0.0;
   }
@@ -283,22 +290,33 @@ __device__ __forceinline__ void sample_range(const SegDesc& d, int64_t L0, int64
 }
 
 // Vector path: 16-byte loads of both tensors, kUnroll vectors per thread.
+//
+// Phase A runs over every element and only tells bit-identical finite pairs
+// apart from the rest: such a pair is never a mismatch, has abs_diff = rel_diff
+// = 0, ULP distance 0, and contributes g*g to the three product sums.  Phase B
+// gives every other element the full treatment (process_elem), each lane
+// walking its own list of such elements re-read from an LDS stage, so the
+// wave pays for the longest list of any lane rather than for every element.
 template <int DT, int MODE>
-__device__ __forceinline__ void scan_item_vec(const SegDesc& d, int64_t L0, int64_t L1, Acc& acc, uint32_t* col) {
+__device__ __forceinline__ void scan_item_vec(const SegDesc& d, int64_t L0, int64_t L1, Acc& acc, uint32_t* col,
+                                              uint4* stage) {
   using E = Elem<DT>;
   using T = typename E::T;
   constexpr int V = 16 / sizeof(T);
+  constexpr int NE = V * kUnroll;
+  static_assert(NE <= 64, "per-lane element mask is 64 bits");
   union Vec {
     uint4 u;
     T e[V];
   };
+  const int tid = threadIdx.x;
   Vec gv[kUnroll], rv[kUnroll];
-  int64_t vs[kUnroll];
+  uint32_t full = 0;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t v = L0 + (int64_t)(u * kBlock + threadIdx.x) * V;
-    vs[u] = v;
+    const int64_t v = L0 + (int64_t)(u * kBlock + tid) * V;
     if (v + V <= L1) {
+      full |= 1u << u;
       int64_t og, orr;
       if (d.layout == L_CONTIG) {
         og = orr = v;
@@ -307,15 +325,60 @@ __device__ __forceinline__ void scan_item_vec(const SegDesc& d, int64_t L0, int6
       }
       gv[u].u = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(d.g) + og);
       rv[u].u = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(d.r) + orr);
+    } else {
+      gv[u].u = make_uint4(0, 0, 0, 0);
+      rv[u].u = make_uint4(0, 0, 0, 0);
     }
   }
+  const bool fast_ok = d.fast != 0;
+  const bool near_mode = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
+  uint64_t slow = 0, valid = 0;
+  double esq = 0.0;
+  uint32_t nnear = 0;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t v = vs[u];
-    if (v + V <= L1) {
+    if (!((full >> u) & 1u)) continue;
 #pragma unroll
-      for (int e = 0; e < V; ++e) process_elem<DT, MODE>(gv[u].e[e], rv[u].e[e], (uint64_t)(v + e), d, acc, col);
-    } else if (v < L1) {
+    for (int e = 0; e < V; ++e) {
+      const T gc = gv[u].e[e], rc = rv[u].e[e];
+      const bool fast = fast_ok && gc == rc && E::finite(gc);
+      const double g64 = fast ? E::f64(gc) : 0.0;
+      esq = fma(g64, g64, esq);
+      if (near_mode) nnear += (fast && fabsf(E::f32(gc)) <= d.nz_abs) ? 1u : 0u;
+      slow |= (uint64_t)(!fast) << (u * V + e);
+    }
+    valid |= ((1ull << V) - 1) << (u * V);
+  }
+  acc.e_sq += esq;
+  acc.nnear_fast += nnear;
+  const uint64_t fastm = valid & ~slow;
+  acc.nfast += (uint32_t)__popcll(fastm);
+  if (fastm && acc.first_fast == kNone) {
+    const int k = __builtin_ctzll(fastm);
+    acc.first_fast = (uint64_t)(L0 + ((int64_t)(k / V) * kBlock + tid) * V + (k % V));
+  }
+  slow &= valid;
+  if (slow) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      stage[(2 * u) * kBlock + tid] = gv[u].u;
+      stage[(2 * u + 1) * kBlock + tid] = rv[u].u;
+    }
+    while (slow) {
+      const int k = __builtin_ctzll(slow);
+      slow &= slow - 1;
+      const int u = k / V, e = k % V;
+      const T gc = reinterpret_cast<const T*>(&stage[(2 * u) * kBlock + tid])[e];
+      const T rc = reinterpret_cast<const T*>(&stage[(2 * u + 1) * kBlock + tid])[e];
+      const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + tid) * V + e);
+      process_elem<DT, MODE>(gc, rc, idx, d, acc, col);
+    }
+  }
+  // a partial last vector (numel not a multiple of the vector width)
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t v = L0 + (int64_t)(u * kBlock + tid) * V;
+    if (!((full >> u) & 1u) && v < L1) {
       for (int64_t idx = v; idx < L1; ++idx) {
         int64_t og, orr;
         elem_offsets(d, idx, og, orr);
@@ -360,20 +423,35 @@ __device__ void flush_run(Acc& acc, uint32_t* s_cnt, BlockScratch& bs, RunRec* o
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __syncthreads();
   for (int c = 0; c < LC_COUNT; ++c) {
-    uint64_t v = wave_sum((uint64_t)s_cnt[c * kBlock + tid]);
+    uint64_t own = s_cnt[c * kBlock + tid];
+    if (c == LC_HIST0) own += acc.nfast;
+    if (c == LC_NEAR) own += acc.nnear_fast;
+    uint64_t v = wave_sum(own);
     s_cnt[c * kBlock + tid] = 0;
     if (lane == 0) bs.u[w][c] = v;
   }
   uint64_t mism = wave_sum((uint64_t)acc.mism);
   uint64_t fmm = wave_min(acc.first_mm), fvi = wave_min(acc.first_viol);
   uint32_t mma = wave_max(acc.mm_abs), mmr = wave_max(acc.mm_rel);
+  // bit-identical pairs have abs_diff = rel_diff = +0, whose key is 0x80000000 in both modes
   uint32_t gak = acc.gabs_k, grk = acc.grel_k;
   uint64_t gai = acc.gabs_i, gri = acc.grel_i;
+  if (better(0x80000000u, acc.first_fast, gak, gai)) {
+    gak = 0x80000000u;
+    gai = acc.first_fast;
+  }
+  if (better(0x80000000u, acc.first_fast, grk, gri)) {
+    grk = 0x80000000u;
+    gri = acc.first_fast;
+  }
   wave_argmax(gak, gai);
   wave_argmax(grk, gri);
   double s[7];
+  s[0] = wave_sum(acc.e_sq + acc.s[0]);
+  s[1] = wave_sum(acc.e_sq + acc.s[1]);
+  s[2] = wave_sum(acc.e_sq + acc.s[2]);
 #pragma unroll
-  for (int i = 0; i < 7; ++i) s[i] = wave_sum(acc.s[i]);
+  for (int i = 3; i < 7; ++i) s[i] = wave_sum(acc.s[i]);
   if (lane == 0) {
     bs.u[w][LC_COUNT + 0] = mism;
     bs.u[w][LC_COUNT + 1] = fmm;
@@ -426,20 +504,20 @@ __device__ void flush_run(Acc& acc, uint32_t* s_cnt, BlockScratch& bs, RunRec* o
 // ------------------------------------------------------------ scan kernel
 template <int DT, int MODE>
 __device__ __forceinline__ void scan_item(const SegDesc& d, int64_t item, const ScanArgs& a, Acc& acc,
-                                          uint32_t* s_cnt, uint32_t* red) {
+                                          uint32_t* s_cnt, uint32_t* red, uint4* stage) {
   const int64_t L0 = (item - d.item_begin) * (int64_t)d.item_elems;
   const int64_t L1 = L0 + d.item_elems < d.n ? L0 + d.item_elems : d.n;
   uint32_t* col = s_cnt + threadIdx.x;
   const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
   uint32_t near_before = 0;
-  if (near) near_before = col[LC_NEAR * kBlock];
+  if (near) near_before = col[LC_NEAR * kBlock] + acc.nnear_fast;
   if (d.vec)
-    scan_item_vec<DT, MODE>(d, L0, L1, acc, col);
+    scan_item_vec<DT, MODE>(d, L0, L1, acc, col, stage);
   else
     scan_item_scalar<DT, MODE>(d, L0, L1, acc, col);
   sample_range<DT, MODE>(d, L0, L1, acc, a.sample_abs, a.sample_rel);
   if (near) {
-    const uint32_t t = block_sum_u32(col[LC_NEAR * kBlock] - near_before, red);
+    const uint32_t t = block_sum_u32(col[LC_NEAR * kBlock] + acc.nnear_fast - near_before, red);
     if (threadIdx.x == 0) a.item_near[item] = t;
   }
 }
@@ -447,6 +525,7 @@ __device__ __forceinline__ void scan_item(const SegDesc& d, int64_t item, const 
 template <int DT, int MODE>
 __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   __shared__ uint32_t s_cnt[LC_COUNT * kBlock];
+  __shared__ uint4 stage[2 * kUnroll * kBlock];
   __shared__ BlockScratch bs;
   __shared__ uint32_t red[kWaves];
   const int tid = threadIdx.x;
@@ -461,7 +540,7 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
     const SegDesc& d = a.seg0;
     for (int64_t it = i0; it < i1; ++it) {
       if (tid == 0) a.run_valid[it] = (it == i0) ? 1u : 0u;
-      scan_item<DT, MODE>(d, it, a, acc, s_cnt, red);
+      scan_item<DT, MODE>(d, it, a, acc, s_cnt, red, stage);
     }
     flush_run(acc, s_cnt, bs, &a.runs[i0]);
     return;
@@ -481,7 +560,7 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
       run_start = it;
     }
     if (tid == 0) a.run_valid[it] = (it == run_start) ? 1u : 0u;
-    scan_item<DT, MODE>(a.table[s], it, a, acc, s_cnt, red);
+    scan_item<DT, MODE>(a.table[s], it, a, acc, s_cnt, red, stage);
   }
   flush_run(acc, s_cnt, bs, &a.runs[run_start]);
 }
@@ -499,31 +578,58 @@ struct ReduceArgs {
   uint64_t* item_near_off;
 };
 
-__device__ __forceinline__ void rec_init(RunRec& r) {
-  for (int c = 0; c < LC_COUNT; ++c) r.cnt[c] = 0;
-  r.mismatch = 0;
-  r.first_mm = r.first_viol = kNone;
-  r.gabs_i = r.grel_i = kNone;
-  r.mm_abs = r.mm_rel = r.gabs_k = r.grel_k = 0;
-  for (int i = 0; i < 7; ++i) r.s[i] = 0.0;
+
+
+constexpr int kReduceBlock = 1024;
+constexpr int kMaxRuns = 4096;   // runs per segment: at most one per scan block (host caps the grid)
+constexpr int kFields = LC_COUNT + 14;
+
+// Field f of a run record folded into a wave-level partial: counts add,
+// first indices take the minimum, keys the maximum, (key, index) pairs the
+// argmax, fp64 sums add.  Every lane visits its runs in item order and the
+// butterfly order is fixed, so the result does not depend on timing.
+struct FieldAcc {
+  uint64_t u;
+  uint32_t k;
+  double x;
+};
+
+__device__ __forceinline__ void field_init(int f, FieldAcc& a) {
+  a.k = 0;
+  a.x = 0.0;
+  a.u = (f == LC_COUNT + 1 || f == LC_COUNT + 2 || f == LC_COUNT + 5 || f == LC_COUNT + 6) ? kNone : 0;
 }
 
-__device__ __forceinline__ void rec_merge(RunRec& a, const RunRec& b) {
-  for (int c = 0; c < LC_COUNT; ++c) a.cnt[c] += b.cnt[c];
-  a.mismatch += b.mismatch;
-  a.first_mm = b.first_mm < a.first_mm ? b.first_mm : a.first_mm;
-  a.first_viol = b.first_viol < a.first_viol ? b.first_viol : a.first_viol;
-  a.mm_abs = b.mm_abs > a.mm_abs ? b.mm_abs : a.mm_abs;
-  a.mm_rel = b.mm_rel > a.mm_rel ? b.mm_rel : a.mm_rel;
-  if (better(b.gabs_k, b.gabs_i, a.gabs_k, a.gabs_i)) {
-    a.gabs_k = b.gabs_k;
-    a.gabs_i = b.gabs_i;
+__device__ __forceinline__ void field_add(int f, FieldAcc& a, const RunRec& r) {
+  if (f < LC_COUNT) {
+    a.u += r.cnt[f];
+  } else {
+    switch (f - LC_COUNT) {
+      case 0: a.u += r.mismatch; break;
+      case 1: a.u = r.first_mm < a.u ? r.first_mm : a.u; break;
+      case 2: a.u = r.first_viol < a.u ? r.first_viol : a.u; break;
+      case 3: a.k = r.mm_abs > a.k ? r.mm_abs : a.k; break;
+      case 4: a.k = r.mm_rel > a.k ? r.mm_rel : a.k; break;
+      case 5: if (better(r.gabs_k, r.gabs_i, a.k, a.u)) { a.k = r.gabs_k; a.u = r.gabs_i; } break;
+      case 6: if (better(r.grel_k, r.grel_i, a.k, a.u)) { a.k = r.grel_k; a.u = r.grel_i; } break;
+      default: a.x += r.s[f - LC_COUNT - 7]; break;
+    }
   }
-  if (better(b.grel_k, b.grel_i, a.grel_k, a.grel_i)) {
-    a.grel_k = b.grel_k;
-    a.grel_i = b.grel_i;
+}
+
+__device__ __forceinline__ void field_wave_reduce(int f, FieldAcc& a) {
+  const int g = f - LC_COUNT;
+  if (f < LC_COUNT || g == 0) {
+    a.u = wave_sum(a.u);
+  } else if (g == 1 || g == 2) {
+    a.u = wave_min(a.u);
+  } else if (g == 3 || g == 4) {
+    a.k = wave_max(a.k);
+  } else if (g == 5 || g == 6) {
+    wave_argmax(a.k, a.u);
+  } else {
+    a.x = wave_sum(a.x);
   }
-  for (int i = 0; i < 7; ++i) a.s[i] += b.s[i];
 }
 
 __device__ __forceinline__ double clamp_cos(double c) {
@@ -539,74 +645,80 @@ __device__ __forceinline__ double cosine_of(double gr, double gg, double rr) {
   return clamp_cos(gr / (gn * rn));
 }
 
-constexpr int kReduceBlock = 1024;
-
-__device__ __forceinline__ RunRec rec_shfl_xor(const RunRec& a, int o) {
-  RunRec b;
-  for (int c = 0; c < LC_COUNT; ++c) b.cnt[c] = __shfl_xor(a.cnt[c], o);
-  b.mismatch = __shfl_xor(a.mismatch, o);
-  b.first_mm = __shfl_xor(a.first_mm, o);
-  b.first_viol = __shfl_xor(a.first_viol, o);
-  b.gabs_i = __shfl_xor(a.gabs_i, o);
-  b.grel_i = __shfl_xor(a.grel_i, o);
-  b.mm_abs = __shfl_xor(a.mm_abs, o);
-  b.mm_rel = __shfl_xor(a.mm_rel, o);
-  b.gabs_k = __shfl_xor(a.gabs_k, o);
-  b.grel_k = __shfl_xor(a.grel_k, o);
-  for (int i = 0; i < 7; ++i) b.s[i] = __shfl_xor(a.s[i], o);
-  return b;
-}
-
-// One block per segment: merges the segment's run records in a fixed order
-// (each thread a strided subset in item order, then a butterfly across the
-// wave, then the waves in order), so fp64 sums are bit-reproducible.
+// One block per segment: lists the segment's runs in item order, then folds
+// the run records field by field (one wave per field group).
 __global__ __launch_bounds__(kReduceBlock) void reduce_kernel(ReduceArgs a) {
   constexpr int kW = kReduceBlock / 64;
-  __shared__ RunRec part[kW];
+  __shared__ uint32_t runs[kMaxRuns];
   __shared__ uint64_t wsum[kW];
+  __shared__ FieldAcc fres[kFields];
+  __shared__ uint32_t s_nruns;
   const int seg = blockIdx.x;
   const SegDesc& d = a.table ? a.table[seg] : a.seg0;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (int i = tid; i < kHistPerSeg; i += kReduceBlock) a.hist[(size_t)seg * kHistPerSeg + i] = 0;
   if (tid < kArrays) a.nan_cnt[seg * kArrays + tid] = 0;
-  RunRec acc;
-  rec_init(acc);
-  for (int64_t k = tid; k < d.item_count; k += kReduceBlock) {
-    const int64_t it = d.item_begin + k;
-    if (a.run_valid[it]) rec_merge(acc, a.runs[it]);
+  // 1. run list (and, in near-zero mode, the exclusive prefix of per-item near counts)
+  const int64_t per = (d.item_count + kReduceBlock - 1) / kReduceBlock;
+  const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
+  const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
+  const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
+  uint64_t nvalid = 0, nnear = 0;
+  for (int64_t k = k0; k < k1; ++k) {
+    nvalid += a.run_valid[d.item_begin + k] ? 1 : 0;
+    if (near) nnear += a.item_near[d.item_begin + k];
   }
-  for (int o = 1; o < 64; o <<= 1) {
-    RunRec other = rec_shfl_xor(acc, o);
-    rec_merge(acc, other);
-  }
-  if (lane == 0) part[w] = acc;
-  // near-zero: exclusive prefix of the per-item counts, in item order
-  if (d.flags & KVV_FLAG_NEAR_ZERO) {
-    const int64_t per = (d.item_count + kReduceBlock - 1) / kReduceBlock;
-    const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
-    const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
-    uint64_t mine = 0;
-    for (int64_t k = k0; k < k1; ++k) mine += a.item_near[d.item_begin + k];
-    // inclusive scan across the wave, then across waves
+  uint64_t base_runs = 0, base_near = 0;
+  for (int pass = 0; pass < (near ? 2 : 1); ++pass) {
+    const uint64_t mine = pass == 0 ? nvalid : nnear;
     uint64_t incl = mine;
     for (int o = 1; o < 64; o <<= 1) {
       const uint64_t v = __shfl_up(incl, o);
       if (lane >= o) incl += v;
     }
+    __syncthreads();
     if (lane == 63) wsum[w] = incl;
     __syncthreads();
     uint64_t base = 0;
     for (int i = 0; i < w; ++i) base += wsum[i];
-    uint64_t run = base + incl - mine;
+    (pass == 0 ? base_runs : base_near) = base + incl - mine;
+  }
+  {
+    uint64_t at = base_runs, nr = base_near;
     for (int64_t k = k0; k < k1; ++k) {
-      a.item_near_off[d.item_begin + k] = run;
-      run += a.item_near[d.item_begin + k];
+      const int64_t it = d.item_begin + k;
+      if (a.run_valid[it] && at < kMaxRuns) runs[at++] = (uint32_t)k;
+      if (near) {
+        a.item_near_off[it] = nr;
+        nr += a.item_near[it];
+      }
     }
+  }
+  if (tid == kReduceBlock - 1) s_nruns = (uint32_t)(base_runs + nvalid);
+  __syncthreads();
+  const uint32_t nruns = s_nruns < kMaxRuns ? s_nruns : kMaxRuns;
+  // 2. field-parallel fold
+  for (int f = w; f < kFields; f += kW) {
+    FieldAcc fa;
+    field_init(f, fa);
+    for (uint32_t r = lane; r < nruns; r += 64) field_add(f, fa, a.runs[d.item_begin + runs[r]]);
+    field_wave_reduce(f, fa);
+    if (lane == 0) fres[f] = fa;
   }
   __syncthreads();
   if (tid != 0) return;
-  for (int i = 1; i < kW; ++i) rec_merge(part[0], part[i]);
-  const RunRec& r = part[0];
+  RunRec r;
+  for (int c = 0; c < LC_COUNT; ++c) r.cnt[c] = fres[c].u;
+  r.mismatch = fres[LC_COUNT + 0].u;
+  r.first_mm = fres[LC_COUNT + 1].u;
+  r.first_viol = fres[LC_COUNT + 2].u;
+  r.mm_abs = fres[LC_COUNT + 3].k;
+  r.mm_rel = fres[LC_COUNT + 4].k;
+  r.gabs_k = fres[LC_COUNT + 5].k;
+  r.gabs_i = fres[LC_COUNT + 5].u;
+  r.grel_k = fres[LC_COUNT + 6].k;
+  r.grel_i = fres[LC_COUNT + 6].u;
+  for (int i = 0; i < 7; ++i) r.s[i] = fres[LC_COUNT + 7 + i].x;
   kvv_result o;
   __builtin_memset(&o, 0, sizeof(o));
   o.numel = d.n;
@@ -802,27 +914,54 @@ __device__ __forceinline__ void q99_ranks(int64_t m, uint64_t& lo, uint64_t& hi,
   w = rank - (float)lo;
 }
 
-// Prefix (high bits fixed so far) and residual rank of target `rr` after `passes` digits.
-__device__ __forceinline__ void select_state(const uint32_t* h, int passes, int rr, uint64_t rank, uint32_t& prefix,
-                                             uint64_t& resid) {
+// Block-cooperative search (kBlock == 256 threads, one per bin): the bin of a
+// 256-bin histogram that holds 0-based rank `resid`, and how many values lie in
+// lower bins.  A rank past the end (only when NaNs were left out) gives bin 255.
+__device__ void block_find_bin(const uint32_t* h, uint64_t resid, uint32_t& bin, uint64_t& below, uint64_t* sh) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint64_t c = h[tid];
+  uint64_t incl = c;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t v = __shfl_up(incl, o);
+    if (lane >= o) incl += v;
+  }
+  __syncthreads();
+  if (lane == 63) sh[w] = incl;
+  if (tid == 0) {
+    sh[kWaves] = 255;
+    sh[kWaves + 1] = 0;
+  }
+  __syncthreads();
+  uint64_t base = 0;
+  for (int i = 0; i < w; ++i) base += sh[i];
+  incl += base;
+  const uint64_t excl = incl - c;
+  if (c > 0 && excl <= resid && resid < incl) {
+    sh[kWaves] = (uint64_t)tid;
+    sh[kWaves + 1] = excl;
+  }
+  __syncthreads();
+  bin = (uint32_t)sh[kWaves];
+  below = sh[kWaves + 1];
+}
+
+// High bits fixed so far (`passes` digits) and the residual rank of target rr.
+__device__ void block_select_state(const uint32_t* h, int passes, int rr, uint64_t rank, uint32_t& prefix,
+                                   uint64_t& resid, uint64_t* sh) {
   prefix = 0;
   resid = rank;
   for (int p = 0; p < passes; ++p) {
-    const uint32_t* hp = h + (p * 2 + rr) * 256;
-    uint64_t cum = 0;
-    int b = 0;
-    for (; b < 255; ++b) {
-      if (cum + hp[b] > resid) break;
-      cum += hp[b];
-    }
-    prefix = (prefix << 8) | (uint32_t)b;
-    resid -= cum;
+    uint32_t bin;
+    uint64_t below;
+    block_find_bin(h + (p * 2 + rr) * 256, resid, bin, below, sh);
+    prefix = (prefix << 8) | bin;
+    resid -= below;
   }
 }
 
 __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   __shared__ uint32_t lh[2][256];
-  __shared__ uint32_t st_prefix[2];
+  __shared__ uint64_t sh[kWaves + 2];
   __shared__ uint32_t s_nan;
   const int tid = threadIdx.x;
   const int64_t gb = blockIdx.x;
@@ -836,18 +975,17 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   const int64_t c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
   uint32_t* h = a.hist + (size_t)s * kHistPerSeg + (size_t)arr * (kSelPasses * 2 * 256);
   const int pass = a.pass;
-  if (tid < 2) {
+  uint32_t p0 = 0, p1 = 0;
+  {
     uint64_t lo, hi, r;
     float w;
     q99_ranks(count, lo, hi, w);
-    uint32_t prefix;
-    select_state(h, pass, tid, tid == 0 ? lo : hi, prefix, r);
-    st_prefix[tid] = prefix;
+    block_select_state(h, pass, 0, lo, p0, r, sh);
+    block_select_state(h, pass, 1, hi, p1, r, sh);
   }
   for (int i = tid; i < 512; i += kBlock) (&lh[0][0])[i] = 0;
   if (tid == 0) s_nan = 0;
   __syncthreads();
-  const uint32_t p0 = st_prefix[0], p1 = st_prefix[1];
   const int shift = 24 - 8 * pass;
   const float* v = a.arr[arr] + d.sample_off;
   uint32_t nans = 0;
@@ -887,36 +1025,52 @@ struct FinalArgs {
   const double* item_near_sum;
 };
 
-__global__ void finalize_kernel(FinalArgs a) {
+// One block per segment: the exact order statistics of each sample array and
+// torch.quantile's interpolation, plus the near-zero sample mean.
+__global__ __launch_bounds__(kBlock) void finalize_kernel(FinalArgs a) {
+  __shared__ uint64_t sh[kWaves + 2];
+  __shared__ double part[kBlock];
   const int s = blockIdx.x;
   const SegDesc& d = a.table ? a.table[s] : a.seg0;
-  const int arr = threadIdx.x;
-  if (arr >= a.narrays) return;
+  const int tid = threadIdx.x;
   kvv_result& r = a.res[d.out_index];
-  const int64_t count = group_count(d, r, arr);
-  double out = __builtin_nan("");
-  if (count > 0 && a.nan_cnt[s * kArrays + arr] == 0) {
-    const uint32_t* h = a.hist + (size_t)s * kHistPerSeg + (size_t)arr * (kSelPasses * 2 * 256);
-    uint64_t lo, hi, resid;
-    float w;
-    q99_ranks(count, lo, hi, w);
-    uint32_t klo, khi;
-    select_state(h, kSelPasses, 0, lo, klo, resid);
-    select_state(h, kSelPasses, 1, hi, khi, resid);
-    const float va = fkey_value(klo), vb = fkey_value(khi);
-    // torch's lerp: small weights from the lower end, large ones from the upper end, fused multiply-add
-    const float diff = vb - va;
-    const float q = fabsf(w) < 0.5f ? fmaf(w, diff, va) : fmaf(w - 1.0f, diff, vb);
-    out = (double)q;
-  }
-  if (arr == 0) r.p99_abs = out;
-  if (arr == 1) r.p99_rel = out;
-  if (arr == 2) {
-    r.near_zero_p99_abs = out;
-    if (count > 0) {
-      double sum = 0.0;
-      for (int64_t k = 0; k < d.item_count; ++k) sum += a.item_near_sum[d.item_begin + k];
-      r.near_zero_mean_abs = (double)(float)(sum / (double)count);
+  for (int arr = 0; arr < a.narrays; ++arr) {
+    const int64_t count = group_count(d, r, arr);
+    double out = __builtin_nan("");
+    if (count > 0 && a.nan_cnt[s * kArrays + arr] == 0) {
+      const uint32_t* h = a.hist + (size_t)s * kHistPerSeg + (size_t)arr * (kSelPasses * 2 * 256);
+      uint64_t lo, hi, resid;
+      float w;
+      q99_ranks(count, lo, hi, w);
+      uint32_t klo, khi;
+      block_select_state(h, kSelPasses, 0, lo, klo, resid, sh);
+      block_select_state(h, kSelPasses, 1, hi, khi, resid, sh);
+      const float va = fkey_value(klo), vb = fkey_value(khi);
+      // torch's lerp: small weights from the lower end, large ones from the upper end, one rounding each
+      const float diff = vb - va;
+      const float q = fabsf(w) < 0.5f ? fmaf(w, diff, va) : fmaf(w - 1.0f, diff, vb);
+      out = (double)q;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      if (arr == 0) r.p99_abs = out;
+      if (arr == 1) r.p99_rel = out;
+      if (arr == 2) r.near_zero_p99_abs = out;
+    }
+    if (arr == 2 && count > 0) {
+      // fixed-order sum of the per-item sampled sums: contiguous chunks, then chunks in order
+      const int64_t per = (d.item_count + kBlock - 1) / kBlock;
+      const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
+      const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
+      double t = 0.0;
+      for (int64_t k = k0; k < k1; ++k) t += a.item_near_sum[d.item_begin + k];
+      part[tid] = t;
+      __syncthreads();
+      if (tid == 0) {
+        double sum = 0.0;
+        for (int i = 0; i < kBlock; ++i) sum += part[i];
+        r.near_zero_mean_abs = (double)(float)(sum / (double)count);
+      }
     }
   }
 }
