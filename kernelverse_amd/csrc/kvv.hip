@@ -10,7 +10,9 @@
 #include <vector>
 
 #include "kvv.h"
+#define KVV_COMMON_KERNELS 1  // reduce/select/finalize live in this unit only
 #include "kvv_kernels.h"
+#include "kvv_launch.h"
 
 namespace kvv {
 namespace {
@@ -22,9 +24,9 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
-#define KVV_HIP(call)                                                                   \
-  do {                                                                                  \
-    hipError_t e_ = (call);                                                             \
+#define KVV_HIP(call)                                                                                \
+  do {                                                                                               \
+    hipError_t e_ = (call);                                                                          \
     if (e_ != hipSuccess) return fail(KVV_E_HIP, std::string(#call) + ": " + hipGetErrorString(e_)); \
   } while (0)
 
@@ -41,6 +43,10 @@ int elem_size(int dt) {
   }
 }
 
+bool is_float_dtype(int dt) {
+  return dt == KVV_F32 || dt == KVV_F16 || dt == KVV_BF16 || dt == KVV_F64 || dt == KVV_F8E4M3FN || dt == KVV_F8E5M2;
+}
+
 int item_elems_for(int dt) { return kBlock * (16 / elem_size(dt)) * kUnroll; }
 
 int device_cus() {
@@ -54,6 +60,40 @@ int device_cus() {
     cached_cus = cus;
   }
   return cached_cus;
+}
+
+// Persistent-style grid: a few blocks per CU, each streaming a contiguous range of items.
+int64_t blocks_target() {
+  const int64_t b = (int64_t)device_cus() * 4;
+  return b < 4096 ? b : 4096;
+}
+
+// Which scan kernel a segment takes: the vector kinds need the dtype's natural
+// test and 16-byte aligned contiguous rows; everything else is scalar.
+int scan_kind(const SegDesc& d) {
+  const int native = is_float_dtype(d.dtype) ? KVV_MODE_ISCLOSE : KVV_MODE_MAX_ABS_DIFF;
+  if (d.mode != native || !d.vec) return K_SCALAR;
+  return d.layout == L_CONTIG ? K_CONTIG : K_ROWS;
+}
+
+ScanFn scan_fn(int dt, int mode, int kind, bool batch) {
+  switch (dt) {
+#define KVV_CASE(X) case X: return KVV_SCAN_FN(X)(mode, kind, batch);
+    KVV_CASE(0) KVV_CASE(1) KVV_CASE(2) KVV_CASE(3) KVV_CASE(4) KVV_CASE(5)
+    KVV_CASE(6) KVV_CASE(7) KVV_CASE(8) KVV_CASE(9) KVV_CASE(10) KVV_CASE(11)
+#undef KVV_CASE
+    default: return nullptr;
+  }
+}
+
+NearFn near_fn(int dt, int mode) {
+  switch (dt) {
+#define KVV_CASE(X) case X: return KVV_NEAR_FN(X)(mode);
+    KVV_CASE(0) KVV_CASE(1) KVV_CASE(2) KVV_CASE(3) KVV_CASE(4) KVV_CASE(5)
+    KVV_CASE(6) KVV_CASE(7) KVV_CASE(8) KVV_CASE(9) KVV_CASE(10) KVV_CASE(11)
+#undef KVV_CASE
+    default: return nullptr;
+  }
 }
 
 // Coalesces the joint (size, gen stride, ref stride) dims and picks the layout.
@@ -117,7 +157,8 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
     }
   }
   const int V = 16 / es;
-  const bool aligned = (reinterpret_cast<uintptr_t>(g->data) % 16 == 0) && (reinterpret_cast<uintptr_t>(r->data) % 16 == 0);
+  const bool aligned =
+      (reinterpret_cast<uintptr_t>(g->data) % 16 == 0) && (reinterpret_cast<uintptr_t>(r->data) % 16 == 0);
   if (n == 0 || nd == 0 || (nd == 1 && gs[0] == 1 && rs[0] == 1)) {
     d.layout = L_CONTIG;
     d.vec = aligned;
@@ -145,38 +186,19 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
   }
   d.item_count = (n + d.item_elems - 1) / d.item_elems;
   d.chunk_count = (d.m + kSelChunk - 1) / kSelChunk;
+  if (n > p->max_samples) {
+    const uint64_t num = (uint64_t)n - 1, den = (uint64_t)d.m - 1;
+    d.s_div = num / den;
+    d.s_mod = num % den;
+    d.s_inv = 1.0 / (double)den;
+  }
   return KVV_OK;
-}
-
-// ------------------------------------------------------------ kernel tables
-using ScanFn = void (*)(ScanArgs);
-using NearFn = void (*)(NearArgs);
-
-template <int DT>
-struct Kern {
-  static ScanFn scan(int mode) {
-    return mode == KVV_MODE_ISCLOSE ? (ScanFn)scan_kernel<DT, KVV_MODE_ISCLOSE> : (ScanFn)scan_kernel<DT, KVV_MODE_MAX_ABS_DIFF>;
-  }
-  static NearFn near(int mode) {
-    return mode == KVV_MODE_ISCLOSE ? (NearFn)near_kernel<DT, KVV_MODE_ISCLOSE> : (NearFn)near_kernel<DT, KVV_MODE_MAX_ABS_DIFF>;
-  }
-};
-
-void kernels_for(int dt, int mode, ScanFn& s, NearFn& nr) {
-  switch (dt) {
-#define KVV_CASE(X) case X: s = Kern<X>::scan(mode); nr = Kern<X>::near(mode); return;
-    KVV_CASE(KVV_F32) KVV_CASE(KVV_F16) KVV_CASE(KVV_BF16) KVV_CASE(KVV_F64) KVV_CASE(KVV_F8E4M3FN)
-    KVV_CASE(KVV_F8E5M2) KVV_CASE(KVV_I8) KVV_CASE(KVV_U8) KVV_CASE(KVV_I16) KVV_CASE(KVV_I32)
-    KVV_CASE(KVV_I64) KVV_CASE(KVV_BOOL)
-#undef KVV_CASE
-    default: s = nullptr; nr = nullptr;
-  }
 }
 
 // ------------------------------------------------------------ workspace
 struct WsLayout {
-  size_t runs, run_valid, sample_abs, sample_rel, hist, nan_cnt, item_near, item_near_off, item_near_sum, near_sample,
-      table, chunk_seg, total;
+  size_t runs, sample_abs, sample_rel, hist, nan_cnt, sel_state, item_near, item_near_off, item_near_sum,
+      near_sample, table, chunk_seg, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -190,11 +212,11 @@ WsLayout workspace_layout(int64_t items, int64_t samples, int64_t nseg, int64_t 
     return at;
   };
   L.runs = take((size_t)items * sizeof(RunRec));
-  L.run_valid = take((size_t)items * 4);
   L.sample_abs = take((size_t)samples * 4);
   L.sample_rel = take((size_t)samples * 4);
   L.hist = take((size_t)nseg * kHistPerSeg * 4);
   L.nan_cnt = take((size_t)nseg * kArrays * 4);
+  L.sel_state = take((size_t)nseg * kSelStatePerSeg * 4);
   if (near) {
     L.item_near = take((size_t)items * 4);
     L.item_near_off = take((size_t)items * 8);
@@ -214,11 +236,90 @@ T* at(void* ws, size_t off) {
   return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
 }
 
-// Persistent-style grid: a few blocks per CU, each streaming a contiguous range of
-// items.  Capped so that a segment never has more runs than reduce_kernel lists.
-int64_t blocks_target() {
-  const int64_t b = (int64_t)device_cus() * 4;
-  return b < 2048 ? b : 2048;
+int check_ws(const WsLayout& L, void* ws, size_t ws_bytes, kvv_result* out) {
+  if (!ws) return fail(KVV_E_WORKSPACE, "workspace is null");
+  if (ws_bytes < L.total) return fail(KVV_E_WORKSPACE, "workspace too small: need " + std::to_string(L.total));
+  if (reinterpret_cast<uintptr_t>(ws) % 256) return fail(KVV_E_WORKSPACE, "workspace must be 256-byte aligned");
+  if (!out) return fail(KVV_E_INVALID, "null result pointer");
+  return KVV_OK;
+}
+
+// One near_kernel launch per scan group (the kernel is templated on dtype/mode).
+struct NearLaunch {
+  NearFn fn;
+  int seg_lo;
+  int nseg;
+  int64_t item_lo, items;
+};
+
+// The launches after the main pass, shared by the single and batch paths.
+int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchunk, int nseg, int64_t total_chunks,
+                bool near, const WsLayout& L, void* ws, kvv_result* out, hipStream_t st,
+                const std::vector<NearLaunch>& nears) {
+  ReduceArgs ra{};
+  if (seg0) ra.seg0 = *seg0;
+  ra.table = dtable;
+  ra.runs = at<RunRec>(ws, L.runs);
+  ra.out = out;
+  ra.hist = at<uint32_t>(ws, L.hist);
+  ra.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
+  ra.sel_state = at<uint32_t>(ws, L.sel_state);
+  ra.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
+  ra.item_near_off = near ? at<uint64_t>(ws, L.item_near_off) : nullptr;
+  hipLaunchKernelGGL(reduce_kernel, dim3(nseg), dim3(kReduceBlock), 0, st, ra);
+  KVV_HIP(hipGetLastError());
+  if (near) {
+    for (const auto& nl : nears) {
+      if (nl.items == 0) continue;
+      NearArgs na{};
+      if (seg0) na.seg0 = *seg0;
+      na.table = dtable ? dtable + nl.seg_lo : nullptr;
+      na.nseg = nl.nseg;
+      na.item_lo = nl.item_lo;
+      na.items = nl.items;
+      na.res = out;
+      na.item_near_off = at<uint64_t>(ws, L.item_near_off);
+      na.item_near = at<uint32_t>(ws, L.item_near);
+      na.near_sample = at<float>(ws, L.near_sample);
+      na.item_near_sum = at<double>(ws, L.item_near_sum);
+      hipLaunchKernelGGL(nl.fn, dim3((unsigned)nl.items), dim3(kBlock), 0, st, na);
+      KVV_HIP(hipGetLastError());
+    }
+  }
+  const int narr = near ? 3 : 2;
+  if (total_chunks > 0) {
+    SelectArgs sa{};
+    if (seg0) sa.seg0 = *seg0;
+    sa.table = dtable;
+    sa.chunk_seg = dchunk;
+    sa.nseg = nseg;
+    sa.narrays = narr;
+    sa.total_chunks = total_chunks;
+    sa.res = out;
+    sa.arr[0] = at<float>(ws, L.sample_abs);
+    sa.arr[1] = at<float>(ws, L.sample_rel);
+    sa.arr[2] = near ? at<float>(ws, L.near_sample) : nullptr;
+    sa.hist = at<uint32_t>(ws, L.hist);
+    sa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
+    sa.sel_state = at<uint32_t>(ws, L.sel_state);
+    for (int pass = 0; pass < kSelPasses; ++pass) {
+      sa.pass = pass;
+      hipLaunchKernelGGL(select_kernel, dim3((unsigned)(narr * total_chunks)), dim3(kBlock), 0, st, sa);
+      KVV_HIP(hipGetLastError());
+    }
+  }
+  FinalArgs fa{};
+  if (seg0) fa.seg0 = *seg0;
+  fa.table = dtable;
+  fa.narrays = narr;
+  fa.res = out;
+  fa.hist = at<uint32_t>(ws, L.hist);
+  fa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
+  fa.sel_state = at<uint32_t>(ws, L.sel_state);
+  fa.item_near_sum = near ? at<double>(ws, L.item_near_sum) : nullptr;
+  hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)(nseg * narr)), dim3(kBlock), 0, st, fa);
+  KVV_HIP(hipGetLastError());
+  return KVV_OK;
 }
 
 // ------------------------------------------------------------ one verdict
@@ -228,17 +329,17 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   d.item_begin = 0;
   d.sample_off = 0;
   d.chunk_begin = 0;
+  d.out_index = 0;
   const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
   const WsLayout L = workspace_layout(d.item_count, d.m, 1, d.chunk_count, near, false);
-  if (!ws) return fail(KVV_E_WORKSPACE, "workspace is null");
-  if (ws_bytes < L.total) return fail(KVV_E_WORKSPACE, "workspace too small: need " + std::to_string(L.total));
-  if (reinterpret_cast<uintptr_t>(ws) % 256) return fail(KVV_E_WORKSPACE, "workspace must be 256-byte aligned");
-  if (!out) return fail(KVV_E_INVALID, "null result pointer");
-  ScanFn scan;
-  NearFn nearfn;
-  kernels_for(d.dtype, d.mode, scan, nearfn);
+  int rc = check_ws(L, ws, ws_bytes, out);
+  if (rc) return rc;
+  const int kind = scan_kind(d);
+  ScanFn scan = scan_fn(d.dtype, d.mode, kind, false);
   if (!scan) return fail(KVV_E_INVALID, "no kernel for dtype");
-
+  const int64_t target = blocks_target();
+  d.run_base = 0;
+  d.run_ipb = d.item_count > 0 ? (d.item_count + target - 1) / target : 1;
   if (d.item_count > 0) {
     ScanArgs a{};
     a.seg0 = d;
@@ -246,10 +347,8 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     a.nseg = 1;
     a.item_lo = 0;
     a.items = d.item_count;
-    const int64_t target = blocks_target();
-    a.items_per_block = (d.item_count + target - 1) / target;
+    a.items_per_block = d.run_ipb;
     a.runs = at<RunRec>(ws, L.runs);
-    a.run_valid = at<uint32_t>(ws, L.run_valid);
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);
     a.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
@@ -259,73 +358,19 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     KVV_HIP(hipGetLastError());
     if (ev_end) KVV_HIP(hipEventRecord(ev_end, st));
   }
-  ReduceArgs ra{};
-  ra.seg0 = d;
-  ra.table = nullptr;
-  ra.runs = at<RunRec>(ws, L.runs);
-  ra.run_valid = at<uint32_t>(ws, L.run_valid);
-  ra.out = out;
-  ra.hist = at<uint32_t>(ws, L.hist);
-  ra.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
-  ra.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
-  ra.item_near_off = near ? at<uint64_t>(ws, L.item_near_off) : nullptr;
-  hipLaunchKernelGGL(reduce_kernel, dim3(1), dim3(kReduceBlock), 0, st, ra);
-  KVV_HIP(hipGetLastError());
-
-  if (near && d.item_count > 0) {
-    NearArgs na{};
-    na.seg0 = d;
-    na.table = nullptr;
-    na.nseg = 1;
-    na.item_lo = 0;
-    na.items = d.item_count;
-    na.res = out;
-    na.item_near_off = at<uint64_t>(ws, L.item_near_off);
-    na.item_near = at<uint32_t>(ws, L.item_near);
-    na.near_sample = at<float>(ws, L.near_sample);
-    na.item_near_sum = at<double>(ws, L.item_near_sum);
-    hipLaunchKernelGGL(nearfn, dim3((unsigned)d.item_count), dim3(kBlock), 0, st, na);
-    KVV_HIP(hipGetLastError());
-  }
-  const int narr = near ? 3 : 2;
-  if (d.chunk_count > 0) {
-    SelectArgs sa{};
-    sa.seg0 = d;
-    sa.table = nullptr;
-    sa.chunk_seg = nullptr;
-    sa.nseg = 1;
-    sa.narrays = narr;
-    sa.total_chunks = d.chunk_count;
-    sa.res = out;
-    sa.arr[0] = at<float>(ws, L.sample_abs);
-    sa.arr[1] = at<float>(ws, L.sample_rel);
-    sa.arr[2] = near ? at<float>(ws, L.near_sample) : nullptr;
-    sa.hist = at<uint32_t>(ws, L.hist);
-    sa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
-    for (int pass = 0; pass < kSelPasses; ++pass) {
-      sa.pass = pass;
-      hipLaunchKernelGGL(select_kernel, dim3((unsigned)(narr * d.chunk_count)), dim3(kBlock), 0, st, sa);
-      KVV_HIP(hipGetLastError());
-    }
-  }
-  FinalArgs fa{};
-  fa.seg0 = d;
-  fa.table = nullptr;
-  fa.narrays = narr;
-  fa.res = out;
-  fa.hist = at<uint32_t>(ws, L.hist);
-  fa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
-  fa.item_near_sum = near ? at<double>(ws, L.item_near_sum) : nullptr;
-  hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kBlock), 0, st, fa);
-  KVV_HIP(hipGetLastError());
-  return KVV_OK;
+  std::vector<NearLaunch> nears{{near_fn(d.dtype, d.mode), 0, 1, 0, d.item_count}};
+  return launch_tail(&d, nullptr, nullptr, 1, d.chunk_count, near, L, ws, out, st, nears);
 }
 
 // ------------------------------------------------------------ batch
 struct BatchPlan {
-  std::vector<SegDesc> table;       // sorted by (dtype, mode) group, then input order
+  std::vector<SegDesc> table;   // sorted by (dtype, mode, kind) group, then input order
   std::vector<int64_t> chunk_seg;
-  struct Group { int dt, mode; int seg_lo, seg_hi; int64_t item_lo, items; };
+  struct Group {
+    int dt, mode, kind;
+    int seg_lo, seg_hi;
+    int64_t item_lo, items, ipb;
+  };
   std::vector<Group> groups;
   int64_t items = 0, samples = 0, chunks = 0;
   bool near = false;
@@ -335,35 +380,44 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   if (count < 0) return fail(KVV_E_INVALID, "negative count");
   if (count > 0 && (!gens || !refs || !pols)) return fail(KVV_E_INVALID, "null batch arrays");
   std::vector<SegDesc> segs((size_t)count);
-  std::vector<int> order((size_t)count);
+  std::vector<int> order((size_t)count), kinds((size_t)count);
   for (int i = 0; i < count; ++i) {
     int rc = plan_segment(&gens[i], &refs[i], &pols[i], segs[i]);
     if (rc) return fail(rc, "pair " + std::to_string(i) + ": " + g_err);
     segs[i].out_index = i;
+    kinds[i] = scan_kind(segs[i]);
     order[i] = i;
   }
-  std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
-    const int ka = segs[a].dtype * 2 + segs[a].mode, kb = segs[b].dtype * 2 + segs[b].mode;
-    return ka < kb;
-  });
+  auto key = [&](int i) { return (segs[i].dtype * 2 + segs[i].mode) * 3 + kinds[i]; };
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return key(a) < key(b); });
   bp.table.clear();
-  for (int i : order) bp.table.push_back(segs[i]);
   int64_t item = 0, sample = 0, chunk = 0;
-  for (size_t s = 0; s < bp.table.size(); ++s) {
-    SegDesc& d = bp.table[s];
+  for (int i : order) {
+    SegDesc d = segs[i];
     d.item_begin = item;
     d.sample_off = sample;
     d.chunk_begin = chunk;
+    const int s = (int)bp.table.size();
+    for (int64_t c = 0; c < d.chunk_count; ++c) bp.chunk_seg.push_back((int64_t)s);
     item += d.item_count;
     sample += d.m;
-    for (int64_t c = 0; c < d.chunk_count; ++c) bp.chunk_seg.push_back((int64_t)s);
     chunk += d.chunk_count;
     bp.near = bp.near || (d.flags & KVV_FLAG_NEAR_ZERO);
-    if (bp.groups.empty() || bp.groups.back().dt != d.dtype || bp.groups.back().mode != d.mode) {
-      bp.groups.push_back({d.dtype, d.mode, (int)s, (int)s + 1, d.item_begin, d.item_count});
+    if (bp.groups.empty() || bp.groups.back().dt != d.dtype || bp.groups.back().mode != d.mode ||
+        bp.groups.back().kind != kinds[i]) {
+      bp.groups.push_back({d.dtype, d.mode, kinds[i], s, s + 1, d.item_begin, d.item_count, 1});
     } else {
-      bp.groups.back().seg_hi = (int)s + 1;
+      bp.groups.back().seg_hi = s + 1;
       bp.groups.back().items += d.item_count;
+    }
+    bp.table.push_back(d);
+  }
+  const int64_t target = blocks_target();
+  for (auto& gr : bp.groups) {
+    gr.ipb = gr.items > 0 ? (gr.items + target - 1) / target : 1;
+    for (int s = gr.seg_lo; s < gr.seg_hi; ++s) {
+      bp.table[s].run_base = gr.item_lo;
+      bp.table[s].run_ipb = gr.ipb;
     }
   }
   bp.items = item;
@@ -376,28 +430,25 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   const int nseg = (int)bp.table.size();
   if (nseg == 0) return KVV_OK;
   const WsLayout L = workspace_layout(bp.items, bp.samples, nseg, bp.chunks, bp.near, true);
-  if (!ws) return fail(KVV_E_WORKSPACE, "workspace is null");
-  if (ws_bytes < L.total) return fail(KVV_E_WORKSPACE, "workspace too small: need " + std::to_string(L.total));
-  if (reinterpret_cast<uintptr_t>(ws) % 256) return fail(KVV_E_WORKSPACE, "workspace must be 256-byte aligned");
-  if (!out) return fail(KVV_E_INVALID, "null result pointer");
+  int rc = check_ws(L, ws, ws_bytes, out);
+  if (rc) return rc;
   SegDesc* dtable = at<SegDesc>(ws, L.table);
   int64_t* dchunk = at<int64_t>(ws, L.chunk_seg);
   KVV_HIP(hipMemcpyAsync(dtable, bp.table.data(), nseg * sizeof(SegDesc), hipMemcpyHostToDevice, st));
   if (bp.chunks) KVV_HIP(hipMemcpyAsync(dchunk, bp.chunk_seg.data(), bp.chunks * 8, hipMemcpyHostToDevice, st));
-  const int64_t target = blocks_target();
+  std::vector<NearLaunch> nears;
   for (const auto& gr : bp.groups) {
+    nears.push_back({near_fn(gr.dt, gr.mode), gr.seg_lo, gr.seg_hi - gr.seg_lo, gr.item_lo, gr.items});
     if (gr.items == 0) continue;
-    ScanFn scan;
-    NearFn nearfn;
-    kernels_for(gr.dt, gr.mode, scan, nearfn);
+    ScanFn scan = scan_fn(gr.dt, gr.mode, gr.kind, true);
+    if (!scan) return fail(KVV_E_INVALID, "no kernel for dtype");
     ScanArgs a{};
     a.table = dtable + gr.seg_lo;
     a.nseg = gr.seg_hi - gr.seg_lo;
     a.item_lo = gr.item_lo;
     a.items = gr.items;
-    a.items_per_block = (gr.items + target - 1) / target;
+    a.items_per_block = gr.ipb;
     a.runs = at<RunRec>(ws, L.runs);
-    a.run_valid = at<uint32_t>(ws, L.run_valid);
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);
     a.item_near = bp.near ? at<uint32_t>(ws, L.item_near) : nullptr;
@@ -405,67 +456,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
     KVV_HIP(hipGetLastError());
   }
-  ReduceArgs ra{};
-  ra.table = dtable;
-  ra.runs = at<RunRec>(ws, L.runs);
-  ra.run_valid = at<uint32_t>(ws, L.run_valid);
-  ra.out = out;
-  ra.hist = at<uint32_t>(ws, L.hist);
-  ra.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
-  ra.item_near = bp.near ? at<uint32_t>(ws, L.item_near) : nullptr;
-  ra.item_near_off = bp.near ? at<uint64_t>(ws, L.item_near_off) : nullptr;
-  hipLaunchKernelGGL(reduce_kernel, dim3(nseg), dim3(kReduceBlock), 0, st, ra);
-  KVV_HIP(hipGetLastError());
-  if (bp.near) {
-    for (const auto& gr : bp.groups) {
-      if (gr.items == 0) continue;
-      ScanFn scan;
-      NearFn nearfn;
-      kernels_for(gr.dt, gr.mode, scan, nearfn);
-      NearArgs na{};
-      na.table = dtable + gr.seg_lo;
-      na.nseg = gr.seg_hi - gr.seg_lo;
-      na.item_lo = gr.item_lo;
-      na.items = gr.items;
-      na.res = out;
-      na.item_near_off = at<uint64_t>(ws, L.item_near_off);
-      na.item_near = at<uint32_t>(ws, L.item_near);
-      na.near_sample = at<float>(ws, L.near_sample);
-      na.item_near_sum = at<double>(ws, L.item_near_sum);
-      hipLaunchKernelGGL(nearfn, dim3((unsigned)gr.items), dim3(kBlock), 0, st, na);
-      KVV_HIP(hipGetLastError());
-    }
-  }
-  const int narr = bp.near ? 3 : 2;
-  if (bp.chunks > 0) {
-    SelectArgs sa{};
-    sa.table = dtable;
-    sa.chunk_seg = dchunk;
-    sa.nseg = nseg;
-    sa.narrays = narr;
-    sa.total_chunks = bp.chunks;
-    sa.res = out;
-    sa.arr[0] = at<float>(ws, L.sample_abs);
-    sa.arr[1] = at<float>(ws, L.sample_rel);
-    sa.arr[2] = bp.near ? at<float>(ws, L.near_sample) : nullptr;
-    sa.hist = at<uint32_t>(ws, L.hist);
-    sa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
-    for (int pass = 0; pass < kSelPasses; ++pass) {
-      sa.pass = pass;
-      hipLaunchKernelGGL(select_kernel, dim3((unsigned)(narr * bp.chunks)), dim3(kBlock), 0, st, sa);
-      KVV_HIP(hipGetLastError());
-    }
-  }
-  FinalArgs fa{};
-  fa.table = dtable;
-  fa.narrays = narr;
-  fa.res = out;
-  fa.hist = at<uint32_t>(ws, L.hist);
-  fa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
-  fa.item_near_sum = bp.near ? at<double>(ws, L.item_near_sum) : nullptr;
-  hipLaunchKernelGGL(finalize_kernel, dim3(nseg), dim3(kBlock), 0, st, fa);
-  KVV_HIP(hipGetLastError());
-  return KVV_OK;
+  return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.near, L, ws, out, st, nears);
 }
 
 }  // namespace
@@ -483,7 +474,8 @@ int kvv_workspace_size(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_p
   kvv::SegDesc d;
   int rc = kvv::plan_segment(gen, ref, policy, d);
   if (rc) return rc;
-  *bytes = kvv::workspace_layout(d.item_count, d.m, 1, d.chunk_count, (d.flags & KVV_FLAG_NEAR_ZERO) != 0, false).total;
+  *bytes =
+      kvv::workspace_layout(d.item_count, d.m, 1, d.chunk_count, (d.flags & KVV_FLAG_NEAR_ZERO) != 0, false).total;
   return KVV_OK;
 }
 

@@ -180,17 +180,37 @@ template <> struct Elem<KVV_BOOL> : IntElemBase {
   __device__ static bool finite(T) { return true; }
 };
 
-// ULP / integer distance of a pair (never called for NaN pairs).
+// Bucket of a ULP / integer distance (width <= 32 bits).
+__device__ __forceinline__ int ulp_bucket32(uint32_t d) {
+  const int bl = 32 - __clz(d);  // 0 for d == 0
+  return bl < kBuckets - 1 ? bl : kBuckets - 1;
+}
+
+// ULP / integer distance bucket of a pair (never called for NaN pairs).  Float
+// codes compare as sign-magnitude (through zero for opposite signs, so +0 and
+// -0 coincide); integers by value.  Types of at most 32 bits stay in 32-bit math.
 template <int DT>
-__device__ __forceinline__ uint64_t pair_distance(typename Elem<DT>::T g, typename Elem<DT>::T r) {
+__device__ __forceinline__ int pair_bucket(typename Elem<DT>::T g, typename Elem<DT>::T r) {
   using E = Elem<DT>;
-  if constexpr (E::is_float) {
-    const uint64_t mg = E::mag(g), mr = E::mag(r);
-    if (E::sign(g) == E::sign(r)) return mg > mr ? mg - mr : mr - mg;
-    return mg + mr;  // opposite signs: distance through zero (+0 and -0 coincide)
+  if constexpr (E::width <= 32) {
+    if constexpr (E::is_float) {
+      const uint32_t mg = (uint32_t)E::mag(g), mr = (uint32_t)E::mag(r);
+      const uint32_t d = (E::sign(g) == E::sign(r)) ? (mg > mr ? mg - mr : mr - mg) : mg + mr;
+      return ulp_bucket32(d);
+    } else {
+      const int64_t a = E::v(g), b = E::v(r);
+      return ulp_bucket32((uint32_t)(a > b ? a - b : b - a));
+    }
   } else {
-    const int64_t a = E::v(g), b = E::v(r);
-    return a > b ? (uint64_t)a - (uint64_t)b : (uint64_t)b - (uint64_t)a;
+    uint64_t d;
+    if constexpr (E::is_float) {
+      const uint64_t mg = E::mag(g), mr = E::mag(r);
+      d = (E::sign(g) == E::sign(r)) ? (mg > mr ? mg - mr : mr - mg) : mg + mr;
+    } else {
+      const int64_t a = E::v(g), b = E::v(r);
+      d = a > b ? (uint64_t)a - (uint64_t)b : (uint64_t)b - (uint64_t)a;
+    }
+    return ulp_bucket(d);
   }
 }
 

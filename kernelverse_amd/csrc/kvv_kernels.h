@@ -1,16 +1,21 @@
-// Verdict kernels for gfx950.
+// Verdict kernels for gfx950 (wave64).
 //
-//   scan_kernel     one HBM pass over both tensors: elementwise test, counts,
-//                   maxima with argmax, ULP histogram, fp64 sums, finite
-//                   pattern, and the strided sample (re-read from cache).
-//                   Per-block partial "run records" go to the workspace.
-//   reduce_kernel   one block per segment: combines its run records in a fixed
-//                   order (bit-reproducible) and writes the kvv_result.
+//   scan_kernel     one HBM pass over both tensors.  Every block owns a
+//                   contiguous range of "items" (fixed-size chunks of one
+//                   segment) and writes one partial record per run of items
+//                   of the same segment.  Inside an item, phase A handles the
+//                   bit-identical finite pairs with a handful of ops each;
+//                   the other pairs are compacted per wave into an LDS queue
+//                   and processed densely (phase B).  The next item's loads
+//                   are in flight during phase B.  The strided sample of the
+//                   reference's p99/cosine/norm-ratio is re-read from cache.
+//   reduce_kernel   one block per segment: folds its run records field by
+//                   field in a fixed order (bit-reproducible) into kvv_result.
 //   near_kernel     tolerant-policy near-zero diagnostics: the rank-strided
 //                   sample of the compacted near-zero abs_diff array.
-//   select_kernel   exact order statistics of the samples: 4 passes of an
-//                   8-bit radix select with shared histograms.
-//   finalize_kernel torch.quantile's rank/lerp arithmetic and the near-zero mean.
+//   select_kernel   exact order statistics of the sample arrays: 4 passes of
+//                   an 8-bit radix select over shared histograms.
+//   finalize_kernel the last digit, torch.quantile's lerp, the near-zero mean.
 #pragma once
 
 #include "kvv_device.h"
@@ -18,12 +23,16 @@
 namespace kvv {
 
 constexpr int kUnroll = 4;            // 16-byte vectors per thread per item
-constexpr int kSelChunk = 16384;      // sample values per select block
+constexpr int kSelChunk = 4096;       // sample values per select block
 constexpr int kArrays = 3;            // abs, rel, near-zero abs
 constexpr int kSelPasses = 4;
 constexpr int kHistPerSeg = kArrays * kSelPasses * 2 * 256;
 
 enum Layout { L_CONTIG = 0, L_ROWS = 1, L_GENERIC = 2 };
+enum ScanKind { K_CONTIG = 0, K_ROWS = 1, K_SCALAR = 2 };
+
+// Wave-level counters kept in LDS (one row per wave).
+enum WaveCounter { WC_MISM = LC_COUNT, WC_COUNT };
 
 struct Dims {
   int32_t ndim;
@@ -45,6 +54,10 @@ struct SegDesc {
   int64_t sample_off;     // offset into the sample arrays
   int64_t chunk_begin;    // first select chunk of this segment (per array)
   int64_t chunk_count;    // select chunks per array (sized for m)
+  int64_t run_base;       // first item of the scan launch holding this segment
+  int64_t run_ipb;        // items per block of that launch
+  uint64_t s_div, s_mod;  // (n-1) = s_div*(m-1) + s_mod: sample i sits at i*s_div + floor(i*s_mod/(m-1))
+  double s_inv;           // 1/(m-1)
   int32_t layout;         // enum Layout
   int32_t vec;            // 16-byte vector access allowed
   int32_t mode;           // enum kvv_mode
@@ -78,29 +91,29 @@ struct ScanArgs {
   int64_t item_lo;         // items of this launch: [item_lo, item_lo + items)
   int64_t items;
   int64_t items_per_block;
-  RunRec* runs;            // indexed by global item
-  uint32_t* run_valid;     // 1 where a run starts at that item
+  RunRec* runs;            // indexed by global item (written where a run starts)
   float* sample_abs;
   float* sample_rel;
   uint32_t* item_near;     // near-zero count per item (KVV_FLAG_NEAR_ZERO)
 };
 
+// Per-lane accumulators.  Counts live in the per-wave LDS counters instead.
 struct Acc {
-  uint32_t mism;
   uint32_t mm_abs, mm_rel;
   uint32_t gabs_k, grel_k;
   uint32_t nfast;          // bit-identical finite pairs (ULP bucket 0, never a mismatch)
   uint32_t nnear_fast;     // ... of which near zero
+  float rel_thr;           // rel-max filter: only rel >= ~rel_thr can still win
   uint64_t first_mm, first_viol;
   uint64_t gabs_i, grel_i;
   uint64_t first_fast;     // lowest index of such a pair (an abs/rel argmax candidate of value 0)
-  double e_sq;             // sum of g*g over those pairs (there g == r, so it feeds gg, rr and gr)
-  double s[7];             // full path: gg rr gr dd | sampled gg rr gr
+  double e_sq;             // sum of g*g over those pairs (there g == r: it feeds gg, rr and gr)
+  double s[7];             // other pairs: gg rr gr dd | sampled gg rr gr
   __device__ void init() {
-    mism = 0;
     mm_abs = mm_rel = 0;
     gabs_k = grel_k = 0;
     nfast = nnear_fast = 0;
+    rel_thr = -__builtin_inff();
     first_mm = first_viol = kNone;
     gabs_i = grel_i = kNone;
     first_fast = kNone;
@@ -110,8 +123,13 @@ struct Acc {
   }
 };
 
-__device__ __forceinline__ void lds_inc(uint32_t* col, int c) {
-  __hip_atomic_fetch_add(&col[c * kBlock], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
+
+// Adds the number of lanes where `pred` holds to a per-wave LDS counter
+// (one ds_add by one lane, whatever the number of lanes).
+__device__ __forceinline__ void wave_add(uint32_t* wc, int c, bool pred) {
+  const uint64_t b = __ballot(pred);
+  if (b && lane_id() == __ffsll((long long)b) - 1) atomicAdd(&wc[c], (uint32_t)__popcll(b));
 }
 
 // ------------------------------------------------------------ addressing
@@ -142,6 +160,11 @@ __device__ __forceinline__ void elem_offsets(const SegDesc& d, int64_t idx, int6
   }
 }
 
+template <int DT>
+__device__ __forceinline__ typename Elem<DT>::T load_elem(const void* base, int64_t off) {
+  return reinterpret_cast<const typename Elem<DT>::T*>(base)[off];
+}
+
 // ------------------------------------------------------------ per element
 // The reference's arithmetic, in float32 with every operation rounded on its
 // own (the library is built with -ffp-contract=off):
@@ -151,8 +174,8 @@ __device__ __forceinline__ void elem_offsets(const SegDesc& d, int64_t idx, int6
 //       mismatch = abs_diff > max_abs_diff
 //   rel_diff = float(abs_diff) / (|float(r)| + 1e-12f)        (GCR:730)
 template <int DT, int MODE>
-__device__ __forceinline__ void elem_diff(typename Elem<DT>::T gc, typename Elem<DT>::T rc, const SegDesc& d,
-                                          float& adf, float& rel, uint32_t& abs_key, bool& mm, float& rf) {
+__device__ __forceinline__ void elem_test(typename Elem<DT>::T gc, typename Elem<DT>::T rc, const SegDesc& d,
+                                          float& adf, uint32_t& abs_key, bool& mm, float& rf) {
   using E = Elem<DT>;
   const float gf = E::f32(gc);
   rf = E::f32(rc);
@@ -177,75 +200,96 @@ __device__ __forceinline__ void elem_diff(typename Elem<DT>::T gc, typename Elem
     adf = (float)ad;
     abs_key = ikey(ad);
   }
-  rel = adf / (fabsf(rf) + 1e-12f);
 }
 
+// Lower bound below which a rel_diff can no longer beat `best` (conservative:
+// the caller skips an element only when abs_diff < thr * (|r| + 1e-12)).
+__device__ __forceinline__ float rel_threshold(float best) {
+  if (best != best) return __builtin_inff();
+  if (best > 0.0f) return best * 0.99999f;
+  if (best < 0.0f) return best * 1.00001f;
+  return 0.0f;
+}
+
+// Full treatment of one element for the lanes with `act` set.  Every lane of
+// the wave calls it (it uses ballots); counts go to the wave's LDS row `wc`.
 template <int DT, int MODE>
-__device__ __forceinline__ void process_elem(typename Elem<DT>::T gc, typename Elem<DT>::T rc, uint64_t idx,
-                                             const SegDesc& d, Acc& acc, uint32_t* col) {
+__device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem<DT>::T rc, bool act, uint64_t idx,
+                                          const SegDesc& d, Acc& acc, uint32_t* wc) {
   using E = Elem<DT>;
-  float adf, rel, rf;
+  float adf, rf;
   uint32_t abs_key;
   bool mm;
-  elem_diff<DT, MODE>(gc, rc, d, adf, rel, abs_key, mm, rf);
-  const uint32_t rel_key = fkey(rel);
+  elem_test<DT, MODE>(gc, rc, d, adf, abs_key, mm, rf);
+  const float den = fabsf(rf) + 1e-12f;
+  mm = mm && act;
+  wave_add(wc, WC_MISM, mm);
   if (mm) {
-    acc.mism++;
-    if (acc.first_mm == kNone) acc.first_mm = idx;
+    const float rel = adf / den;
+    const uint32_t rk = fkey(rel);
+    if (idx < acc.first_mm) acc.first_mm = idx;
     acc.mm_abs = abs_key > acc.mm_abs ? abs_key : acc.mm_abs;
-    acc.mm_rel = rel_key > acc.mm_rel ? rel_key : acc.mm_rel;
+    acc.mm_rel = rk > acc.mm_rel ? rk : acc.mm_rel;
   }
-  // Within a thread indices only grow, so "strictly greater, or first seen" is the argmax rule.
-  if (abs_key > acc.gabs_k || acc.gabs_i == kNone) {
+  if (act && better(abs_key, idx, acc.gabs_k, acc.gabs_i)) {
     acc.gabs_k = abs_key;
     acc.gabs_i = idx;
   }
-  if (rel_key > acc.grel_k || acc.grel_i == kNone) {
-    acc.grel_k = rel_key;
-    acc.grel_i = idx;
+  if (act && !(adf < acc.rel_thr * den)) {
+    const float rel = adf / den;
+    const uint32_t rk = fkey(rel);
+    if (better(rk, idx, acc.grel_k, acc.grel_i)) {
+      acc.grel_k = rk;
+      acc.grel_i = idx;
+      acc.rel_thr = rel_threshold(rel);
+    }
   }
   bool nan_pair = false;
   if constexpr (E::is_float) {
-    const bool ng = E::isnan(gc), nr = E::isnan(rc);
-    const bool ig = E::isinf(gc), ir = E::isinf(rc);
-    if (ng | nr | ig | ir) {
+    const bool nf = act && !(E::finite(gc) && E::finite(rc));
+    if (__ballot(nf)) {
       // finite-pattern rule of GCR:414-437 at a non-finite position
+      const bool ng = E::isnan(gc), nr = E::isnan(rc);
+      const bool ig = E::isinf(gc), ir = E::isinf(rc);
       const bool ok = (ng && nr) || (ig && ir && E::sign(gc) == E::sign(rc));
-      if (!ok) {
-        lds_inc(col, LC_VIOL);
-        if (acc.first_viol == kNone) acc.first_viol = idx;
-      }
-      if (ng) lds_inc(col, LC_NAN_G);
-      if (nr) lds_inc(col, LC_NAN_R);
-      if (ig) lds_inc(col, E::sign(gc) ? LC_NINF_G : LC_PINF_G);
-      if (ir) lds_inc(col, E::sign(rc) ? LC_NINF_R : LC_PINF_R);
-      if (ng | nr) {
-        lds_inc(col, LC_NANPAIR);
-        nan_pair = true;
-      }
+      const bool viol = nf && !ok;
+      wave_add(wc, LC_VIOL, viol);
+      if (viol && idx < acc.first_viol) acc.first_viol = idx;
+      wave_add(wc, LC_NAN_G, nf && ng);
+      wave_add(wc, LC_NAN_R, nf && nr);
+      wave_add(wc, LC_PINF_G, nf && ig && !E::sign(gc));
+      wave_add(wc, LC_NINF_G, nf && ig && E::sign(gc));
+      wave_add(wc, LC_PINF_R, nf && ir && !E::sign(rc));
+      wave_add(wc, LC_NINF_R, nf && ir && E::sign(rc));
+      nan_pair = ng || nr;
+      wave_add(wc, LC_NANPAIR, act && nan_pair);
     }
   }
-  if (!nan_pair) lds_inc(col, LC_HIST0 + ulp_bucket(pair_distance<DT>(gc, rc)));
-  const double g64 = E::f64(gc), r64 = E::f64(rc);
-  const double d64 = g64 - r64;
-  acc.s[0] = fma(g64, g64, acc.s[0]);
-  acc.s[1] = fma(r64, r64, acc.s[1]);
-  acc.s[2] = fma(g64, r64, acc.s[2]);
-  acc.s[3] = fma(d64, d64, acc.s[3]);
+  // ULP histogram: one ds_add per distinct bucket present in the wave
+  const bool hv = act && !nan_pair;
+  const int bk = pair_bucket<DT>(gc, rc);
+  uint64_t pend = __ballot(hv);
+  while (pend) {
+    const int l0 = __ffsll((long long)pend) - 1;
+    const int kb = __shfl(bk, l0);
+    const uint64_t same = __ballot(hv && bk == kb);
+    if (lane_id() == l0) atomicAdd(&wc[LC_HIST0 + kb], (uint32_t)__popcll(same));
+    pend &= ~same;
+  }
+  if (act) {
+    const double g64 = E::f64(gc), r64 = E::f64(rc);
+    const double d64 = g64 - r64;
+    acc.s[0] = fma(g64, g64, acc.s[0]);
+    acc.s[1] = fma(r64, r64, acc.s[1]);
+    acc.s[2] = fma(g64, r64, acc.s[2]);
+    acc.s[3] = fma(d64, d64, acc.s[3]);
+  }
   if (d.flags & KVV_FLAG_NEAR_ZERO) {
     const bool near = fabsf(rf) <= d.nz_abs;
-    if (near) {
-      lds_inc(col, LC_NEAR);
-      if (adf > d.nz_bad) lds_inc(col, LC_NEARBAD);
-    } else if (mm) {
-      lds_inc(col, LC_FARMM);
-    }
+    wave_add(wc, LC_NEAR, act && near);
+    wave_add(wc, LC_NEARBAD, act && near && adf > d.nz_bad);
+    wave_add(wc, LC_FARMM, mm && !near);
   }
-}
-
-template <int DT>
-__device__ __forceinline__ typename Elem<DT>::T load_elem(const void* base, int64_t off) {
-  return reinterpret_cast<const typename Elem<DT>::T*>(base)[off];
 }
 
 // One sampled element: its abs/rel go to the sample arrays at sample index i,
@@ -258,12 +302,12 @@ __device__ __forceinline__ void sample_one(const SegDesc& d, int64_t idx, int64_
   elem_offsets(d, idx, og, orr);
   const auto gc = load_elem<DT>(d.g, og);
   const auto rc = load_elem<DT>(d.r, orr);
-  float adf, rel, rf;
+  float adf, rf;
   uint32_t k;
   bool mm;
-  elem_diff<DT, MODE>(gc, rc, d, adf, rel, k, mm, rf);
+  elem_test<DT, MODE>(gc, rc, d, adf, k, mm, rf);
   sabs[d.sample_off + i] = adf;
-  srel[d.sample_off + i] = rel;
+  srel[d.sample_off + i] = adf / (fabsf(rf) + 1e-12f);
   const double g64 = E::f64(gc), r64 = E::f64(rc);
   acc.s[4] = fma(g64, g64, acc.s[4]);
   acc.s[5] = fma(r64, r64, acc.s[5]);
@@ -289,112 +333,321 @@ __device__ __forceinline__ void sample_range(const SegDesc& d, int64_t L0, int64
   }
 }
 
-// Vector path: 16-byte loads of both tensors, kUnroll vectors per thread.
-//
-// Phase A runs over every element and only tells bit-identical finite pairs
-// apart from the rest: such a pair is never a mismatch, has abs_diff = rel_diff
-// = 0, ULP distance 0, and contributes g*g to the three product sums.  Phase B
-// gives every other element the full treatment (process_elem), each lane
-// walking its own list of such elements re-read from an LDS stage, so the
-// wave pays for the longest list of any lane rather than for every element.
-template <int DT, int MODE>
-__device__ __forceinline__ void scan_item_vec(const SegDesc& d, int64_t L0, int64_t L1, Acc& acc, uint32_t* col,
-                                              uint4* stage) {
-  using E = Elem<DT>;
-  using T = typename E::T;
-  constexpr int V = 16 / sizeof(T);
-  constexpr int NE = V * kUnroll;
-  static_assert(NE <= 64, "per-lane element mask is 64 bits");
+// ------------------------------------------------------------ vector item
+template <int DT>
+struct VecIO {
+  using T = typename Elem<DT>::T;
+  static constexpr int V = 16 / sizeof(T);
+  static constexpr int NE = V * kUnroll;
   union Vec {
     uint4 u;
     T e[V];
   };
-  const int tid = threadIdx.x;
-  Vec gv[kUnroll], rv[kUnroll];
+};
+
+// Issues the 16-byte loads of one item (kUnroll vectors per thread per tensor).
+template <int DT, int KIND>
+__device__ __forceinline__ uint32_t load_item(const SegDesc& d, int64_t L0, int64_t L1, uint4* gv, uint4* rv) {
+  using IO = VecIO<DT>;
+  using T = typename IO::T;
+  constexpr int V = IO::V;
   uint32_t full = 0;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t v = L0 + (int64_t)(u * kBlock + tid) * V;
+    const int64_t v = L0 + (int64_t)(u * kBlock + threadIdx.x) * V;
     if (v + V <= L1) {
       full |= 1u << u;
       int64_t og, orr;
-      if (d.layout == L_CONTIG) {
+      if constexpr (KIND == K_CONTIG) {
         og = orr = v;
       } else {
-        elem_offsets(d, v, og, orr);
+        const int64_t row = v / d.row_len;
+        const int64_t col = v - row * d.row_len;
+        outer_offsets(d.dims, row, og, orr);
+        og += col;
+        orr += col;
       }
-      gv[u].u = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(d.g) + og);
-      rv[u].u = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(d.r) + orr);
+      gv[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(d.g) + og);
+      rv[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(d.r) + orr);
     } else {
-      gv[u].u = make_uint4(0, 0, 0, 0);
-      rv[u].u = make_uint4(0, 0, 0, 0);
+      gv[u] = make_uint4(0, 0, 0, 0);
+      rv[u] = make_uint4(0, 0, 0, 0);
     }
   }
+  return full;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves only (no LDS):
+// shifts 1, 2, 4, 8 inside each 16-lane row, then row 15 -> next row and lane 31
+// -> upper half.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);  // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);  // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);  // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);  // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false); // row_bcast:15
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false); // row_bcast:31
+  return v;
+}
+
+// Phase A over the registers of one item.  Bit-identical finite pairs are
+// finished here (count, g*g into e_sq); returns the lane's mask of the other
+// elements of its full vectors.
+template <int DT, bool NEAR, bool TRACK>
+__device__ __forceinline__ uint64_t phase_a(const SegDesc& d, int64_t L0, const uint4* stage, uint32_t full,
+                                            Acc& acc) {
+  using E = Elem<DT>;
+  using IO = VecIO<DT>;
+  using T = typename IO::T;
+  constexpr int V = IO::V;
   const bool fast_ok = d.fast != 0;
-  const bool near_mode = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
-  uint64_t slow = 0, valid = 0;
+  const int tid = threadIdx.x;
+  uint64_t slow = 0, fastm = 0;
   double esq = 0.0;
   uint32_t nnear = 0;
-#pragma unroll
+  uint64_t ff = acc.first_fast;
+  // one vector pair at a time (not unrolled), so few values are live at once
+#pragma unroll 1
   for (int u = 0; u < kUnroll; ++u) {
     if (!((full >> u) & 1u)) continue;
+    typename IO::Vec gv, rv;
+    gv.u = stage[(2 * u) * kBlock + tid];
+    rv.u = stage[(2 * u + 1) * kBlock + tid];
+    uint32_t sb = 0, fb = 0;
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-      const T gc = gv[u].e[e], rc = rv[u].e[e];
+      const T gc = gv.e[e], rc = rv.e[e];
       const bool fast = fast_ok && gc == rc && E::finite(gc);
-      const double g64 = fast ? E::f64(gc) : 0.0;
+      const float gf = fast ? E::f32(gc) : 0.0f;
+      const double g64 = (double)gf;
       esq = fma(g64, g64, esq);
-      if (near_mode) nnear += (fast && fabsf(E::f32(gc)) <= d.nz_abs) ? 1u : 0u;
-      slow |= (uint64_t)(!fast) << (u * V + e);
+      if constexpr (NEAR) nnear += (fast && fabsf(gf) <= d.nz_abs) ? 1u : 0u;
+      if constexpr (TRACK) {
+        const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + tid) * V + e);
+        if (fast && idx < ff) ff = idx;
+      }
+      sb |= (fast ? 0u : 1u) << e;
+      fb |= (fast ? 1u : 0u) << e;
     }
-    valid |= ((1ull << V) - 1) << (u * V);
+    slow |= (uint64_t)sb << (u * V);
+    fastm |= (uint64_t)fb << (u * V);
   }
   acc.e_sq += esq;
-  acc.nnear_fast += nnear;
-  const uint64_t fastm = valid & ~slow;
   acc.nfast += (uint32_t)__popcll(fastm);
-  if (fastm && acc.first_fast == kNone) {
-    const int k = __builtin_ctzll(fastm);
-    acc.first_fast = (uint64_t)(L0 + ((int64_t)(k / V) * kBlock + tid) * V + (k % V));
+  if constexpr (NEAR) acc.nnear_fast += nnear;
+  if constexpr (TRACK) acc.first_fast = ff;
+  return slow;
+}
+
+// Appends the lanes' remaining elements to the wave's queue in lane order
+// (entry = (lane << 6) | slot); returns the number of entries.
+template <int NE>
+__device__ __forceinline__ uint32_t build_queue(uint64_t slow, uint16_t* queue) {
+  const int lane = lane_id();
+  const uint32_t cnt = (uint32_t)__popcll(slow);
+  const uint32_t incl = wave_incl_scan(cnt);
+  const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  uint32_t at = incl - cnt;
+  while (slow) {
+    const int k = __builtin_ctzll(slow);
+    slow &= slow - 1;
+    if (at < 64u * NE) queue[at] = (uint16_t)((lane << 6) | k);
+    ++at;
   }
-  slow &= valid;
-  if (slow) {
-#pragma unroll
+  return total < 64u * NE ? total : 64u * NE;
+}
+
+// Phase B: the wave's queued elements, 64 at a time, from the LDS stage.
+template <int DT, int MODE>
+__device__ __forceinline__ void phase_b(const SegDesc& d, int64_t L0, uint32_t total, const uint4* stage,
+                                        const uint16_t* queue, Acc& acc, uint32_t* wc) {
+  using IO = VecIO<DT>;
+  using T = typename IO::T;
+  constexpr int V = IO::V;
+  const int lane = lane_id(), w = threadIdx.x >> 6;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (uint32_t j = 0; j < total; j += 64) {
+    const uint32_t qi = j + lane;
+    const bool act = qi < total;
+    const uint32_t ent = act ? queue[qi] : 0u;
+    const int src = (int)(ent >> 6), k = (int)(ent & 63);
+    const int u = k / V, e = k % V;
+    const int t = w * 64 + src;
+    const T gc = reinterpret_cast<const T*>(&stage[(2 * u) * kBlock + t])[e];
+    const T rc = reinterpret_cast<const T*>(&stage[(2 * u + 1) * kBlock + t])[e];
+    const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + t) * V + e);
+    slow_elem<DT, MODE>(gc, rc, act, idx, d, acc, wc);
+  }
+}
+
+// Strided-sample cursor: the next sample index i, its logical position idx =
+// floor(i*(n-1)/(m-1)) and rem = i*(n-1) mod (m-1).  Kept identical in every
+// wave of the block (wave-uniform), advanced item by item.
+struct SampleCursor {
+  uint64_t i, idx;
+  uint32_t rem;
+};
+
+// Cursor at the first sample whose position is >= L0 (64-bit division, once per run).
+__device__ __forceinline__ SampleCursor cursor_at(const SegDesc& d, int64_t L0) {
+  SampleCursor c;
+  if (d.n <= d.max_samples) {
+    c.i = c.idx = (uint64_t)L0;
+    c.rem = 0;
+    return c;
+  }
+  const uint64_t num = (uint64_t)d.n - 1, den = (uint64_t)d.m - 1;
+  c.i = ((uint64_t)L0 * den + num - 1) / num;  // ceil(L0 * den / num)
+  const uint64_t p = c.i * num;
+  c.idx = p / den;
+  c.rem = (uint32_t)(p - c.idx * den);
+  return c;
+}
+
+// The pair at logical index idx of a vector item: from the stage when its
+// vector was a full 16-byte load, else (partial last vector) from memory.
+template <int DT>
+__device__ __forceinline__ void stage_pair(const SegDesc& d, int64_t L0, int64_t L1, int64_t idx, const uint4* stage,
+                                           typename Elem<DT>::T& gc, typename Elem<DT>::T& rc) {
+  using IO = VecIO<DT>;
+  using T = typename IO::T;
+  constexpr int V = IO::V;
+  const int64_t q = idx - L0;
+  const int64_t vstart = idx - q % V;
+  if (vstart + V <= L1) {
+    const int vec = (int)(q / V);
+    const int u = vec / kBlock, t = vec % kBlock, e = (int)(q % V);
+    gc = reinterpret_cast<const T*>(&stage[(2 * u) * kBlock + t])[e];
+    rc = reinterpret_cast<const T*>(&stage[(2 * u + 1) * kBlock + t])[e];
+  } else {
+    int64_t og, orr;
+    elem_offsets(d, idx, og, orr);
+    gc = load_elem<DT>(d.g, og);
+    rc = load_elem<DT>(d.r, orr);
+  }
+}
+
+template <int DT, int MODE>
+__device__ __forceinline__ void sample_write(const SegDesc& d, typename Elem<DT>::T gc, typename Elem<DT>::T rc,
+                                             uint64_t i, Acc& acc, float* sabs, float* srel) {
+  using E = Elem<DT>;
+  float adf, rf;
+  uint32_t kk;
+  bool mm;
+  elem_test<DT, MODE>(gc, rc, d, adf, kk, mm, rf);
+  sabs[d.sample_off + i] = adf;
+  srel[d.sample_off + i] = adf / (fabsf(rf) + 1e-12f);
+  const double g64 = E::f64(gc), r64 = E::f64(rc);
+  acc.s[4] = fma(g64, g64, acc.s[4]);
+  acc.s[5] = fma(r64, r64, acc.s[5]);
+  acc.s[6] = fma(g64, r64, acc.s[6]);
+}
+
+// Samples of a vector item (GCR:346-347).  Every wave walks the same cursor, 64
+// samples per step (lane l takes sample cursor.i + l), and a lane handles its
+// sample only when the element sits in its own wave's stage slots, so no
+// barrier is needed.  When n <= max_samples every element is a sample and each
+// lane simply takes its own slots.
+template <int DT, int MODE>
+__device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_t L1, const uint4* stage, Acc& acc,
+                                            float* sabs, float* srel, SampleCursor& cur) {
+  using IO = VecIO<DT>;
+  using T = typename IO::T;
+  constexpr int V = IO::V;
+  const int lane = lane_id(), w = threadIdx.x >> 6;
+  if (d.n <= d.max_samples) {
+#pragma unroll 1
     for (int u = 0; u < kUnroll; ++u) {
-      stage[(2 * u) * kBlock + tid] = gv[u].u;
-      stage[(2 * u + 1) * kBlock + tid] = rv[u].u;
-    }
-    while (slow) {
-      const int k = __builtin_ctzll(slow);
-      slow &= slow - 1;
-      const int u = k / V, e = k % V;
-      const T gc = reinterpret_cast<const T*>(&stage[(2 * u) * kBlock + tid])[e];
-      const T rc = reinterpret_cast<const T*>(&stage[(2 * u + 1) * kBlock + tid])[e];
-      const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + tid) * V + e);
-      process_elem<DT, MODE>(gc, rc, idx, d, acc, col);
-    }
-  }
-  // a partial last vector (numel not a multiple of the vector width)
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t v = L0 + (int64_t)(u * kBlock + tid) * V;
-    if (!((full >> u) & 1u) && v < L1) {
-      for (int64_t idx = v; idx < L1; ++idx) {
-        int64_t og, orr;
-        elem_offsets(d, idx, og, orr);
-        process_elem<DT, MODE>(load_elem<DT>(d.g, og), load_elem<DT>(d.r, orr), (uint64_t)idx, d, acc, col);
+      const int64_t v = L0 + (int64_t)(u * kBlock + threadIdx.x) * V;
+      for (int e = 0; e < V; ++e) {
+        if (v + e >= L1) break;
+        T gc, rc;
+        stage_pair<DT>(d, L0, L1, v + e, stage, gc, rc);
+        sample_write<DT, MODE>(d, gc, rc, (uint64_t)(v + e), acc, sabs, srel);
       }
+    }
+    return;
+  }
+  const uint32_t den = (uint32_t)(d.m - 1);
+  for (;;) {
+    if (cur.i >= (uint64_t)d.m || cur.idx >= (uint64_t)L1) return;
+    const uint32_t t = cur.rem + (uint32_t)lane * (uint32_t)d.s_mod;  // < 64 * den < 2^30
+    uint32_t q = (uint32_t)((double)t * d.s_inv);
+    if (q * den > t) --q;
+    if ((q + 1) * den <= t) ++q;
+    const uint32_t rem = t - q * den;
+    const uint64_t i = cur.i + (uint64_t)lane;
+    const uint64_t idx = cur.idx + (uint64_t)lane * d.s_div + q;
+    const bool in = i < (uint64_t)d.m && idx < (uint64_t)L1;
+    if (in) {
+      const int64_t qq = (int64_t)idx - L0;
+      const int owner = (int)((qq / V) % kBlock) >> 6;
+      if (owner == w) {
+        T gc, rc;
+        stage_pair<DT>(d, L0, L1, (int64_t)idx, stage, gc, rc);
+        sample_write<DT, MODE>(d, gc, rc, i, acc, sabs, srel);
+      }
+    }
+    const uint64_t inb = __ballot(in);
+    const int c = (int)__popcll(inb);  // the in-range lanes are a prefix
+    if (c < 64) {
+      // the first out-of-range lane holds the next sample
+      cur.i += (uint64_t)c;
+      cur.idx = (uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)idx, c) |
+                ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(idx >> 32), c) << 32);
+      cur.rem = (uint32_t)__builtin_amdgcn_readlane((int)rem, c);
+      return;
+    }
+    // all 64 in range: step past lane 63
+    const uint64_t idx63 = (uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)idx, 63) |
+                           ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(idx >> 32), 63) << 32);
+    const uint32_t rem63 = (uint32_t)__builtin_amdgcn_readlane((int)rem, 63);
+    uint32_t nr = rem63 + (uint32_t)d.s_mod;
+    uint64_t nidx = idx63 + d.s_div;
+    if (nr >= den) {
+      nr -= den;
+      nidx += 1;
+    }
+    cur.i += 64;
+    cur.idx = nidx;
+    cur.rem = nr;
+  }
+}
+
+// Elements of a partial last vector (numel not a multiple of the vector width).
+template <int DT, int MODE>
+__device__ __forceinline__ void vec_tail(const SegDesc& d, int64_t L0, int64_t L1, uint32_t full, Acc& acc,
+                                         uint32_t* wc) {
+  constexpr int V = VecIO<DT>::V;
+#pragma unroll 1
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t v = L0 + (int64_t)(u * kBlock + threadIdx.x) * V;
+    const bool part = !((full >> u) & 1u) && v < L1;
+    if (__ballot(part) == 0) continue;
+    for (int e = 0; e < V; ++e) {
+      const bool act = part && v + e < L1;
+      int64_t og = 0, orr = 0;
+      if (act) elem_offsets(d, v + e, og, orr);
+      const auto gc = act ? load_elem<DT>(d.g, og) : (typename Elem<DT>::T)0;
+      const auto rc = act ? load_elem<DT>(d.r, orr) : (typename Elem<DT>::T)0;
+      slow_elem<DT, MODE>(gc, rc, act, (uint64_t)(v + e), d, acc, wc);
     }
   }
 }
 
 // Scalar path: any strides, one element per thread per step.
 template <int DT, int MODE>
-__device__ __forceinline__ void scan_item_scalar(const SegDesc& d, int64_t L0, int64_t L1, Acc& acc, uint32_t* col) {
-  for (int64_t idx = L0 + threadIdx.x; idx < L1; idx += kBlock) {
-    int64_t og, orr;
-    elem_offsets(d, idx, og, orr);
-    process_elem<DT, MODE>(load_elem<DT>(d.g, og), load_elem<DT>(d.r, orr), (uint64_t)idx, d, acc, col);
+__device__ __forceinline__ void scan_item_scalar(const SegDesc& d, int64_t L0, int64_t L1, Acc& acc, uint32_t* wc) {
+  for (int64_t base = L0; base < L1; base += kBlock) {
+    const int64_t idx = base + threadIdx.x;
+    const bool act = idx < L1;
+    int64_t og = 0, orr = 0;
+    if (act) elem_offsets(d, idx, og, orr);
+    const auto gc = act ? load_elem<DT>(d.g, og) : (typename Elem<DT>::T)0;
+    const auto rc = act ? load_elem<DT>(d.r, orr) : (typename Elem<DT>::T)0;
+    slow_elem<DT, MODE>(gc, rc, act, (uint64_t)idx, d, acc, wc);
   }
 }
 
@@ -417,20 +670,13 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
   return t;
 }
 
-// Reduces the block's accumulators and LDS counter columns into one RunRec
-// (written by thread 0 at runs[slot]) and resets them for the next run.
-__device__ void flush_run(Acc& acc, uint32_t* s_cnt, BlockScratch& bs, RunRec* out) {
+// Reduces the block's accumulators and wave counters into one RunRec (written
+// by thread 0 at *out) and resets them for the next run.
+__device__ inline void flush_run(Acc& acc, uint32_t (*wcnt)[WC_COUNT], BlockScratch& bs, RunRec* out) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __syncthreads();
-  for (int c = 0; c < LC_COUNT; ++c) {
-    uint64_t own = s_cnt[c * kBlock + tid];
-    if (c == LC_HIST0) own += acc.nfast;
-    if (c == LC_NEAR) own += acc.nnear_fast;
-    uint64_t v = wave_sum(own);
-    s_cnt[c * kBlock + tid] = 0;
-    if (lane == 0) bs.u[w][c] = v;
-  }
-  uint64_t mism = wave_sum((uint64_t)acc.mism);
+  const uint64_t nfast = wave_sum((uint64_t)acc.nfast);
+  const uint64_t nnear = wave_sum((uint64_t)acc.nnear_fast);
   uint64_t fmm = wave_min(acc.first_mm), fvi = wave_min(acc.first_viol);
   uint32_t mma = wave_max(acc.mm_abs), mmr = wave_max(acc.mm_rel);
   // bit-identical pairs have abs_diff = rel_diff = +0, whose key is 0x80000000 in both modes
@@ -453,7 +699,11 @@ __device__ void flush_run(Acc& acc, uint32_t* s_cnt, BlockScratch& bs, RunRec* o
 #pragma unroll
   for (int i = 3; i < 7; ++i) s[i] = wave_sum(acc.s[i]);
   if (lane == 0) {
-    bs.u[w][LC_COUNT + 0] = mism;
+    for (int c = 0; c < LC_COUNT; ++c) bs.u[w][c] = wcnt[w][c];
+    bs.u[w][LC_HIST0] += nfast;
+    bs.u[w][LC_NEAR] += nnear;
+    bs.u[w][LC_COUNT + 0] = wcnt[w][WC_MISM];
+    for (int c = 0; c < WC_COUNT; ++c) wcnt[w][c] = 0;
     bs.u[w][LC_COUNT + 1] = fmm;
     bs.u[w][LC_COUNT + 2] = fvi;
     bs.u[w][LC_COUNT + 3] = gai;
@@ -502,67 +752,122 @@ __device__ void flush_run(Acc& acc, uint32_t* s_cnt, BlockScratch& bs, RunRec* o
 }
 
 // ------------------------------------------------------------ scan kernel
-template <int DT, int MODE>
-__device__ __forceinline__ void scan_item(const SegDesc& d, int64_t item, const ScanArgs& a, Acc& acc,
-                                          uint32_t* s_cnt, uint32_t* red, uint4* stage) {
-  const int64_t L0 = (item - d.item_begin) * (int64_t)d.item_elems;
-  const int64_t L1 = L0 + d.item_elems < d.n ? L0 + d.item_elems : d.n;
-  uint32_t* col = s_cnt + threadIdx.x;
-  const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
-  uint32_t near_before = 0;
-  if (near) near_before = col[LC_NEAR * kBlock] + acc.nnear_fast;
-  if (d.vec)
-    scan_item_vec<DT, MODE>(d, L0, L1, acc, col, stage);
-  else
-    scan_item_scalar<DT, MODE>(d, L0, L1, acc, col);
-  sample_range<DT, MODE>(d, L0, L1, acc, a.sample_abs, a.sample_rel);
-  if (near) {
-    const uint32_t t = block_sum_u32(col[LC_NEAR * kBlock] + acc.nnear_fast - near_before, red);
-    if (threadIdx.x == 0) a.item_near[item] = t;
-  }
+// LDS of one scan block: the item's vectors (NS uint4 per tensor-vector slot)
+// and the per-wave queues of stage positions (NQ = 64 lanes x elements per lane).
+template <int NS, int NQ>
+struct ScanShared {
+  uint4 stage[NS];
+  uint16_t queue[kWaves][NQ];
+  uint32_t wcnt[kWaves][WC_COUNT];
+  uint32_t red[kWaves];
+  BlockScratch bs;
+};
+
+template <int DT, int KIND>
+struct ScanLds {
+  static constexpr bool vec = KIND != K_SCALAR;
+  using type = ScanShared<vec ? 2 * kUnroll * kBlock : 1, vec ? 64 * VecIO<DT>::NE : 2>;
+};
+
+// Per-item near-zero count (feeds the compacted-rank prefix of near_kernel).
+template <typename SM>
+__device__ __forceinline__ void near_item_count(const ScanArgs& a, int64_t item, Acc& acc, SM& sm,
+                                                uint32_t& near_prev) {
+  const int w = threadIdx.x >> 6;
+  uint32_t mine = acc.nnear_fast;
+  if (lane_id() == 0) mine += sm.wcnt[w][LC_NEAR];
+  const uint32_t now = block_sum_u32(mine, sm.red);
+  if (threadIdx.x == 0) a.item_near[item] = now - near_prev;
+  near_prev = now;
 }
 
-template <int DT, int MODE>
+// Phase A variant by wave-uniform conditions: near-zero counting, and tracking
+// of the lowest bit-identical index while it can still be an argmax.
+template <int DT>
+__device__ __forceinline__ uint64_t phase_a_any(const SegDesc& d, int64_t L0, const uint4* stage, uint32_t full,
+                                                Acc& acc) {
+  const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
+  const bool track = __ballot(acc.first_fast == kNone && (acc.gabs_k <= 0x80000000u || acc.grel_k <= 0x80000000u)) != 0;
+  if (near) {
+    return track ? phase_a<DT, true, true>(d, L0, stage, full, acc) : phase_a<DT, true, false>(d, L0, stage, full, acc);
+  }
+  return track ? phase_a<DT, false, true>(d, L0, stage, full, acc) : phase_a<DT, false, false>(d, L0, stage, full, acc);
+}
+
+template <int DT, int MODE, int KIND, bool BATCH>
 __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
-  __shared__ uint32_t s_cnt[LC_COUNT * kBlock];
-  __shared__ uint4 stage[2 * kUnroll * kBlock];
-  __shared__ BlockScratch bs;
-  __shared__ uint32_t red[kWaves];
-  const int tid = threadIdx.x;
-  for (int c = 0; c < LC_COUNT; ++c) s_cnt[c * kBlock + tid] = 0;
+  __shared__ typename ScanLds<DT, KIND>::type sm;
+  const int tid = threadIdx.x, w = tid >> 6;
+  if (tid < kWaves * WC_COUNT) (&sm.wcnt[0][0])[tid] = 0;
   const int64_t i0 = a.item_lo + (int64_t)blockIdx.x * a.items_per_block;
   int64_t i1 = i0 + a.items_per_block;
   if (i1 > a.item_lo + a.items) i1 = a.item_lo + a.items;
   if (i0 >= i1) return;
+  __syncthreads();
   Acc acc;
   acc.init();
-  if (a.table == nullptr) {
-    const SegDesc& d = a.seg0;
-    for (int64_t it = i0; it < i1; ++it) {
-      if (tid == 0) a.run_valid[it] = (it == i0) ? 1u : 0u;
-      scan_item<DT, MODE>(d, it, a, acc, s_cnt, red, stage);
+  uint32_t* wc = sm.wcnt[w];
+  int s = 0;
+  if constexpr (BATCH) {
+    int lo = 0, hi = a.nseg - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (a.table[mid].item_begin <= i0) lo = mid; else hi = mid - 1;
     }
-    flush_run(acc, s_cnt, bs, &a.runs[i0]);
-    return;
+    s = lo;
   }
-  // batch: segments sorted by item_begin; find the one holding i0
-  int lo = 0, hi = a.nseg - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (a.table[mid].item_begin <= i0) lo = mid; else hi = mid - 1;
-  }
-  int s = lo;
   int64_t run_start = i0;
-  for (int64_t it = i0; it < i1; ++it) {
-    while (it >= a.table[s].item_begin + a.table[s].item_count) ++s;
-    if (it != run_start && it == a.table[s].item_begin) {
-      flush_run(acc, s_cnt, bs, &a.runs[run_start]);
-      run_start = it;
-    }
-    if (tid == 0) a.run_valid[it] = (it == run_start) ? 1u : 0u;
-    scan_item<DT, MODE>(a.table[s], it, a, acc, s_cnt, red, stage);
+  uint32_t near_prev = 0;
+  uint4 gv[kUnroll], rv[kUnroll];
+  uint32_t full = 0;
+  bool loaded = false;
+  SampleCursor cur;
+  {
+    const SegDesc& d = BATCH ? a.table[s] : a.seg0;
+    cur = cursor_at(d, (i0 - d.item_begin) * (int64_t)d.item_elems);
   }
-  flush_run(acc, s_cnt, bs, &a.runs[run_start]);
+  for (int64_t it = i0; it < i1; ++it) {
+    if constexpr (BATCH) {
+      if (it >= a.table[s].item_begin + a.table[s].item_count) {
+        while (it >= a.table[s].item_begin + a.table[s].item_count) ++s;
+        flush_run(acc, sm.wcnt, sm.bs, &a.runs[run_start]);
+        run_start = it;
+        near_prev = 0;
+        loaded = false;
+        cur = cursor_at(a.table[s], 0);
+      }
+    }
+    const SegDesc& d = BATCH ? a.table[s] : a.seg0;
+    const int64_t L0 = (it - d.item_begin) * (int64_t)d.item_elems;
+    const int64_t L1 = L0 + d.item_elems < d.n ? L0 + d.item_elems : d.n;
+    if constexpr (KIND == K_SCALAR) {
+      scan_item_scalar<DT, MODE>(d, L0, L1, acc, wc);
+      sample_range<DT, MODE>(d, L0, L1, acc, a.sample_abs, a.sample_rel);
+    } else {
+      if (!loaded) full = load_item<DT, KIND>(d, L0, L1, gv, rv);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        sm.stage[(2 * u) * kBlock + tid] = gv[u];
+        sm.stage[(2 * u + 1) * kBlock + tid] = rv[u];
+      }
+      const uint32_t full_now = full;
+      // next item of the same segment: its loads fly while this one finishes
+      loaded = false;
+      if (it + 1 < i1 && it + 1 < d.item_begin + d.item_count) {
+        const int64_t N0 = L1;
+        const int64_t N1 = N0 + d.item_elems < d.n ? N0 + d.item_elems : d.n;
+        full = load_item<DT, KIND>(d, N0, N1, gv, rv);
+        loaded = true;
+      }
+      const uint64_t slow = phase_a_any<DT>(d, L0, sm.stage, full_now, acc);
+      const uint32_t nslow = __ballot(slow != 0) ? build_queue<VecIO<DT>::NE>(slow, sm.queue[w]) : 0u;
+      if (nslow) phase_b<DT, MODE>(d, L0, nslow, sm.stage, sm.queue[w], acc, wc);
+      if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, full_now, acc, wc);
+      sample_item<DT, MODE>(d, L0, L1, sm.stage, acc, a.sample_abs, a.sample_rel, cur);
+    }
+    if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, sm, near_prev);
+  }
+  flush_run(acc, sm.wcnt, sm.bs, &a.runs[run_start]);
 }
 
 // ------------------------------------------------------------ reduce kernel
@@ -570,24 +875,18 @@ struct ReduceArgs {
   SegDesc seg0;
   const SegDesc* table;
   const RunRec* runs;
-  const uint32_t* run_valid;
   kvv_result* out;
   uint32_t* hist;        // kHistPerSeg per segment
   uint32_t* nan_cnt;     // kArrays per segment
+  uint32_t* sel_state;   // kSelStatePerSeg per segment
   const uint32_t* item_near;
   uint64_t* item_near_off;
 };
 
-
-
 constexpr int kReduceBlock = 1024;
-constexpr int kMaxRuns = 4096;   // runs per segment: at most one per scan block (host caps the grid)
 constexpr int kFields = LC_COUNT + 14;
+constexpr int kSelStatePerSeg = kArrays * (kSelPasses + 1) * 2 * 4;
 
-// Field f of a run record folded into a wave-level partial: counts add,
-// first indices take the minimum, keys the maximum, (key, index) pairs the
-// argmax, fp64 sums add.  Every lane visits its runs in item order and the
-// butterfly order is fixed, so the result does not depend on timing.
 struct FieldAcc {
   uint64_t u;
   uint32_t k;
@@ -600,20 +899,43 @@ __device__ __forceinline__ void field_init(int f, FieldAcc& a) {
   a.u = (f == LC_COUNT + 1 || f == LC_COUNT + 2 || f == LC_COUNT + 5 || f == LC_COUNT + 6) ? kNone : 0;
 }
 
-__device__ __forceinline__ void field_add(int f, FieldAcc& a, const RunRec& r) {
+// Field f of a run record: counts add, first indices take the minimum, keys the
+// maximum, (key, index) pairs the argmax, fp64 sums add.
+__device__ __forceinline__ void field_load(int f, const RunRec& r, FieldAcc& v) {
+  v.k = 0;
+  v.x = 0.0;
+  v.u = 0;
   if (f < LC_COUNT) {
-    a.u += r.cnt[f];
-  } else {
-    switch (f - LC_COUNT) {
-      case 0: a.u += r.mismatch; break;
-      case 1: a.u = r.first_mm < a.u ? r.first_mm : a.u; break;
-      case 2: a.u = r.first_viol < a.u ? r.first_viol : a.u; break;
-      case 3: a.k = r.mm_abs > a.k ? r.mm_abs : a.k; break;
-      case 4: a.k = r.mm_rel > a.k ? r.mm_rel : a.k; break;
-      case 5: if (better(r.gabs_k, r.gabs_i, a.k, a.u)) { a.k = r.gabs_k; a.u = r.gabs_i; } break;
-      case 6: if (better(r.grel_k, r.grel_i, a.k, a.u)) { a.k = r.grel_k; a.u = r.grel_i; } break;
-      default: a.x += r.s[f - LC_COUNT - 7]; break;
+    v.u = r.cnt[f];
+    return;
+  }
+  switch (f - LC_COUNT) {
+    case 0: v.u = r.mismatch; break;
+    case 1: v.u = r.first_mm; break;
+    case 2: v.u = r.first_viol; break;
+    case 3: v.k = r.mm_abs; break;
+    case 4: v.k = r.mm_rel; break;
+    case 5: v.k = r.gabs_k; v.u = r.gabs_i; break;
+    case 6: v.k = r.grel_k; v.u = r.grel_i; break;
+    default: v.x = r.s[f - LC_COUNT - 7]; break;
+  }
+}
+
+__device__ __forceinline__ void field_merge(int f, FieldAcc& a, const FieldAcc& v) {
+  const int g = f - LC_COUNT;
+  if (f < LC_COUNT || g == 0) {
+    a.u += v.u;
+  } else if (g == 1 || g == 2) {
+    a.u = v.u < a.u ? v.u : a.u;
+  } else if (g == 3 || g == 4) {
+    a.k = v.k > a.k ? v.k : a.k;
+  } else if (g == 5 || g == 6) {
+    if (better(v.k, v.u, a.k, a.u)) {
+      a.k = v.k;
+      a.u = v.u;
     }
+  } else {
+    a.x += v.x;
   }
 }
 
@@ -645,65 +967,76 @@ __device__ __forceinline__ double cosine_of(double gr, double gg, double rr) {
   return clamp_cos(gr / (gn * rn));
 }
 
-// One block per segment: lists the segment's runs in item order, then folds
-// the run records field by field (one wave per field group).
+// Item holding run j of a segment.  Runs start at the segment's first item and
+// at every block-range start (run_base + b * run_ipb) inside the segment.
+__device__ __forceinline__ int64_t run_item(const SegDesc& d, int64_t j, int64_t b_first) {
+  return j == 0 ? d.item_begin : d.run_base + (b_first + j - 1) * d.run_ipb;
+}
+
+// One block per segment: folds the segment's run records field by field
+// (16 waves, one field per wave at a time; each lane loads a batch of runs up front).
+#ifdef KVV_COMMON_KERNELS
 __global__ __launch_bounds__(kReduceBlock) void reduce_kernel(ReduceArgs a) {
   constexpr int kW = kReduceBlock / 64;
-  __shared__ uint32_t runs[kMaxRuns];
-  __shared__ uint64_t wsum[kW];
+  constexpr int kBatch = 8;
   __shared__ FieldAcc fres[kFields];
-  __shared__ uint32_t s_nruns;
+  __shared__ uint64_t wsum[kW];
   const int seg = blockIdx.x;
   const SegDesc& d = a.table ? a.table[seg] : a.seg0;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (int i = tid; i < kHistPerSeg; i += kReduceBlock) a.hist[(size_t)seg * kHistPerSeg + i] = 0;
   if (tid < kArrays) a.nan_cnt[seg * kArrays + tid] = 0;
-  // 1. run list (and, in near-zero mode, the exclusive prefix of per-item near counts)
-  const int64_t per = (d.item_count + kReduceBlock - 1) / kReduceBlock;
-  const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
-  const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
-  const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
-  uint64_t nvalid = 0, nnear = 0;
-  for (int64_t k = k0; k < k1; ++k) {
-    nvalid += a.run_valid[d.item_begin + k] ? 1 : 0;
-    if (near) nnear += a.item_near[d.item_begin + k];
+  if (tid < kSelStatePerSeg) a.sel_state[(size_t)seg * kSelStatePerSeg + tid] = 0;
+  // runs of this segment: its first item plus the block starts strictly inside it
+  int64_t nruns = 0, b_first = 0;
+  if (d.item_count > 0) {
+    const int64_t rel0 = d.item_begin - d.run_base;                    // >= 0
+    b_first = rel0 / d.run_ipb + 1;                                     // first block start after item_begin
+    const int64_t rel_end = d.item_begin + d.item_count - d.run_base;  // exclusive
+    const int64_t b_end = (rel_end + d.run_ipb - 1) / d.run_ipb;       // block starts < rel_end
+    nruns = 1 + (b_end > b_first ? b_end - b_first : 0);
   }
-  uint64_t base_runs = 0, base_near = 0;
-  for (int pass = 0; pass < (near ? 2 : 1); ++pass) {
-    const uint64_t mine = pass == 0 ? nvalid : nnear;
+  for (int f = w; f < kFields; f += kW) {
+    FieldAcc fa;
+    field_init(f, fa);
+    for (int64_t base = 0; base < nruns; base += 64 * kBatch) {
+      FieldAcc v[kBatch];
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int64_t j = base + q * 64 + lane;
+        if (j < nruns) {
+          field_load(f, a.runs[run_item(d, j, b_first)], v[q]);
+        } else {
+          field_init(f, v[q]);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) field_merge(f, fa, v[q]);
+    }
+    field_wave_reduce(f, fa);
+    if (lane == 0) fres[f] = fa;
+  }
+  // near-zero: exclusive prefix of the per-item counts, in item order
+  if (d.flags & KVV_FLAG_NEAR_ZERO) {
+    const int64_t per = (d.item_count + kReduceBlock - 1) / kReduceBlock;
+    const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
+    const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
+    uint64_t mine = 0;
+    for (int64_t k = k0; k < k1; ++k) mine += a.item_near[d.item_begin + k];
     uint64_t incl = mine;
     for (int o = 1; o < 64; o <<= 1) {
       const uint64_t v = __shfl_up(incl, o);
       if (lane >= o) incl += v;
     }
-    __syncthreads();
     if (lane == 63) wsum[w] = incl;
     __syncthreads();
     uint64_t base = 0;
     for (int i = 0; i < w; ++i) base += wsum[i];
-    (pass == 0 ? base_runs : base_near) = base + incl - mine;
-  }
-  {
-    uint64_t at = base_runs, nr = base_near;
+    uint64_t run = base + incl - mine;
     for (int64_t k = k0; k < k1; ++k) {
-      const int64_t it = d.item_begin + k;
-      if (a.run_valid[it] && at < kMaxRuns) runs[at++] = (uint32_t)k;
-      if (near) {
-        a.item_near_off[it] = nr;
-        nr += a.item_near[it];
-      }
+      a.item_near_off[d.item_begin + k] = run;
+      run += a.item_near[d.item_begin + k];
     }
-  }
-  if (tid == kReduceBlock - 1) s_nruns = (uint32_t)(base_runs + nvalid);
-  __syncthreads();
-  const uint32_t nruns = s_nruns < kMaxRuns ? s_nruns : kMaxRuns;
-  // 2. field-parallel fold
-  for (int f = w; f < kFields; f += kW) {
-    FieldAcc fa;
-    field_init(f, fa);
-    for (uint32_t r = lane; r < nruns; r += 64) field_add(f, fa, a.runs[d.item_begin + runs[r]]);
-    field_wave_reduce(f, fa);
-    if (lane == 0) fres[f] = fa;
   }
   __syncthreads();
   if (tid != 0) return;
@@ -777,6 +1110,7 @@ __global__ __launch_bounds__(kReduceBlock) void reduce_kernel(ReduceArgs a) {
   o.near_zero_p99_abs = o.near_zero_mean_abs = __builtin_nan("");
   a.out[d.out_index] = o;
 }
+#endif  // KVV_COMMON_KERNELS
 
 // ------------------------------------------------------------ near-zero sample
 // GCR:525-529 compacts abs_diff over |ref| <= near_zero_abs in row-major order
@@ -831,13 +1165,9 @@ __global__ __launch_bounds__(kBlock) void near_kernel(NearArgs a) {
   for (int64_t idx = e0; idx < e1; ++idx) {
     int64_t og, orr;
     elem_offsets(d, idx, og, orr);
-    float adf, rel, rf;
-    uint32_t k;
-    bool mmk;
-    elem_diff<DT, MODE>(load_elem<DT>(d.g, og), load_elem<DT>(d.r, orr), d, adf, rel, k, mmk, rf);
-    mine += fabsf(rf) <= d.nz_abs;
+    mine += fabsf(Elem<DT>::f32(load_elem<DT>(d.r, orr))) <= d.nz_abs;
   }
-  // exclusive block scan (Hillis-Steele in LDS; one item per block, cheap)
+  // exclusive block scan (Hillis-Steele in LDS; one item per block)
   scan[tid] = mine;
   __syncthreads();
   for (int o = 1; o < kBlock; o <<= 1) {
@@ -847,7 +1177,7 @@ __global__ __launch_bounds__(kBlock) void near_kernel(NearArgs a) {
     __syncthreads();
   }
   uint64_t rank = off + scan[tid] - mine;
-  // next sampled rank >= rank: rank j is sampled iff j == floor(i*(c-1)/(mm-1)) for some i
+  // rank j is sampled iff j == floor(i*(c-1)/(mm-1)) for some i
   const bool all = c <= mm;
   uint64_t i_next = 0, j_next = 0;
   if (!all) {
@@ -859,10 +1189,10 @@ __global__ __launch_bounds__(kBlock) void near_kernel(NearArgs a) {
   for (int64_t idx = e0; idx < e1 && mine; ++idx) {
     int64_t og, orr;
     elem_offsets(d, idx, og, orr);
-    float adf, rel, rf;
+    float adf, rf;
     uint32_t k;
     bool mmk;
-    elem_diff<DT, MODE>(load_elem<DT>(d.g, og), load_elem<DT>(d.r, orr), d, adf, rel, k, mmk, rf);
+    elem_test<DT, MODE>(load_elem<DT>(d.g, og), load_elem<DT>(d.r, orr), d, adf, k, mmk, rf);
     if (!(fabsf(rf) <= d.nz_abs)) continue;
     if (all) {
       a.near_sample[d.sample_off + rank] = adf;
@@ -886,10 +1216,12 @@ __global__ __launch_bounds__(kBlock) void near_kernel(NearArgs a) {
 }
 
 // ------------------------------------------------------------ order statistics
+// Selection state per (segment, array, pass, rank): the high bits fixed so far
+// and the residual rank, stored as 4 words {prefix, resid_lo, resid_hi, pad}.
 struct SelectArgs {
   SegDesc seg0;
   const SegDesc* table;
-  const int64_t* chunk_seg;   // batch: owning segment of each chunk (per array layout)
+  const int64_t* chunk_seg;   // batch: owning segment of each chunk
   int32_t nseg;
   int32_t narrays;            // 2, or 3 with near-zero
   int64_t total_chunks;       // chunks per array over all segments
@@ -897,6 +1229,7 @@ struct SelectArgs {
   const float* arr[kArrays];
   uint32_t* hist;
   uint32_t* nan_cnt;
+  uint32_t* sel_state;
   int32_t pass;
   int32_t pad;
 };
@@ -917,7 +1250,7 @@ __device__ __forceinline__ void q99_ranks(int64_t m, uint64_t& lo, uint64_t& hi,
 // Block-cooperative search (kBlock == 256 threads, one per bin): the bin of a
 // 256-bin histogram that holds 0-based rank `resid`, and how many values lie in
 // lower bins.  A rank past the end (only when NaNs were left out) gives bin 255.
-__device__ void block_find_bin(const uint32_t* h, uint64_t resid, uint32_t& bin, uint64_t& below, uint64_t* sh) {
+__device__ inline void block_find_bin(const uint32_t* h, uint64_t resid, uint32_t& bin, uint64_t& below, uint64_t* sh) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const uint64_t c = h[tid];
   uint64_t incl = c;
@@ -945,20 +1278,32 @@ __device__ void block_find_bin(const uint32_t* h, uint64_t resid, uint32_t& bin,
   below = sh[kWaves + 1];
 }
 
-// High bits fixed so far (`passes` digits) and the residual rank of target rr.
-__device__ void block_select_state(const uint32_t* h, int passes, int rr, uint64_t rank, uint32_t& prefix,
-                                   uint64_t& resid, uint64_t* sh) {
-  prefix = 0;
-  resid = rank;
-  for (int p = 0; p < passes; ++p) {
+__device__ __forceinline__ uint32_t* sel_state_at(uint32_t* st, int s, int arr, int pass, int rr) {
+  return st + (size_t)s * kSelStatePerSeg + ((arr * (kSelPasses + 1) + pass) * 2 + rr) * 4;
+}
+
+// State after `pass` digits for both ranks: from the stored state after
+// pass-1 digits and that pass's histogram (pass 0: prefix 0, resid = rank).
+__device__ inline void select_state(uint32_t* st, const uint32_t* h, int s, int arr, int pass, const uint64_t rank[2],
+                             uint32_t prefix[2], uint64_t resid[2], uint64_t* sh) {
+  for (int rr = 0; rr < 2; ++rr) {
+    if (pass == 0) {
+      prefix[rr] = 0;
+      resid[rr] = rank[rr];
+      continue;
+    }
+    const uint32_t* prev = sel_state_at(st, s, arr, pass - 1, rr);
+    const uint32_t pp = prev[0];
+    const uint64_t pr = (uint64_t)prev[1] | ((uint64_t)prev[2] << 32);
     uint32_t bin;
     uint64_t below;
-    block_find_bin(h + (p * 2 + rr) * 256, resid, bin, below, sh);
-    prefix = (prefix << 8) | bin;
-    resid -= below;
+    block_find_bin(h + ((pass - 1) * 2 + rr) * 256, pr, bin, below, sh);
+    prefix[rr] = (pp << 8) | bin;
+    resid[rr] = pr - below;
   }
 }
 
+#ifdef KVV_COMMON_KERNELS
 __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   __shared__ uint32_t lh[2][256];
   __shared__ uint64_t sh[kWaves + 2];
@@ -975,17 +1320,21 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   const int64_t c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
   uint32_t* h = a.hist + (size_t)s * kHistPerSeg + (size_t)arr * (kSelPasses * 2 * 256);
   const int pass = a.pass;
-  uint32_t p0 = 0, p1 = 0;
-  {
-    uint64_t lo, hi, r;
-    float w;
-    q99_ranks(count, lo, hi, w);
-    block_select_state(h, pass, 0, lo, p0, r, sh);
-    block_select_state(h, pass, 1, hi, p1, r, sh);
+  uint64_t rank[2], resid[2];
+  uint32_t prefix[2];
+  float wgt;
+  q99_ranks(count, rank[0], rank[1], wgt);
+  select_state(a.sel_state, h, s, arr, pass, rank, prefix, resid, sh);
+  if (c0 == 0 && tid < 2) {
+    uint32_t* dst = sel_state_at(a.sel_state, s, arr, pass, tid);
+    dst[0] = prefix[tid];
+    dst[1] = (uint32_t)resid[tid];
+    dst[2] = (uint32_t)(resid[tid] >> 32);
   }
   for (int i = tid; i < 512; i += kBlock) (&lh[0][0])[i] = 0;
   if (tid == 0) s_nan = 0;
   __syncthreads();
+  const uint32_t p0 = prefix[0], p1 = prefix[1];
   const int shift = 24 - 8 * pass;
   const float* v = a.arr[arr] + d.sample_off;
   uint32_t nans = 0;
@@ -1013,6 +1362,7 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   }
   if (pass == 0 && tid == 0 && s_nan) atomicAdd(&a.nan_cnt[s * kArrays + arr], s_nan);
 }
+#endif  // KVV_COMMON_KERNELS
 
 struct FinalArgs {
   SegDesc seg0;
@@ -1022,57 +1372,57 @@ struct FinalArgs {
   kvv_result* res;
   const uint32_t* hist;
   const uint32_t* nan_cnt;
+  uint32_t* sel_state;
   const double* item_near_sum;
 };
 
-// One block per segment: the exact order statistics of each sample array and
-// torch.quantile's interpolation, plus the near-zero sample mean.
+// One block per (segment, array): the last digit of both order statistics,
+// torch.quantile's interpolation, and (near-zero array) the sample mean.
+#ifdef KVV_COMMON_KERNELS
 __global__ __launch_bounds__(kBlock) void finalize_kernel(FinalArgs a) {
   __shared__ uint64_t sh[kWaves + 2];
   __shared__ double part[kBlock];
-  const int s = blockIdx.x;
+  const int s = blockIdx.x / a.narrays;
+  const int arr = blockIdx.x % a.narrays;
   const SegDesc& d = a.table ? a.table[s] : a.seg0;
   const int tid = threadIdx.x;
   kvv_result& r = a.res[d.out_index];
-  for (int arr = 0; arr < a.narrays; ++arr) {
-    const int64_t count = group_count(d, r, arr);
-    double out = __builtin_nan("");
-    if (count > 0 && a.nan_cnt[s * kArrays + arr] == 0) {
-      const uint32_t* h = a.hist + (size_t)s * kHistPerSeg + (size_t)arr * (kSelPasses * 2 * 256);
-      uint64_t lo, hi, resid;
-      float w;
-      q99_ranks(count, lo, hi, w);
-      uint32_t klo, khi;
-      block_select_state(h, kSelPasses, 0, lo, klo, resid, sh);
-      block_select_state(h, kSelPasses, 1, hi, khi, resid, sh);
-      const float va = fkey_value(klo), vb = fkey_value(khi);
-      // torch's lerp: small weights from the lower end, large ones from the upper end, one rounding each
-      const float diff = vb - va;
-      const float q = fabsf(w) < 0.5f ? fmaf(w, diff, va) : fmaf(w - 1.0f, diff, vb);
-      out = (double)q;
-    }
+  const int64_t count = group_count(d, r, arr);
+  double out = __builtin_nan("");
+  if (count > 0 && a.nan_cnt[s * kArrays + arr] == 0) {
+    const uint32_t* h = a.hist + (size_t)s * kHistPerSeg + (size_t)arr * (kSelPasses * 2 * 256);
+    uint64_t rank[2], resid[2];
+    uint32_t key[2];
+    float w;
+    q99_ranks(count, rank[0], rank[1], w);
+    select_state(a.sel_state, h, s, arr, kSelPasses, rank, key, resid, sh);
+    const float va = fkey_value(key[0]), vb = fkey_value(key[1]);
+    // torch's lerp: small weights from the lower end, large ones from the upper end, one rounding each
+    const float diff = vb - va;
+    const float q = fabsf(w) < 0.5f ? fmaf(w, diff, va) : fmaf(w - 1.0f, diff, vb);
+    out = (double)q;
+  }
+  if (tid == 0) {
+    if (arr == 0) r.p99_abs = out;
+    if (arr == 1) r.p99_rel = out;
+    if (arr == 2) r.near_zero_p99_abs = out;
+  }
+  if (arr == 2 && count > 0) {
+    // fixed-order sum of the per-item sampled sums: contiguous chunks, then chunks in order
+    const int64_t per = (d.item_count + kBlock - 1) / kBlock;
+    const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
+    const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
+    double t = 0.0;
+    for (int64_t k = k0; k < k1; ++k) t += a.item_near_sum[d.item_begin + k];
+    part[tid] = t;
     __syncthreads();
     if (tid == 0) {
-      if (arr == 0) r.p99_abs = out;
-      if (arr == 1) r.p99_rel = out;
-      if (arr == 2) r.near_zero_p99_abs = out;
-    }
-    if (arr == 2 && count > 0) {
-      // fixed-order sum of the per-item sampled sums: contiguous chunks, then chunks in order
-      const int64_t per = (d.item_count + kBlock - 1) / kBlock;
-      const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
-      const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
-      double t = 0.0;
-      for (int64_t k = k0; k < k1; ++k) t += a.item_near_sum[d.item_begin + k];
-      part[tid] = t;
-      __syncthreads();
-      if (tid == 0) {
-        double sum = 0.0;
-        for (int i = 0; i < kBlock; ++i) sum += part[i];
-        r.near_zero_mean_abs = (double)(float)(sum / (double)count);
-      }
+      double sum = 0.0;
+      for (int i = 0; i < kBlock; ++i) sum += part[i];
+      r.near_zero_mean_abs = (double)(float)(sum / (double)count);
     }
   }
 }
+#endif  // KVV_COMMON_KERNELS
 
 }  // namespace kvv
