@@ -114,6 +114,24 @@ def cpu_baseline(g_dev, r_dev, tol, budget_s: float = 20.0):
     }
 
 
+def copy_calibration(steps: int):
+    """A plain device copy of known size: 512 MiB read + 512 MiB written per launch."""
+    dev = torch.device("cuda", 0)
+    src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    print(json.dumps({"copy_bytes_read": src.numel(), "copy_bytes_written": dst.numel(),
+                      "us_per_copy": round(dt * 1e6, 1), "GBps_read_plus_write": round(2 * src.numel() / dt / 1e9, 1)}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -121,6 +139,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c1")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="time a plain 512 MiB device copy instead (the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counts to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the verdict path has no multi-GPU mode "
@@ -128,6 +149,9 @@ def main():
         sys.exit(2)
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a ROCm GPU")
+    if args.copy_calibration:
+        copy_calibration(args.steps)
+        return
     from kernelverse_amd import _lib, verdict
 
     lib = _lib.load()

@@ -62,9 +62,24 @@ int device_cus() {
   return cached_cus;
 }
 
-// Persistent-style grid: a few blocks per CU, each streaming a contiguous range of items.
-int64_t blocks_target() {
-  const int64_t b = (int64_t)device_cus() * 4;
+// Persistent-style grid: exactly as many blocks as the device keeps resident for
+// this kernel (one round, no straggler round), each streaming a contiguous
+// range of items.
+int64_t blocks_target(ScanFn fn) {
+  static thread_local ScanFn cached_fn = nullptr;
+  static thread_local int cached_dev = -1, cached_nb = 0;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  if (fn != cached_fn || dev != cached_dev) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(fn), kBlock, 0) != hipSuccess ||
+        nb <= 0)
+      nb = 2;
+    cached_fn = fn;
+    cached_dev = dev;
+    cached_nb = nb;
+  }
+  const int64_t b = (int64_t)device_cus() * cached_nb;
   return b < 4096 ? b : 4096;
 }
 
@@ -337,7 +352,7 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   const int kind = scan_kind(d);
   ScanFn scan = scan_fn(d.dtype, d.mode, kind, false);
   if (!scan) return fail(KVV_E_INVALID, "no kernel for dtype");
-  const int64_t target = blocks_target();
+  const int64_t target = blocks_target(scan);
   d.run_base = 0;
   d.run_ipb = d.item_count > 0 ? (d.item_count + target - 1) / target : 1;
   if (d.item_count > 0) {
@@ -412,8 +427,8 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     }
     bp.table.push_back(d);
   }
-  const int64_t target = blocks_target();
   for (auto& gr : bp.groups) {
+    const int64_t target = blocks_target(scan_fn(gr.dt, gr.mode, gr.kind, true));
     gr.ipb = gr.items > 0 ? (gr.items + target - 1) / target : 1;
     for (int s = gr.seg_lo; s < gr.seg_hi; ++s) {
       bp.table[s].run_base = gr.item_lo;

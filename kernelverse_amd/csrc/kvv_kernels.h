@@ -345,6 +345,13 @@ struct VecIO {
   };
 };
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 nt_load16(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Issues the 16-byte loads of one item (kUnroll vectors per thread per tensor).
 template <int DT, int KIND>
 __device__ __forceinline__ uint32_t load_item(const SegDesc& d, int64_t L0, int64_t L1, uint4* gv, uint4* rv) {
@@ -367,8 +374,9 @@ __device__ __forceinline__ uint32_t load_item(const SegDesc& d, int64_t L0, int6
         og += col;
         orr += col;
       }
-      gv[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(d.g) + og);
-      rv[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(d.r) + orr);
+      // streamed once: non-temporal loads keep them from displacing reusable lines
+      gv[u] = nt_load16(reinterpret_cast<const T*>(d.g) + og);
+      rv[u] = nt_load16(reinterpret_cast<const T*>(d.r) + orr);
     } else {
       gv[u] = make_uint4(0, 0, 0, 0);
       rv[u] = make_uint4(0, 0, 0, 0);
@@ -390,52 +398,183 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   return v;
 }
 
-// Phase A over the registers of one item.  Bit-identical finite pairs are
-// finished here (count, g*g into e_sq); returns the lane's mask of the other
-// elements of its full vectors.
+// ------------------------------------------------------------ phase A (SWAR)
+// Phase A classifies every element of a lane's full vectors as "fast" (the
+// pair is bit-identical and finite: abs_diff = rel_diff = 0, ULP bucket 0,
+// never a mismatch) or "slow" (everything else, finished in phase B).  The
+// test runs on whole dwords with packed integer arithmetic, so it costs a few
+// instructions per dword instead of compares and lane masks per element.
+//
+// Slow-mask layout (one bit per element of the lane's kUnroll vectors, dword
+// d = u * 4 + j of the item, element s inside the dword):
+//   8-bit  elements: bit (d >> 3) * 32 + s * 8 + (d & 7)
+//   16-bit elements: bit s * 16 + d
+//   32-bit elements: bit d
+//   64-bit elements: bit u * 2 + s   (s = element of the vector)
+// slot_of() maps a bit back to (vector u, element e of that vector).
+static_assert(kUnroll == 4, "the slow-mask layout assumes 16 dwords per lane and item");
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+template <int W>
+__device__ __forceinline__ void slot_of(int p, int& u, int& e) {
+  if constexpr (W == 8) {
+    const int dd = ((p >> 5) << 3) | (p & 7);
+    u = dd >> 2;
+    e = ((dd & 3) << 2) | ((p >> 3) & 3);
+  } else if constexpr (W == 16) {
+    const int dd = p & 15;
+    u = dd >> 2;
+    e = ((dd & 3) << 1) | (p >> 4);
+  } else if constexpr (W == 32) {
+    u = p >> 2;
+    e = p & 3;
+  } else {
+    u = p >> 1;
+    e = p & 1;
+  }
+}
+
+// Packed per-half minimum with 1: 0 where the 16-bit half is 0, else 1.
+__device__ __forceinline__ uint32_t pk_nonzero16(uint32_t v) {
+  uint32_t o;
+  asm("v_pk_min_u16 %0, %1, %2" : "=v"(o) : "v"(v), "s"(0x00010001u));
+  return o;
+}
+
+// Per-element slow flags of one dword (32-bit codes): 1 at bit s * W of
+// element s when the pair differs bitwise or the generated value is not finite.
+template <int DT>
+__device__ __forceinline__ uint32_t dword_flags(uint32_t g, uint32_t r) {
+  using E = Elem<DT>;
+  constexpr int W = E::width;
+  if constexpr (W == 8) {
+    const uint32_t x = g ^ r;
+    uint32_t t = ((x & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | x;  // bit 7 of a byte: byte != 0
+    if constexpr (DT == KVV_F8E4M3FN) {
+      t |= (g & 0x7F7F7F7Fu) + 0x01010101u;              // bit 7: magnitude 0x7F (NaN)
+    } else if constexpr (DT == KVV_F8E5M2) {
+      t |= (g & 0x7C7C7C7Cu) + 0x04040404u;              // bit 7: exponent all ones
+    }
+    return (t >> 7) & 0x01010101u;
+  } else if constexpr (W == 16) {
+    uint32_t v = g ^ r;
+    if constexpr (DT == KVV_BF16 || DT == KVV_F16) {
+      constexpr uint32_t em = DT == KVV_BF16 ? 0x7F80u : 0x7C00u;
+      const u16x2 ge = __builtin_bit_cast(u16x2, g & (em | (em << 16)));
+      const u16x2 nf = __builtin_elementwise_sub_sat(ge, (u16x2){(uint16_t)(em - 1), (uint16_t)(em - 1)});
+      v |= __builtin_bit_cast(uint32_t, nf);
+    }
+    return pk_nonzero16(v);
+  } else {  // 32-bit lanes (64-bit elements are combined by the caller)
+    uint32_t v = g ^ r;
+    if constexpr (DT == KVV_F32) v |= __builtin_elementwise_sub_sat(g & 0x7F800000u, 0x7F7FFFFFu);
+    return v < 1u ? v : 1u;
+  }
+}
+
+// Zero mask of a dword from its flags: all ones over each flagged element.
+template <int W>
+__device__ __forceinline__ uint32_t flag_mask(uint32_t f) {
+  if constexpr (W == 8) return (f << 8) - f;
+  else if constexpr (W == 16) return __umul24(f, 0xFFFFu);
+  else return 0u - f;
+}
+
+// Sum of squares (fp64) and near-zero count of the elements of one dword whose
+// code was zeroed where slow (a zeroed element adds 0 and counts as near).
+template <int DT, bool NEAR>
+__device__ __forceinline__ void dword_fast_sums(uint32_t gz, float nz_abs, double& s0, double& s1, uint32_t& nnear) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  constexpr int W = E::width;
+  constexpr int EPD = 32 / W;
+#pragma unroll
+  for (int k = 0; k < EPD; ++k) {
+    const T c = (T)(gz >> (k * W));
+    if constexpr (NEAR) {
+      const float f = E::f32(c);
+      nnear += fabsf(f) <= nz_abs ? 1u : 0u;
+      const double v = (double)f;
+      if (k & 1) s1 = fma(v, v, s1); else s0 = fma(v, v, s0);
+    } else {
+      const double v = E::f64(c);
+      if (k & 1) s1 = fma(v, v, s1); else s0 = fma(v, v, s0);
+    }
+  }
+}
+
+// Phase A over the stage copy of one item: bit-identical finite pairs are
+// finished here (count; g*g into e_sq, which feeds gg, rr and gr since g == r);
+// returns the lane's slow mask in the layout above.
 template <int DT, bool NEAR, bool TRACK>
 __device__ __forceinline__ uint64_t phase_a(const SegDesc& d, int64_t L0, const uint4* stage, uint32_t full,
                                             Acc& acc) {
   using E = Elem<DT>;
   using IO = VecIO<DT>;
-  using T = typename IO::T;
   constexpr int V = IO::V;
-  const bool fast_ok = d.fast != 0;
+  constexpr int W = E::width;
   const int tid = threadIdx.x;
-  uint64_t slow = 0, fastm = 0;
-  double esq = 0.0;
-  uint32_t nnear = 0;
-  uint64_t ff = acc.first_fast;
-  // one vector pair at a time (not unrolled), so few values are live at once
+  uint32_t m0 = 0, m1 = 0;  // slow mask, low and high 32 bits
+  double s0 = 0.0, s1 = 0.0;
+  uint32_t nnear = 0, nvec = 0;
+  const float nz_abs = d.nz_abs;
 #pragma unroll 1
   for (int u = 0; u < kUnroll; ++u) {
     if (!((full >> u) & 1u)) continue;
-    typename IO::Vec gv, rv;
-    gv.u = stage[(2 * u) * kBlock + tid];
-    rv.u = stage[(2 * u + 1) * kBlock + tid];
-    uint32_t sb = 0, fb = 0;
+    ++nvec;
+    const uint4 gq = stage[(2 * u) * kBlock + tid];
+    const uint4 rq = stage[(2 * u + 1) * kBlock + tid];
+    const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w};
+    const uint32_t rw[4] = {rq.x, rq.y, rq.z, rq.w};
+    if constexpr (W == 64) {
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      const T gc = gv.e[e], rc = rv.e[e];
-      const bool fast = fast_ok && gc == rc && E::finite(gc);
-      const float gf = fast ? E::f32(gc) : 0.0f;
-      const double g64 = (double)gf;
-      esq = fma(g64, g64, esq);
-      if constexpr (NEAR) nnear += (fast && fabsf(gf) <= d.nz_abs) ? 1u : 0u;
-      if constexpr (TRACK) {
-        const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + tid) * V + e);
-        if (fast && idx < ff) ff = idx;
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t glo = gw[2 * e], ghi = gw[2 * e + 1];
+        uint32_t v = (glo ^ rw[2 * e]) | (ghi ^ rw[2 * e + 1]);
+        if constexpr (DT == KVV_F64) v |= __builtin_elementwise_sub_sat(ghi & 0x7FF00000u, 0x7FEFFFFFu);
+        const uint32_t f = v < 1u ? v : 1u;
+        m0 |= f << (u * 2 + e);
+        const uint32_t z = ~(0u - f);
+        const uint64_t c = ((uint64_t)(ghi & z) << 32) | (glo & z);
+        const double x = E::f64(c);
+        if (e) s1 = fma(x, x, s1); else s0 = fma(x, x, s0);
       }
-      sb |= (fast ? 0u : 1u) << e;
-      fb |= (fast ? 1u : 0u) << e;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int dd = u * 4 + j;
+        const uint32_t f = dword_flags<DT>(gw[j], rw[j]);
+        if constexpr (W == 8) {
+          if (dd < 8) m0 |= f << dd; else m1 |= f << (dd - 8);
+        } else {
+          m0 |= f << dd;
+        }
+        const uint32_t gz = gw[j] & ~flag_mask<W>(f);
+        dword_fast_sums<DT, NEAR>(gz, nz_abs, s0, s1, nnear);
+      }
     }
-    slow |= (uint64_t)sb << (u * V);
-    fastm |= (uint64_t)fb << (u * V);
   }
-  acc.e_sq += esq;
-  acc.nfast += (uint32_t)__popcll(fastm);
-  if constexpr (NEAR) acc.nnear_fast += nnear;
-  if constexpr (TRACK) acc.first_fast = ff;
+  const uint64_t slow = ((uint64_t)m1 << 32) | m0;
+  const uint32_t nslow = (uint32_t)__popcll(slow);
+  acc.e_sq += s0 + s1;
+  acc.nfast += nvec * V - nslow;
+  if constexpr (NEAR) {
+    // zeroed slow elements were counted as near when 0 <= nz_abs
+    acc.nnear_fast += nnear - (0.0f <= nz_abs ? nslow : 0u);
+  }
+  if constexpr (TRACK) {
+    // lowest logical index of a fast element (vectors in order, then elements)
+    uint64_t ff = acc.first_fast;
+    for (int p = 0; p < V * kUnroll; ++p) {
+      int u, e;
+      slot_of<W>(p, u, e);
+      if (!((full >> u) & 1u) || ((slow >> p) & 1u)) continue;
+      const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + tid) * V + e);
+      if (idx < ff) ff = idx;
+    }
+    acc.first_fast = ff;
+  }
   return slow;
 }
 
@@ -472,8 +611,9 @@ __device__ __forceinline__ void phase_b(const SegDesc& d, int64_t L0, uint32_t t
     const uint32_t qi = j + lane;
     const bool act = qi < total;
     const uint32_t ent = act ? queue[qi] : 0u;
-    const int src = (int)(ent >> 6), k = (int)(ent & 63);
-    const int u = k / V, e = k % V;
+    const int src = (int)(ent >> 6);
+    int u, e;
+    slot_of<Elem<DT>::width>((int)(ent & 63), u, e);
     const int t = w * 64 + src;
     const T gc = reinterpret_cast<const T*>(&stage[(2 * u) * kBlock + t])[e];
     const T rc = reinterpret_cast<const T*>(&stage[(2 * u + 1) * kBlock + t])[e];
@@ -786,6 +926,16 @@ __device__ __forceinline__ void near_item_count(const ScanArgs& a, int64_t item,
 template <int DT>
 __device__ __forceinline__ uint64_t phase_a_any(const SegDesc& d, int64_t L0, const uint4* stage, uint32_t full,
                                                 Acc& acc) {
+  if (!d.fast) {
+    // no element can take the fast path: all elements of the full vectors are slow
+    uint64_t all = 0;
+    for (int p = 0; p < VecIO<DT>::NE; ++p) {
+      int u, e;
+      slot_of<Elem<DT>::width>(p, u, e);
+      if ((full >> u) & 1u) all |= 1ull << p;
+    }
+    return all;
+  }
   const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
   const bool track = __ballot(acc.first_fast == kNone && (acc.gabs_k <= 0x80000000u || acc.grel_k <= 0x80000000u)) != 0;
   if (near) {
@@ -1338,13 +1488,23 @@ __global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
   const int shift = 24 - 8 * pass;
   const float* v = a.arr[arr] + d.sample_off;
   uint32_t nans = 0;
-  for (int64_t i = c0 + tid; i < c1; i += kBlock) {
-    const float x = v[i];
-    if (__builtin_isnan(x)) {
+  constexpr int kPer = kSelChunk / kBlock;
+  float x[kPer];
+  // all loads first (independent), then the histogram updates
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int64_t i = c0 + (int64_t)j * kBlock + tid;
+    x[j] = i < c1 ? v[i] : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int64_t i = c0 + (int64_t)j * kBlock + tid;
+    if (i >= c1) continue;
+    if (__builtin_isnan(x[j])) {
       ++nans;
       continue;
     }
-    const uint32_t k = fkey(x);
+    const uint32_t k = fkey(x[j]);
     const uint32_t dig = (k >> shift) & 255u;
     const uint32_t top = pass == 0 ? 0u : (k >> (shift + 8));
     if (top == p0) atomicAdd(&lh[0][dig], 1u);
