@@ -10,7 +10,7 @@
 #include <vector>
 
 #include "kvv.h"
-#define KVV_COMMON_KERNELS 1  // reduce/select/finalize live in this unit only
+#define KVV_COMMON_KERNELS 1  // reduce/select live in this unit only
 #include "kvv_kernels.h"
 #include "kvv_launch.h"
 
@@ -200,7 +200,9 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
     d.vec = 0;
   }
   d.item_count = (n + d.item_elems - 1) / d.item_elems;
-  d.chunk_count = (d.m + kSelChunk - 1) / kSelChunk;
+  // select blocks per array: one for a small group, one per kSelChunk samples otherwise
+  d.chunk_count = d.m == 0 ? 0 : (d.m <= kSmall ? 1 : (d.m + kSelChunk - 1) / kSelChunk);
+  d.lslot = -1;
   if (n > p->max_samples) {
     const uint64_t num = (uint64_t)n - 1, den = (uint64_t)d.m - 1;
     d.s_div = num / den;
@@ -212,13 +214,14 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
 
 // ------------------------------------------------------------ workspace
 struct WsLayout {
-  size_t runs, sample_abs, sample_rel, hist, nan_cnt, sel_state, item_near, item_near_off, item_near_sum,
-      near_sample, table, chunk_seg, total;
+  size_t runs, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample, table,
+      chunk_seg, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-WsLayout workspace_layout(int64_t items, int64_t samples, int64_t nseg, int64_t chunks, bool near, bool batch) {
+WsLayout workspace_layout(int64_t items, int64_t samples, int64_t nseg, int64_t nslots, int64_t chunks, bool near,
+                          bool batch) {
   WsLayout L{};
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -229,9 +232,8 @@ WsLayout workspace_layout(int64_t items, int64_t samples, int64_t nseg, int64_t 
   L.runs = take((size_t)items * sizeof(RunRec));
   L.sample_abs = take((size_t)samples * 4);
   L.sample_rel = take((size_t)samples * 4);
-  L.hist = take((size_t)nseg * kHistPerSeg * 4);
-  L.nan_cnt = take((size_t)nseg * kArrays * 4);
-  L.sel_state = take((size_t)nseg * kSelStatePerSeg * 4);
+  L.slot_bytes = (size_t)nslots * kArrays * kSlotWords * 4;
+  L.slots = take(L.slot_bytes);
   if (near) {
     L.item_near = take((size_t)items * 4);
     L.item_near_off = take((size_t)items * 8);
@@ -267,22 +269,45 @@ struct NearLaunch {
   int64_t item_lo, items;
 };
 
-// The launches after the main pass, shared by the single and batch paths.
+// The launches after the main pass, shared by the single and batch paths:
+// run-record fold + first select level (+ small groups) of the abs/rel samples
+// in one launch; with near-zero diagnostics the near-zero sample and its first
+// level; then select levels 1 and 2 and the final read-off of every array.
 int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchunk, int nseg, int64_t total_chunks,
-                bool near, const WsLayout& L, void* ws, kvv_result* out, hipStream_t st,
+                int64_t nslots, bool near, const WsLayout& L, void* ws, kvv_result* out, hipStream_t st,
                 const std::vector<NearLaunch>& nears) {
-  ReduceArgs ra{};
-  if (seg0) ra.seg0 = *seg0;
-  ra.table = dtable;
-  ra.runs = at<RunRec>(ws, L.runs);
-  ra.out = out;
-  ra.hist = at<uint32_t>(ws, L.hist);
-  ra.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
-  ra.sel_state = at<uint32_t>(ws, L.sel_state);
-  ra.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
-  ra.item_near_off = near ? at<uint64_t>(ws, L.item_near_off) : nullptr;
-  hipLaunchKernelGGL(reduce_kernel, dim3(nseg), dim3(kReduceBlock), 0, st, ra);
-  KVV_HIP(hipGetLastError());
+  TailArgs t{};
+  if (seg0) t.seg0 = *seg0;
+  t.table = dtable;
+  t.chunk_seg = dchunk;
+  t.nseg = nseg;
+  t.total_chunks = total_chunks > 0 ? total_chunks : 1;
+  t.res = out;
+  t.runs = at<RunRec>(ws, L.runs);
+  t.arr[0] = at<float>(ws, L.sample_abs);
+  t.arr[1] = at<float>(ws, L.sample_rel);
+  t.arr[2] = near ? at<float>(ws, L.near_sample) : nullptr;
+  t.slots = at<uint32_t>(ws, L.slots);
+  t.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
+  t.item_near_off = near ? at<uint64_t>(ws, L.item_near_off) : nullptr;
+  t.item_near_sum = near ? at<double>(ws, L.item_near_sum) : nullptr;
+  auto launch = [&](int reduce_blocks, int level, int arr_lo, int narr) -> int {
+    TailArgs x = t;
+    x.reduce_blocks = reduce_blocks;
+    x.level = level;
+    x.arr_lo = arr_lo;
+    x.narr = narr;
+    const int64_t grid = reduce_blocks + (total_chunks > 0 ? (int64_t)narr * total_chunks : 0);
+    if (grid == 0) return KVV_OK;
+    if (level == 0) hipLaunchKernelGGL(tail_kernel<0>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
+    else if (level == 1) hipLaunchKernelGGL(tail_kernel<1>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
+    else if (level == 2) hipLaunchKernelGGL(tail_kernel<2>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
+    else hipLaunchKernelGGL(tail_kernel<3>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
+    KVV_HIP(hipGetLastError());
+    return KVV_OK;
+  };
+  int rc = launch(nseg, 0, 0, 2);
+  if (rc) return rc;
   if (near) {
     for (const auto& nl : nears) {
       if (nl.items == 0) continue;
@@ -300,40 +325,18 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
       hipLaunchKernelGGL(nl.fn, dim3((unsigned)nl.items), dim3(kBlock), 0, st, na);
       KVV_HIP(hipGetLastError());
     }
+    rc = launch(0, 0, 2, 1);
+    if (rc) return rc;
   }
-  const int narr = near ? 3 : 2;
-  if (total_chunks > 0) {
-    SelectArgs sa{};
-    if (seg0) sa.seg0 = *seg0;
-    sa.table = dtable;
-    sa.chunk_seg = dchunk;
-    sa.nseg = nseg;
-    sa.narrays = narr;
-    sa.total_chunks = total_chunks;
-    sa.res = out;
-    sa.arr[0] = at<float>(ws, L.sample_abs);
-    sa.arr[1] = at<float>(ws, L.sample_rel);
-    sa.arr[2] = near ? at<float>(ws, L.near_sample) : nullptr;
-    sa.hist = at<uint32_t>(ws, L.hist);
-    sa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
-    sa.sel_state = at<uint32_t>(ws, L.sel_state);
-    for (int pass = 0; pass < kSelPasses; ++pass) {
-      sa.pass = pass;
-      hipLaunchKernelGGL(select_kernel, dim3((unsigned)(narr * total_chunks)), dim3(kBlock), 0, st, sa);
-      KVV_HIP(hipGetLastError());
-    }
+  if (nslots > 0) {
+    const int narr = near ? 3 : 2;
+    rc = launch(0, 1, 0, narr);
+    if (rc) return rc;
+    rc = launch(0, 2, 0, narr);
+    if (rc) return rc;
+    rc = launch(0, 3, 0, narr);
+    if (rc) return rc;
   }
-  FinalArgs fa{};
-  if (seg0) fa.seg0 = *seg0;
-  fa.table = dtable;
-  fa.narrays = narr;
-  fa.res = out;
-  fa.hist = at<uint32_t>(ws, L.hist);
-  fa.nan_cnt = at<uint32_t>(ws, L.nan_cnt);
-  fa.sel_state = at<uint32_t>(ws, L.sel_state);
-  fa.item_near_sum = near ? at<double>(ws, L.item_near_sum) : nullptr;
-  hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)(nseg * narr)), dim3(kBlock), 0, st, fa);
-  KVV_HIP(hipGetLastError());
   return KVV_OK;
 }
 
@@ -345,8 +348,10 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   d.sample_off = 0;
   d.chunk_begin = 0;
   d.out_index = 0;
+  d.lslot = d.m > kSmall ? 0 : -1;
+  const int64_t nslots = d.lslot >= 0 ? 1 : 0;
   const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
-  const WsLayout L = workspace_layout(d.item_count, d.m, 1, d.chunk_count, near, false);
+  const WsLayout L = workspace_layout(d.item_count, d.m, 1, nslots, d.chunk_count, near, false);
   int rc = check_ws(L, ws, ws_bytes, out);
   if (rc) return rc;
   const int kind = scan_kind(d);
@@ -355,6 +360,8 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   const int64_t target = blocks_target(scan);
   d.run_base = 0;
   d.run_ipb = d.item_count > 0 ? (d.item_count + target - 1) / target : 1;
+  if ((uint64_t)d.run_ipb * (uint64_t)d.item_elems >= (1ull << 32))
+    return fail(KVV_E_UNSUPPORTED, "tensor too large for 32-bit per-block counts");
   if (d.item_count > 0) {
     ScanArgs a{};
     a.seg0 = d;
@@ -367,6 +374,8 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);
     a.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
+    a.zero_ptr = at<uint4>(ws, L.slots);
+    a.zero_n4 = (int64_t)(L.slot_bytes / 16);
     const int64_t grid = (d.item_count + a.items_per_block - 1) / a.items_per_block;
     if (ev_begin) KVV_HIP(hipEventRecord(ev_begin, st));
     hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
@@ -374,7 +383,7 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     if (ev_end) KVV_HIP(hipEventRecord(ev_end, st));
   }
   std::vector<NearLaunch> nears{{near_fn(d.dtype, d.mode), 0, 1, 0, d.item_count}};
-  return launch_tail(&d, nullptr, nullptr, 1, d.chunk_count, near, L, ws, out, st, nears);
+  return launch_tail(&d, nullptr, nullptr, 1, d.chunk_count, nslots, near, L, ws, out, st, nears);
 }
 
 // ------------------------------------------------------------ batch
@@ -387,7 +396,7 @@ struct BatchPlan {
     int64_t item_lo, items, ipb;
   };
   std::vector<Group> groups;
-  int64_t items = 0, samples = 0, chunks = 0;
+  int64_t items = 0, samples = 0, chunks = 0, nslots = 0;
   bool near = false;
 };
 
@@ -412,6 +421,7 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     d.item_begin = item;
     d.sample_off = sample;
     d.chunk_begin = chunk;
+    d.lslot = d.m > kSmall ? (int32_t)bp.nslots++ : -1;
     const int s = (int)bp.table.size();
     for (int64_t c = 0; c < d.chunk_count; ++c) bp.chunk_seg.push_back((int64_t)s);
     item += d.item_count;
@@ -430,6 +440,8 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   for (auto& gr : bp.groups) {
     const int64_t target = blocks_target(scan_fn(gr.dt, gr.mode, gr.kind, true));
     gr.ipb = gr.items > 0 ? (gr.items + target - 1) / target : 1;
+    if ((uint64_t)gr.ipb * (uint64_t)item_elems_for(gr.dt) >= (1ull << 32))
+      return fail(KVV_E_UNSUPPORTED, "batch group too large for 32-bit per-block counts");
     for (int s = gr.seg_lo; s < gr.seg_hi; ++s) {
       bp.table[s].run_base = gr.item_lo;
       bp.table[s].run_ipb = gr.ipb;
@@ -444,7 +456,7 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
 int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st) {
   const int nseg = (int)bp.table.size();
   if (nseg == 0) return KVV_OK;
-  const WsLayout L = workspace_layout(bp.items, bp.samples, nseg, bp.chunks, bp.near, true);
+  const WsLayout L = workspace_layout(bp.items, bp.samples, nseg, bp.nslots, bp.chunks, bp.near, true);
   int rc = check_ws(L, ws, ws_bytes, out);
   if (rc) return rc;
   SegDesc* dtable = at<SegDesc>(ws, L.table);
@@ -452,6 +464,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   KVV_HIP(hipMemcpyAsync(dtable, bp.table.data(), nseg * sizeof(SegDesc), hipMemcpyHostToDevice, st));
   if (bp.chunks) KVV_HIP(hipMemcpyAsync(dchunk, bp.chunk_seg.data(), bp.chunks * 8, hipMemcpyHostToDevice, st));
   std::vector<NearLaunch> nears;
+  bool zeroed = false;
   for (const auto& gr : bp.groups) {
     nears.push_back({near_fn(gr.dt, gr.mode), gr.seg_lo, gr.seg_hi - gr.seg_lo, gr.item_lo, gr.items});
     if (gr.items == 0) continue;
@@ -467,11 +480,17 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);
     a.item_near = bp.near ? at<uint32_t>(ws, L.item_near) : nullptr;
+    if (!zeroed) {
+      // the first main-pass launch clears the select slots of the whole batch
+      a.zero_ptr = at<uint4>(ws, L.slots);
+      a.zero_n4 = (int64_t)(L.slot_bytes / 16);
+      zeroed = true;
+    }
     const int64_t grid = (gr.items + a.items_per_block - 1) / a.items_per_block;
     hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
     KVV_HIP(hipGetLastError());
   }
-  return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.near, L, ws, out, st, nears);
+  return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, bp.near, L, ws, out, st, nears);
 }
 
 }  // namespace
@@ -490,7 +509,8 @@ int kvv_workspace_size(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_p
   int rc = kvv::plan_segment(gen, ref, policy, d);
   if (rc) return rc;
   *bytes =
-      kvv::workspace_layout(d.item_count, d.m, 1, d.chunk_count, (d.flags & KVV_FLAG_NEAR_ZERO) != 0, false).total;
+      kvv::workspace_layout(d.item_count, d.m, 1, d.m > kvv::kSmall ? 1 : 0, d.chunk_count,
+                            (d.flags & KVV_FLAG_NEAR_ZERO) != 0, false).total;
   return KVV_OK;
 }
 
@@ -517,7 +537,8 @@ int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_te
   kvv::BatchPlan bp;
   int rc = kvv::plan_batch(count, gens, refs, policies, bp);
   if (rc) return rc;
-  *bytes = kvv::workspace_layout(bp.items, bp.samples, (int64_t)bp.table.size(), bp.chunks, bp.near, true).total;
+  *bytes = kvv::workspace_layout(bp.items, bp.samples, (int64_t)bp.table.size(), bp.nslots, bp.chunks, bp.near, true)
+               .total;
   return KVV_OK;
 }
 

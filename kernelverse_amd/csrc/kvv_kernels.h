@@ -3,19 +3,22 @@
 //   scan_kernel     one HBM pass over both tensors.  Every block owns a
 //                   contiguous range of "items" (fixed-size chunks of one
 //                   segment) and writes one partial record per run of items
-//                   of the same segment.  Inside an item, phase A handles the
-//                   bit-identical finite pairs with a handful of ops each;
-//                   the other pairs are compacted per wave into an LDS queue
-//                   and processed densely (phase B).  The next item's loads
-//                   are in flight during phase B.  The strided sample of the
-//                   reference's p99/cosine/norm-ratio is re-read from cache.
-//   reduce_kernel   one block per segment: folds its run records field by
-//                   field in a fixed order (bit-reproducible) into kvv_result.
+//                   of the same segment.  Inside an item, phase A settles the
+//                   bit-identical finite pairs with packed-integer tests on
+//                   whole dwords; the other pairs are compacted per wave into
+//                   an LDS queue and processed densely (phase B).  The next
+//                   item's loads are in flight meanwhile.  The strided sample
+//                   of the reference's p99/cosine/norm-ratio comes from the
+//                   item's LDS copy.
+//   reduce_kernel   one block per segment: folds its run records in a fixed
+//                   order (bit-reproducible) into kvv_result and clears the
+//                   select histograms, state and counters.
 //   near_kernel     tolerant-policy near-zero diagnostics: the rank-strided
 //                   sample of the compacted near-zero abs_diff array.
-//   select_kernel   exact order statistics of the sample arrays: 4 passes of
-//                   an 8-bit radix select over shared histograms.
-//   finalize_kernel the last digit, torch.quantile's lerp, the near-zero mean.
+//   select_kernel   exact order statistics of the sample arrays: 4 launches
+//                   of an 8-bit radix select over shared histograms; the last
+//                   block of each (segment, array) advances the prefix, and
+//                   after the last digit interpolates like torch.quantile.
 #pragma once
 
 #include "kvv_device.h"
@@ -23,10 +26,13 @@
 namespace kvv {
 
 constexpr int kUnroll = 4;            // 16-byte vectors per thread per item
-constexpr int kSelChunk = 4096;       // sample values per select block
+constexpr int kSelChunk = 8192;       // sample values per select block of a large group
+constexpr int kSmall = 8192;          // groups of at most this many samples are selected by one block
 constexpr int kArrays = 3;            // abs, rel, near-zero abs
-constexpr int kSelPasses = 4;
-constexpr int kHistPerSeg = kArrays * kSelPasses * 2 * 256;
+// Per (large segment, array) slot: level-0 histogram (256), level-1 and level-2
+// histograms (2 ranks x 4096 each) and the NaN count.
+constexpr int kH0 = 0, kH1 = 256, kH2 = 256 + 8192, kMisc = 256 + 16384;
+constexpr int kSlotWords = kMisc + 64;
 
 enum Layout { L_CONTIG = 0, L_ROWS = 1, L_GENERIC = 2 };
 enum ScanKind { K_CONTIG = 0, K_ROWS = 1, K_SCALAR = 2 };
@@ -69,18 +75,31 @@ struct SegDesc {
   int32_t dtype;
   int32_t item_elems;
   int32_t out_index;      // position of this pair's kvv_result in the caller's array
+  int32_t lslot;          // large-group select slot (m > kSmall), else -1
+  int32_t pad2;
   int64_t row_len;        // L_ROWS: contiguous inner length
   Dims dims;              // L_ROWS: outer dims; L_GENERIC: all dims
 };
 
-// Partial verdict of a contiguous run of items handled by one block.
+// Partial verdict of a contiguous run of items handled by one block.  Counts
+// of one run fit 32 bits (the host keeps a block's element range below 2^32).
 struct RunRec {
+  uint64_t first_mm, first_viol;
+  uint64_t gabs_i, grel_i;
+  double s[7];  // gg rr gr dd | sampled gg rr gr
+  uint32_t cnt[LC_COUNT];
+  uint32_t mismatch;
+  uint32_t mm_abs, mm_rel, gabs_k, grel_k;
+};
+
+// The same fields with 64-bit counts, for folding many runs.
+struct RunAcc {
   uint64_t cnt[LC_COUNT];
   uint64_t mismatch;
   uint64_t first_mm, first_viol;
   uint64_t gabs_i, grel_i;
   uint32_t mm_abs, mm_rel, gabs_k, grel_k;
-  double s[7];  // gg rr gr dd | sampled gg rr gr
+  double s[7];
 };
 
 struct ScanArgs {
@@ -95,6 +114,8 @@ struct ScanArgs {
   float* sample_abs;
   float* sample_rel;
   uint32_t* item_near;     // near-zero count per item (KVV_FLAG_NEAR_ZERO)
+  uint4* zero_ptr;         // select slots cleared by this launch (split over its blocks)
+  int64_t zero_n4;         // their size in 16-byte words (0: none)
 };
 
 // Per-lane accumulators.  Counts live in the per-wave LDS counters instead.
@@ -396,6 +417,49 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false); // row_bcast:15
   v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false); // row_bcast:31
   return v;
+}
+
+// Wave totals through the same DPP sweep (lane 63 ends with the sum; the tree
+// is fixed, so fp64 totals are reproducible).  No LDS round trips.
+__device__ __forceinline__ uint64_t wave_total_u64(uint64_t v) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+#define KVV_DPP_ADD64(ctrl, rm, bc)                                                       \
+  {                                                                                       \
+    const uint32_t ol = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, ctrl, rm, 0xf, bc); \
+    const uint32_t oh = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, ctrl, rm, 0xf, bc); \
+    const uint32_t sl = lo + ol;                                                          \
+    hi = hi + oh + (sl < lo ? 1u : 0u);                                                   \
+    lo = sl;                                                                              \
+  }
+  KVV_DPP_ADD64(0x111, 0xf, true)
+  KVV_DPP_ADD64(0x112, 0xf, true)
+  KVV_DPP_ADD64(0x114, 0xf, true)
+  KVV_DPP_ADD64(0x118, 0xf, true)
+  KVV_DPP_ADD64(0x142, 0xa, false)
+  KVV_DPP_ADD64(0x143, 0xc, false)
+#undef KVV_DPP_ADD64
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi, 63) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)lo, 63);
+}
+
+__device__ __forceinline__ double wave_total_f64(double v) {
+#define KVV_DPP_ADDF(ctrl, rm, bc)                                                                 \
+  {                                                                                                \
+    const uint64_t b = (uint64_t)__double_as_longlong(v);                                          \
+    const uint32_t ol = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, ctrl, rm, 0xf, bc); \
+    const uint32_t oh = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), ctrl, rm, 0xf, bc); \
+    v = v + __longlong_as_double((long long)(((uint64_t)oh << 32) | ol));                           \
+  }
+  KVV_DPP_ADDF(0x111, 0xf, true)
+  KVV_DPP_ADDF(0x112, 0xf, true)
+  KVV_DPP_ADDF(0x114, 0xf, true)
+  KVV_DPP_ADDF(0x118, 0xf, true)
+  KVV_DPP_ADDF(0x142, 0xa, false)
+  KVV_DPP_ADDF(0x143, 0xc, false)
+#undef KVV_DPP_ADDF
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  return __longlong_as_double((long long)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63) << 32) |
+                                          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63)));
 }
 
 // ------------------------------------------------------------ phase A (SWAR)
@@ -861,7 +925,7 @@ __device__ inline void flush_run(Acc& acc, uint32_t (*wcnt)[WC_COUNT], BlockScra
     for (int c = 0; c < LC_COUNT; ++c) {
       uint64_t t = 0;
       for (int i = 0; i < kWaves; ++i) t += bs.u[i][c];
-      rr.cnt[c] = t;
+      rr.cnt[c] = (uint32_t)t;
     }
     rr.mismatch = 0;
     rr.first_mm = rr.first_viol = kNone;
@@ -949,6 +1013,14 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   __shared__ typename ScanLds<DT, KIND>::type sm;
   const int tid = threadIdx.x, w = tid >> 6;
   if (tid < kWaves * WC_COUNT) (&sm.wcnt[0][0])[tid] = 0;
+  if (a.zero_n4) {
+    // the select histograms and counters of this call start at zero (the later
+    // launches accumulate into them; nothing in this kernel touches them)
+    const int64_t per = (a.zero_n4 + gridDim.x - 1) / gridDim.x;
+    const int64_t z0 = (int64_t)blockIdx.x * per;
+    const int64_t z1 = z0 + per < a.zero_n4 ? z0 + per : a.zero_n4;
+    for (int64_t i = z0 + tid; i < z1; i += kBlock) a.zero_ptr[i] = make_uint4(0, 0, 0, 0);
+  }
   const int64_t i0 = a.item_lo + (int64_t)blockIdx.x * a.items_per_block;
   int64_t i1 = i0 + a.items_per_block;
   if (i1 > a.item_lo + a.items) i1 = a.item_lo + a.items;
@@ -1020,90 +1092,7 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   flush_run(acc, sm.wcnt, sm.bs, &a.runs[run_start]);
 }
 
-// ------------------------------------------------------------ reduce kernel
-struct ReduceArgs {
-  SegDesc seg0;
-  const SegDesc* table;
-  const RunRec* runs;
-  kvv_result* out;
-  uint32_t* hist;        // kHistPerSeg per segment
-  uint32_t* nan_cnt;     // kArrays per segment
-  uint32_t* sel_state;   // kSelStatePerSeg per segment
-  const uint32_t* item_near;
-  uint64_t* item_near_off;
-};
-
-constexpr int kReduceBlock = 1024;
-constexpr int kFields = LC_COUNT + 14;
-constexpr int kSelStatePerSeg = kArrays * (kSelPasses + 1) * 2 * 4;
-
-struct FieldAcc {
-  uint64_t u;
-  uint32_t k;
-  double x;
-};
-
-__device__ __forceinline__ void field_init(int f, FieldAcc& a) {
-  a.k = 0;
-  a.x = 0.0;
-  a.u = (f == LC_COUNT + 1 || f == LC_COUNT + 2 || f == LC_COUNT + 5 || f == LC_COUNT + 6) ? kNone : 0;
-}
-
-// Field f of a run record: counts add, first indices take the minimum, keys the
-// maximum, (key, index) pairs the argmax, fp64 sums add.
-__device__ __forceinline__ void field_load(int f, const RunRec& r, FieldAcc& v) {
-  v.k = 0;
-  v.x = 0.0;
-  v.u = 0;
-  if (f < LC_COUNT) {
-    v.u = r.cnt[f];
-    return;
-  }
-  switch (f - LC_COUNT) {
-    case 0: v.u = r.mismatch; break;
-    case 1: v.u = r.first_mm; break;
-    case 2: v.u = r.first_viol; break;
-    case 3: v.k = r.mm_abs; break;
-    case 4: v.k = r.mm_rel; break;
-    case 5: v.k = r.gabs_k; v.u = r.gabs_i; break;
-    case 6: v.k = r.grel_k; v.u = r.grel_i; break;
-    default: v.x = r.s[f - LC_COUNT - 7]; break;
-  }
-}
-
-__device__ __forceinline__ void field_merge(int f, FieldAcc& a, const FieldAcc& v) {
-  const int g = f - LC_COUNT;
-  if (f < LC_COUNT || g == 0) {
-    a.u += v.u;
-  } else if (g == 1 || g == 2) {
-    a.u = v.u < a.u ? v.u : a.u;
-  } else if (g == 3 || g == 4) {
-    a.k = v.k > a.k ? v.k : a.k;
-  } else if (g == 5 || g == 6) {
-    if (better(v.k, v.u, a.k, a.u)) {
-      a.k = v.k;
-      a.u = v.u;
-    }
-  } else {
-    a.x += v.x;
-  }
-}
-
-__device__ __forceinline__ void field_wave_reduce(int f, FieldAcc& a) {
-  const int g = f - LC_COUNT;
-  if (f < LC_COUNT || g == 0) {
-    a.u = wave_sum(a.u);
-  } else if (g == 1 || g == 2) {
-    a.u = wave_min(a.u);
-  } else if (g == 3 || g == 4) {
-    a.k = wave_max(a.k);
-  } else if (g == 5 || g == 6) {
-    wave_argmax(a.k, a.u);
-  } else {
-    a.x = wave_sum(a.x);
-  }
-}
-
+// ------------------------------------------------------------ run records
 __device__ __forceinline__ double clamp_cos(double c) {
   if (c != c) return c;
   return c < -1.0 ? -1.0 : (c > 1.0 ? 1.0 : c);
@@ -1123,144 +1112,54 @@ __device__ __forceinline__ int64_t run_item(const SegDesc& d, int64_t j, int64_t
   return j == 0 ? d.item_begin : d.run_base + (b_first + j - 1) * d.run_ipb;
 }
 
-// One block per segment: folds the segment's run records field by field
-// (16 waves, one field per wave at a time; each lane loads a batch of runs up front).
-#ifdef KVV_COMMON_KERNELS
-__global__ __launch_bounds__(kReduceBlock) void reduce_kernel(ReduceArgs a) {
-  constexpr int kW = kReduceBlock / 64;
-  constexpr int kBatch = 8;
-  __shared__ FieldAcc fres[kFields];
-  __shared__ uint64_t wsum[kW];
-  const int seg = blockIdx.x;
-  const SegDesc& d = a.table ? a.table[seg] : a.seg0;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  for (int i = tid; i < kHistPerSeg; i += kReduceBlock) a.hist[(size_t)seg * kHistPerSeg + i] = 0;
-  if (tid < kArrays) a.nan_cnt[seg * kArrays + tid] = 0;
-  if (tid < kSelStatePerSeg) a.sel_state[(size_t)seg * kSelStatePerSeg + tid] = 0;
-  // runs of this segment: its first item plus the block starts strictly inside it
-  int64_t nruns = 0, b_first = 0;
-  if (d.item_count > 0) {
-    const int64_t rel0 = d.item_begin - d.run_base;                    // >= 0
-    b_first = rel0 / d.run_ipb + 1;                                     // first block start after item_begin
-    const int64_t rel_end = d.item_begin + d.item_count - d.run_base;  // exclusive
-    const int64_t b_end = (rel_end + d.run_ipb - 1) / d.run_ipb;       // block starts < rel_end
-    nruns = 1 + (b_end > b_first ? b_end - b_first : 0);
-  }
-  for (int f = w; f < kFields; f += kW) {
-    FieldAcc fa;
-    field_init(f, fa);
-    for (int64_t base = 0; base < nruns; base += 64 * kBatch) {
-      FieldAcc v[kBatch];
+// Merge of two partial verdicts: counts add, first indices take the minimum,
+// keys the maximum, (key, index) pairs the argmax, fp64 sums add.
+__device__ __forceinline__ void run_init(RunAcc& r) {
 #pragma unroll
-      for (int q = 0; q < kBatch; ++q) {
-        const int64_t j = base + q * 64 + lane;
-        if (j < nruns) {
-          field_load(f, a.runs[run_item(d, j, b_first)], v[q]);
-        } else {
-          field_init(f, v[q]);
-        }
-      }
+  for (int c = 0; c < LC_COUNT; ++c) r.cnt[c] = 0;
+  r.mismatch = 0;
+  r.first_mm = r.first_viol = kNone;
+  r.gabs_i = r.grel_i = kNone;
+  r.mm_abs = r.mm_rel = r.gabs_k = r.grel_k = 0;
 #pragma unroll
-      for (int q = 0; q < kBatch; ++q) field_merge(f, fa, v[q]);
-    }
-    field_wave_reduce(f, fa);
-    if (lane == 0) fres[f] = fa;
-  }
-  // near-zero: exclusive prefix of the per-item counts, in item order
-  if (d.flags & KVV_FLAG_NEAR_ZERO) {
-    const int64_t per = (d.item_count + kReduceBlock - 1) / kReduceBlock;
-    const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
-    const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
-    uint64_t mine = 0;
-    for (int64_t k = k0; k < k1; ++k) mine += a.item_near[d.item_begin + k];
-    uint64_t incl = mine;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t v = __shfl_up(incl, o);
-      if (lane >= o) incl += v;
-    }
-    if (lane == 63) wsum[w] = incl;
-    __syncthreads();
-    uint64_t base = 0;
-    for (int i = 0; i < w; ++i) base += wsum[i];
-    uint64_t run = base + incl - mine;
-    for (int64_t k = k0; k < k1; ++k) {
-      a.item_near_off[d.item_begin + k] = run;
-      run += a.item_near[d.item_begin + k];
-    }
-  }
-  __syncthreads();
-  if (tid != 0) return;
-  RunRec r;
-  for (int c = 0; c < LC_COUNT; ++c) r.cnt[c] = fres[c].u;
-  r.mismatch = fres[LC_COUNT + 0].u;
-  r.first_mm = fres[LC_COUNT + 1].u;
-  r.first_viol = fres[LC_COUNT + 2].u;
-  r.mm_abs = fres[LC_COUNT + 3].k;
-  r.mm_rel = fres[LC_COUNT + 4].k;
-  r.gabs_k = fres[LC_COUNT + 5].k;
-  r.gabs_i = fres[LC_COUNT + 5].u;
-  r.grel_k = fres[LC_COUNT + 6].k;
-  r.grel_i = fres[LC_COUNT + 6].u;
-  for (int i = 0; i < 7; ++i) r.s[i] = fres[LC_COUNT + 7 + i].x;
-  kvv_result o;
-  __builtin_memset(&o, 0, sizeof(o));
-  o.numel = d.n;
-  o.mismatch_count = (int64_t)r.mismatch;
-  o.first_mismatch_index = r.first_mm == kNone ? -1 : (int64_t)r.first_mm;
-  const bool imode = d.mode == KVV_MODE_MAX_ABS_DIFF;
-  if (r.mismatch) {
-    o.mismatch_max_abs = imode ? (double)ikey_value(r.mm_abs) : (double)fkey_value(r.mm_abs);
-    o.mismatch_max_rel = (double)fkey_value(r.mm_rel);
-  }
-  o.sample_count = d.m;
-  o.sample_sum_gg = r.s[4];
-  o.sample_sum_rr = r.s[5];
-  o.sample_sum_gr = r.s[6];
-  o.sample_cosine = cosine_of(r.s[6], r.s[4], r.s[5]);
-  {
-    const double gn = sqrt(r.s[4]), rn = sqrt(r.s[5]);
-    o.sample_norm_ratio = (gn == 0.0 && rn == 0.0) ? 1.0 : (gn == 0.0 ? 0.0 : (rn == 0.0 ? __builtin_inf() : gn / rn));
-  }
-  o.finite_violations = (int64_t)r.cnt[LC_VIOL];
-  o.first_finite_violation = r.first_viol == kNone ? -1 : (int64_t)r.first_viol;
-  o.nan_gen = (int64_t)r.cnt[LC_NAN_G];
-  o.nan_ref = (int64_t)r.cnt[LC_NAN_R];
-  o.posinf_gen = (int64_t)r.cnt[LC_PINF_G];
-  o.posinf_ref = (int64_t)r.cnt[LC_PINF_R];
-  o.neginf_gen = (int64_t)r.cnt[LC_NINF_G];
-  o.neginf_ref = (int64_t)r.cnt[LC_NINF_R];
-  o.near_zero_count = (int64_t)r.cnt[LC_NEAR];
-  o.far_count = d.n - (int64_t)r.cnt[LC_NEAR];
-  o.far_mismatch_count = (int64_t)r.cnt[LC_FARMM];
-  o.near_zero_bad_count = (int64_t)r.cnt[LC_NEARBAD];
-  {
-    const int64_t c = o.near_zero_count;
-    o.near_zero_sample_count = c < d.max_samples ? c : d.max_samples;
-  }
-  if (d.n > 0) {
-    o.max_abs = imode ? (double)ikey_value(r.gabs_k) : (double)fkey_value(r.gabs_k);
-    o.max_abs_index = (int64_t)r.gabs_i;
-    o.max_rel = (double)fkey_value(r.grel_k);
-    o.max_rel_index = (int64_t)r.grel_i;
-  } else {
-    o.max_abs_index = o.max_rel_index = -1;
-  }
-  for (int b = 0; b < kBuckets; ++b) o.ulp_hist[b] = r.cnt[LC_HIST0 + b];
-  o.nan_pairs = (int64_t)r.cnt[LC_NANPAIR];
-  o.sum_gg = r.s[0];
-  o.sum_rr = r.s[1];
-  o.sum_gr = r.s[2];
-  o.sum_dd = r.s[3];
-  {
-    const double dn = sqrt(r.s[3]), rn = sqrt(r.s[1]);
-    o.rel_l2 = rn == 0.0 ? (dn == 0.0 ? 0.0 : __builtin_inf()) : dn / rn;
-  }
-  o.cosine = cosine_of(r.s[2], r.s[0], r.s[1]);
-  o.p99_abs = o.p99_rel = __builtin_nan("");
-  o.near_zero_p99_abs = o.near_zero_mean_abs = __builtin_nan("");
-  a.out[d.out_index] = o;
+  for (int i = 0; i < 7; ++i) r.s[i] = 0.0;
 }
-#endif  // KVV_COMMON_KERNELS
+
+template <typename R>
+__device__ __forceinline__ void run_merge(RunAcc& a, const R& v) {
+#pragma unroll
+  for (int c = 0; c < LC_COUNT; ++c) a.cnt[c] += v.cnt[c];
+  a.mismatch += v.mismatch;
+  a.first_mm = v.first_mm < a.first_mm ? v.first_mm : a.first_mm;
+  a.first_viol = v.first_viol < a.first_viol ? v.first_viol : a.first_viol;
+  a.mm_abs = v.mm_abs > a.mm_abs ? v.mm_abs : a.mm_abs;
+  a.mm_rel = v.mm_rel > a.mm_rel ? v.mm_rel : a.mm_rel;
+  if (better(v.gabs_k, v.gabs_i, a.gabs_k, a.gabs_i)) {
+    a.gabs_k = v.gabs_k;
+    a.gabs_i = v.gabs_i;
+  }
+  if (better(v.grel_k, v.grel_i, a.grel_k, a.grel_i)) {
+    a.grel_k = v.grel_k;
+    a.grel_i = v.grel_i;
+  }
+#pragma unroll
+  for (int i = 0; i < 7; ++i) a.s[i] += v.s[i];
+}
+
+// Fixed-order fold of a RunAcc over the 64 lanes of a wave (result in every lane).
+__device__ __forceinline__ void run_wave_reduce(RunAcc& r) {
+#pragma unroll
+  for (int c = 0; c < LC_COUNT; ++c) r.cnt[c] = wave_total_u64(r.cnt[c]);
+  r.mismatch = wave_total_u64(r.mismatch);
+  r.first_mm = wave_min(r.first_mm);
+  r.first_viol = wave_min(r.first_viol);
+  r.mm_abs = wave_max(r.mm_abs);
+  r.mm_rel = wave_max(r.mm_rel);
+  wave_argmax(r.gabs_k, r.gabs_i);
+  wave_argmax(r.grel_k, r.grel_i);
+#pragma unroll
+  for (int i = 0; i < 7; ++i) r.s[i] = wave_total_f64(r.s[i]);
+}
 
 // ------------------------------------------------------------ near-zero sample
 // GCR:525-529 compacts abs_diff over |ref| <= near_zero_abs in row-major order
@@ -1365,224 +1264,6 @@ __global__ __launch_bounds__(kBlock) void near_kernel(NearArgs a) {
   }
 }
 
-// ------------------------------------------------------------ order statistics
-// Selection state per (segment, array, pass, rank): the high bits fixed so far
-// and the residual rank, stored as 4 words {prefix, resid_lo, resid_hi, pad}.
-struct SelectArgs {
-  SegDesc seg0;
-  const SegDesc* table;
-  const int64_t* chunk_seg;   // batch: owning segment of each chunk
-  int32_t nseg;
-  int32_t narrays;            // 2, or 3 with near-zero
-  int64_t total_chunks;       // chunks per array over all segments
-  const kvv_result* res;
-  const float* arr[kArrays];
-  uint32_t* hist;
-  uint32_t* nan_cnt;
-  uint32_t* sel_state;
-  int32_t pass;
-  int32_t pad;
-};
-
-__device__ __forceinline__ int64_t group_count(const SegDesc& d, const kvv_result& r, int arr) {
-  return arr < 2 ? d.m : r.near_zero_sample_count;
-}
-
-// torch.quantile(q=0.99) ranks: rank = f32(0.99) * f32(m-1) rounded to float32;
-// lower = trunc(rank), upper = ceil(rank).
-__device__ __forceinline__ void q99_ranks(int64_t m, uint64_t& lo, uint64_t& hi, float& w) {
-  const float rank = 0.99f * (float)(m - 1);
-  lo = (uint64_t)rank;
-  hi = (uint64_t)ceilf(rank);
-  w = rank - (float)lo;
-}
-
-// Block-cooperative search (kBlock == 256 threads, one per bin): the bin of a
-// 256-bin histogram that holds 0-based rank `resid`, and how many values lie in
-// lower bins.  A rank past the end (only when NaNs were left out) gives bin 255.
-__device__ inline void block_find_bin(const uint32_t* h, uint64_t resid, uint32_t& bin, uint64_t& below, uint64_t* sh) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const uint64_t c = h[tid];
-  uint64_t incl = c;
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint64_t v = __shfl_up(incl, o);
-    if (lane >= o) incl += v;
-  }
-  __syncthreads();
-  if (lane == 63) sh[w] = incl;
-  if (tid == 0) {
-    sh[kWaves] = 255;
-    sh[kWaves + 1] = 0;
-  }
-  __syncthreads();
-  uint64_t base = 0;
-  for (int i = 0; i < w; ++i) base += sh[i];
-  incl += base;
-  const uint64_t excl = incl - c;
-  if (c > 0 && excl <= resid && resid < incl) {
-    sh[kWaves] = (uint64_t)tid;
-    sh[kWaves + 1] = excl;
-  }
-  __syncthreads();
-  bin = (uint32_t)sh[kWaves];
-  below = sh[kWaves + 1];
-}
-
-__device__ __forceinline__ uint32_t* sel_state_at(uint32_t* st, int s, int arr, int pass, int rr) {
-  return st + (size_t)s * kSelStatePerSeg + ((arr * (kSelPasses + 1) + pass) * 2 + rr) * 4;
-}
-
-// State after `pass` digits for both ranks: from the stored state after
-// pass-1 digits and that pass's histogram (pass 0: prefix 0, resid = rank).
-__device__ inline void select_state(uint32_t* st, const uint32_t* h, int s, int arr, int pass, const uint64_t rank[2],
-                             uint32_t prefix[2], uint64_t resid[2], uint64_t* sh) {
-  for (int rr = 0; rr < 2; ++rr) {
-    if (pass == 0) {
-      prefix[rr] = 0;
-      resid[rr] = rank[rr];
-      continue;
-    }
-    const uint32_t* prev = sel_state_at(st, s, arr, pass - 1, rr);
-    const uint32_t pp = prev[0];
-    const uint64_t pr = (uint64_t)prev[1] | ((uint64_t)prev[2] << 32);
-    uint32_t bin;
-    uint64_t below;
-    block_find_bin(h + ((pass - 1) * 2 + rr) * 256, pr, bin, below, sh);
-    prefix[rr] = (pp << 8) | bin;
-    resid[rr] = pr - below;
-  }
-}
-
-#ifdef KVV_COMMON_KERNELS
-__global__ __launch_bounds__(kBlock) void select_kernel(SelectArgs a) {
-  __shared__ uint32_t lh[2][256];
-  __shared__ uint64_t sh[kWaves + 2];
-  __shared__ uint32_t s_nan;
-  const int tid = threadIdx.x;
-  const int64_t gb = blockIdx.x;
-  const int arr = (int)(gb / a.total_chunks);
-  const int64_t chunk = gb - (int64_t)arr * a.total_chunks;
-  const int s = a.table ? (int)a.chunk_seg[chunk] : 0;
-  const SegDesc& d = a.table ? a.table[s] : a.seg0;
-  const int64_t count = group_count(d, a.res[d.out_index], arr);
-  const int64_t c0 = (chunk - d.chunk_begin) * (int64_t)kSelChunk;
-  if (c0 >= count) return;
-  const int64_t c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
-  uint32_t* h = a.hist + (size_t)s * kHistPerSeg + (size_t)arr * (kSelPasses * 2 * 256);
-  const int pass = a.pass;
-  uint64_t rank[2], resid[2];
-  uint32_t prefix[2];
-  float wgt;
-  q99_ranks(count, rank[0], rank[1], wgt);
-  select_state(a.sel_state, h, s, arr, pass, rank, prefix, resid, sh);
-  if (c0 == 0 && tid < 2) {
-    uint32_t* dst = sel_state_at(a.sel_state, s, arr, pass, tid);
-    dst[0] = prefix[tid];
-    dst[1] = (uint32_t)resid[tid];
-    dst[2] = (uint32_t)(resid[tid] >> 32);
-  }
-  for (int i = tid; i < 512; i += kBlock) (&lh[0][0])[i] = 0;
-  if (tid == 0) s_nan = 0;
-  __syncthreads();
-  const uint32_t p0 = prefix[0], p1 = prefix[1];
-  const int shift = 24 - 8 * pass;
-  const float* v = a.arr[arr] + d.sample_off;
-  uint32_t nans = 0;
-  constexpr int kPer = kSelChunk / kBlock;
-  float x[kPer];
-  // all loads first (independent), then the histogram updates
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int64_t i = c0 + (int64_t)j * kBlock + tid;
-    x[j] = i < c1 ? v[i] : 0.0f;
-  }
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int64_t i = c0 + (int64_t)j * kBlock + tid;
-    if (i >= c1) continue;
-    if (__builtin_isnan(x[j])) {
-      ++nans;
-      continue;
-    }
-    const uint32_t k = fkey(x[j]);
-    const uint32_t dig = (k >> shift) & 255u;
-    const uint32_t top = pass == 0 ? 0u : (k >> (shift + 8));
-    if (top == p0) atomicAdd(&lh[0][dig], 1u);
-    if (top == p1) atomicAdd(&lh[1][dig], 1u);
-  }
-  if (pass == 0) {
-    nans = wave_sum(nans);
-    if ((tid & 63) == 0 && nans) atomicAdd(&s_nan, nans);
-  }
-  __syncthreads();
-  uint32_t* hp = h + pass * 2 * 256;
-  for (int i = tid; i < 512; i += kBlock) {
-    const uint32_t c = (&lh[0][0])[i];
-    if (c) atomicAdd(&hp[i], c);
-  }
-  if (pass == 0 && tid == 0 && s_nan) atomicAdd(&a.nan_cnt[s * kArrays + arr], s_nan);
-}
-#endif  // KVV_COMMON_KERNELS
-
-struct FinalArgs {
-  SegDesc seg0;
-  const SegDesc* table;
-  int32_t narrays;
-  int32_t pad;
-  kvv_result* res;
-  const uint32_t* hist;
-  const uint32_t* nan_cnt;
-  uint32_t* sel_state;
-  const double* item_near_sum;
-};
-
-// One block per (segment, array): the last digit of both order statistics,
-// torch.quantile's interpolation, and (near-zero array) the sample mean.
-#ifdef KVV_COMMON_KERNELS
-__global__ __launch_bounds__(kBlock) void finalize_kernel(FinalArgs a) {
-  __shared__ uint64_t sh[kWaves + 2];
-  __shared__ double part[kBlock];
-  const int s = blockIdx.x / a.narrays;
-  const int arr = blockIdx.x % a.narrays;
-  const SegDesc& d = a.table ? a.table[s] : a.seg0;
-  const int tid = threadIdx.x;
-  kvv_result& r = a.res[d.out_index];
-  const int64_t count = group_count(d, r, arr);
-  double out = __builtin_nan("");
-  if (count > 0 && a.nan_cnt[s * kArrays + arr] == 0) {
-    const uint32_t* h = a.hist + (size_t)s * kHistPerSeg + (size_t)arr * (kSelPasses * 2 * 256);
-    uint64_t rank[2], resid[2];
-    uint32_t key[2];
-    float w;
-    q99_ranks(count, rank[0], rank[1], w);
-    select_state(a.sel_state, h, s, arr, kSelPasses, rank, key, resid, sh);
-    const float va = fkey_value(key[0]), vb = fkey_value(key[1]);
-    // torch's lerp: small weights from the lower end, large ones from the upper end, one rounding each
-    const float diff = vb - va;
-    const float q = fabsf(w) < 0.5f ? fmaf(w, diff, va) : fmaf(w - 1.0f, diff, vb);
-    out = (double)q;
-  }
-  if (tid == 0) {
-    if (arr == 0) r.p99_abs = out;
-    if (arr == 1) r.p99_rel = out;
-    if (arr == 2) r.near_zero_p99_abs = out;
-  }
-  if (arr == 2 && count > 0) {
-    // fixed-order sum of the per-item sampled sums: contiguous chunks, then chunks in order
-    const int64_t per = (d.item_count + kBlock - 1) / kBlock;
-    const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
-    const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
-    double t = 0.0;
-    for (int64_t k = k0; k < k1; ++k) t += a.item_near_sum[d.item_begin + k];
-    part[tid] = t;
-    __syncthreads();
-    if (tid == 0) {
-      double sum = 0.0;
-      for (int i = 0; i < kBlock; ++i) sum += part[i];
-      r.near_zero_mean_abs = (double)(float)(sum / (double)count);
-    }
-  }
-}
-#endif  // KVV_COMMON_KERNELS
+#include "kvv_tail.h"
 
 }  // namespace kvv
