@@ -214,14 +214,22 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
 
 // ------------------------------------------------------------ workspace
 struct WsLayout {
-  size_t runs, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample, table,
+  int64_t run_stride;
+  size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample, table,
       chunk_seg, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-WsLayout workspace_layout(int64_t items, int64_t samples, int64_t nseg, int64_t nslots, int64_t chunks, bool near,
-                          bool batch) {
+// Run slots a segment may need: one per block range it meets, at most one per
+// item and at most one per block of a launch (the grid is capped at 4096).
+int64_t run_slot_bound(int64_t item_count) {
+  const int64_t b = item_count < 4096 ? item_count : 4096;
+  return (b + 3) & ~int64_t(3);
+}
+
+WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int64_t nslots, int64_t chunks,
+                          int64_t items, bool near, bool batch) {
   WsLayout L{};
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -229,7 +237,9 @@ WsLayout workspace_layout(int64_t items, int64_t samples, int64_t nseg, int64_t 
     off += align256(bytes);
     return at;
   };
-  L.runs = take((size_t)items * sizeof(RunRec));
+  L.run_stride = run_slots;
+  L.runs_u32 = take((size_t)run_slots * kColU32 * 4);
+  L.runs_u64 = take((size_t)run_slots * kColU64 * 8);
   L.sample_abs = take((size_t)samples * 4);
   L.sample_rel = take((size_t)samples * 4);
   L.slot_bytes = (size_t)nslots * kArrays * kSlotWords * 4;
@@ -251,6 +261,10 @@ WsLayout workspace_layout(int64_t items, int64_t samples, int64_t nseg, int64_t 
 template <typename T>
 T* at(void* ws, size_t off) {
   return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
+}
+
+RunCols run_cols(const WsLayout& L, void* ws) {
+  return RunCols{at<uint32_t>(ws, L.runs_u32), at<uint64_t>(ws, L.runs_u64), L.run_stride};
 }
 
 int check_ws(const WsLayout& L, void* ws, size_t ws_bytes, kvv_result* out) {
@@ -283,7 +297,8 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   t.nseg = nseg;
   t.total_chunks = total_chunks > 0 ? total_chunks : 1;
   t.res = out;
-  t.runs = at<RunRec>(ws, L.runs);
+  t.runs = run_cols(L, ws);
+  t.reduce_roles = near ? 6 : 5;
   t.arr[0] = at<float>(ws, L.sample_abs);
   t.arr[1] = at<float>(ws, L.sample_rel);
   t.arr[2] = near ? at<float>(ws, L.near_sample) : nullptr;
@@ -306,7 +321,7 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
     KVV_HIP(hipGetLastError());
     return KVV_OK;
   };
-  int rc = launch(nseg, 0, 0, 2);
+  int rc = launch(nseg * t.reduce_roles, 0, 0, 2);
   if (rc) return rc;
   if (near) {
     for (const auto& nl : nears) {
@@ -351,7 +366,9 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   d.lslot = d.m > kSmall ? 0 : -1;
   const int64_t nslots = d.lslot >= 0 ? 1 : 0;
   const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
-  const WsLayout L = workspace_layout(d.item_count, d.m, 1, nslots, d.chunk_count, near, false);
+  d.run_slot0 = 0;
+  const WsLayout L = workspace_layout(run_slot_bound(d.item_count), d.m, 1, nslots, d.chunk_count, d.item_count, near,
+                                      false);
   int rc = check_ws(L, ws, ws_bytes, out);
   if (rc) return rc;
   const int kind = scan_kind(d);
@@ -370,7 +387,7 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     a.item_lo = 0;
     a.items = d.item_count;
     a.items_per_block = d.run_ipb;
-    a.runs = at<RunRec>(ws, L.runs);
+    a.runs = run_cols(L, ws);
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);
     a.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
@@ -396,7 +413,7 @@ struct BatchPlan {
     int64_t item_lo, items, ipb;
   };
   std::vector<Group> groups;
-  int64_t items = 0, samples = 0, chunks = 0, nslots = 0;
+  int64_t items = 0, samples = 0, chunks = 0, nslots = 0, run_slots = 0;
   bool near = false;
 };
 
@@ -422,6 +439,8 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     d.sample_off = sample;
     d.chunk_begin = chunk;
     d.lslot = d.m > kSmall ? (int32_t)bp.nslots++ : -1;
+    d.run_slot0 = bp.run_slots;
+    bp.run_slots += run_slot_bound(d.item_count);
     const int s = (int)bp.table.size();
     for (int64_t c = 0; c < d.chunk_count; ++c) bp.chunk_seg.push_back((int64_t)s);
     item += d.item_count;
@@ -456,7 +475,8 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
 int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st) {
   const int nseg = (int)bp.table.size();
   if (nseg == 0) return KVV_OK;
-  const WsLayout L = workspace_layout(bp.items, bp.samples, nseg, bp.nslots, bp.chunks, bp.near, true);
+  const WsLayout L =
+      workspace_layout(bp.run_slots, bp.samples, nseg, bp.nslots, bp.chunks, bp.items, bp.near, true);
   int rc = check_ws(L, ws, ws_bytes, out);
   if (rc) return rc;
   SegDesc* dtable = at<SegDesc>(ws, L.table);
@@ -476,7 +496,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     a.item_lo = gr.item_lo;
     a.items = gr.items;
     a.items_per_block = gr.ipb;
-    a.runs = at<RunRec>(ws, L.runs);
+    a.runs = run_cols(L, ws);
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);
     a.item_near = bp.near ? at<uint32_t>(ws, L.item_near) : nullptr;
@@ -509,8 +529,9 @@ int kvv_workspace_size(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_p
   int rc = kvv::plan_segment(gen, ref, policy, d);
   if (rc) return rc;
   *bytes =
-      kvv::workspace_layout(d.item_count, d.m, 1, d.m > kvv::kSmall ? 1 : 0, d.chunk_count,
-                            (d.flags & KVV_FLAG_NEAR_ZERO) != 0, false).total;
+      kvv::workspace_layout(kvv::run_slot_bound(d.item_count), d.m, 1, d.m > kvv::kSmall ? 1 : 0, d.chunk_count,
+                            d.item_count, (d.flags & KVV_FLAG_NEAR_ZERO) != 0, false)
+          .total;
   return KVV_OK;
 }
 
@@ -537,7 +558,8 @@ int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_te
   kvv::BatchPlan bp;
   int rc = kvv::plan_batch(count, gens, refs, policies, bp);
   if (rc) return rc;
-  *bytes = kvv::workspace_layout(bp.items, bp.samples, (int64_t)bp.table.size(), bp.nslots, bp.chunks, bp.near, true)
+  *bytes = kvv::workspace_layout(bp.run_slots, bp.samples, (int64_t)bp.table.size(), bp.nslots, bp.chunks, bp.items,
+                                 bp.near, true)
                .total;
   return KVV_OK;
 }

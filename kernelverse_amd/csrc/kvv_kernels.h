@@ -77,29 +77,21 @@ struct SegDesc {
   int32_t out_index;      // position of this pair's kvv_result in the caller's array
   int32_t lslot;          // large-group select slot (m > kSmall), else -1
   int32_t pad2;
+  int64_t run_slot0;      // first run slot of this segment (a multiple of 4)
   int64_t row_len;        // L_ROWS: contiguous inner length
   Dims dims;              // L_ROWS: outer dims; L_GENERIC: all dims
 };
 
-// Partial verdict of a contiguous run of items handled by one block.  Counts
-// of one run fit 32 bits (the host keeps a block's element range below 2^32).
-struct RunRec {
-  uint64_t first_mm, first_viol;
-  uint64_t gabs_i, grel_i;
-  double s[7];  // gg rr gr dd | sampled gg rr gr
-  uint32_t cnt[LC_COUNT];
-  uint32_t mismatch;
-  uint32_t mm_abs, mm_rel, gabs_k, grel_k;
-};
-
-// The same fields with 64-bit counts, for folding many runs.
-struct RunAcc {
-  uint64_t cnt[LC_COUNT];
-  uint64_t mismatch;
-  uint64_t first_mm, first_viol;
-  uint64_t gabs_i, grel_i;
-  uint32_t mm_abs, mm_rel, gabs_k, grel_k;
-  double s[7];
+// Partial verdict of a contiguous run of items handled by one block, stored
+// field-major ("columns") at a dense run slot: column c of slot k is at
+// u32[c * stride + k] or u64[c * stride + k].  Counts of one run fit 32 bits
+// (the host keeps a block's element range below 2^32).
+enum RunColU32 { CU_MISM = LC_COUNT, CU_MMABS, CU_MMREL, CU_GABSK, CU_GRELK, kColU32 };
+enum RunColU64 { CL_FIRSTMM = 0, CL_FIRSTVIOL, CL_GABSI, CL_GRELI, CL_S0, kColU64 = CL_S0 + 7 };
+struct RunCols {
+  uint32_t* u32;
+  uint64_t* u64;
+  int64_t stride;  // slots per column (a multiple of 4)
 };
 
 struct ScanArgs {
@@ -110,7 +102,7 @@ struct ScanArgs {
   int64_t item_lo;         // items of this launch: [item_lo, item_lo + items)
   int64_t items;
   int64_t items_per_block;
-  RunRec* runs;            // indexed by global item (written where a run starts)
+  RunCols runs;            // one slot per run (see run_slot)
   float* sample_abs;
   float* sample_rel;
   uint32_t* item_near;     // near-zero count per item (KVV_FLAG_NEAR_ZERO)
@@ -874,9 +866,18 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
   return t;
 }
 
-// Reduces the block's accumulators and wave counters into one RunRec (written
-// by thread 0 at *out) and resets them for the next run.
-__device__ inline void flush_run(Acc& acc, uint32_t (*wcnt)[WC_COUNT], BlockScratch& bs, RunRec* out) {
+// Run slot of the run that starts at item `it` of segment d: runs start at the
+// segment's first item and at every block-range start inside it.
+__device__ __forceinline__ int64_t run_slot(const SegDesc& d, int64_t it) {
+  if (it == d.item_begin) return d.run_slot0;
+  const int64_t b_first = (d.item_begin - d.run_base) / d.run_ipb + 1;
+  return d.run_slot0 + (it - d.run_base) / d.run_ipb - b_first + 1;
+}
+
+// Reduces the block's accumulators and wave counters into the run's columns
+// (one thread per column, waves in order) and resets them for the next run.
+__device__ inline void flush_run(Acc& acc, uint32_t (*wcnt)[WC_COUNT], BlockScratch& bs, const RunCols& out,
+                                 int64_t slot) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __syncthreads();
   const uint64_t nfast = wave_sum((uint64_t)acc.nfast);
@@ -920,36 +921,46 @@ __device__ inline void flush_run(Acc& acc, uint32_t (*wcnt)[WC_COUNT], BlockScra
     for (int i = 0; i < 7; ++i) bs.s[w][i] = s[i];
   }
   __syncthreads();
-  if (tid == 0) {
-    RunRec rr;
-    for (int c = 0; c < LC_COUNT; ++c) {
+  if (tid < kColU32) {
+    if (tid < CU_GABSK) {
       uint64_t t = 0;
-      for (int i = 0; i < kWaves; ++i) t += bs.u[i][c];
-      rr.cnt[c] = (uint32_t)t;
-    }
-    rr.mismatch = 0;
-    rr.first_mm = rr.first_viol = kNone;
-    rr.mm_abs = rr.mm_rel = 0;
-    rr.gabs_k = rr.grel_k = 0;
-    rr.gabs_i = rr.grel_i = kNone;
-    for (int i = 0; i < 7; ++i) rr.s[i] = 0.0;
-    for (int i = 0; i < kWaves; ++i) {
-      rr.mismatch += bs.u[i][LC_COUNT + 0];
-      rr.first_mm = bs.u[i][LC_COUNT + 1] < rr.first_mm ? bs.u[i][LC_COUNT + 1] : rr.first_mm;
-      rr.first_viol = bs.u[i][LC_COUNT + 2] < rr.first_viol ? bs.u[i][LC_COUNT + 2] : rr.first_viol;
-      rr.mm_abs = bs.k[i][0] > rr.mm_abs ? bs.k[i][0] : rr.mm_abs;
-      rr.mm_rel = bs.k[i][1] > rr.mm_rel ? bs.k[i][1] : rr.mm_rel;
-      if (better(bs.k[i][2], bs.u[i][LC_COUNT + 3], rr.gabs_k, rr.gabs_i)) {
-        rr.gabs_k = bs.k[i][2];
-        rr.gabs_i = bs.u[i][LC_COUNT + 3];
+      if (tid <= CU_MISM) {
+        const int src = tid < LC_COUNT ? tid : LC_COUNT + 0;
+        for (int i = 0; i < kWaves; ++i) t += bs.u[i][src];
+      } else {
+        for (int i = 0; i < kWaves; ++i) {
+          const uint64_t k = bs.k[i][tid - CU_MMABS];
+          t = k > t ? k : t;
+        }
       }
-      if (better(bs.k[i][3], bs.u[i][LC_COUNT + 4], rr.grel_k, rr.grel_i)) {
-        rr.grel_k = bs.k[i][3];
-        rr.grel_i = bs.u[i][LC_COUNT + 4];
-      }
-      for (int j = 0; j < 7; ++j) rr.s[j] += bs.s[i][j];
+      out.u32[tid * out.stride + slot] = (uint32_t)t;
     }
-    *out = rr;
+  } else if (tid >= 64 && tid < 64 + kColU64) {
+    const int c = tid - 64;
+    if (c == CL_FIRSTMM || c == CL_FIRSTVIOL) {
+      uint64_t t = kNone;
+      for (int i = 0; i < kWaves; ++i) {
+        const uint64_t v = bs.u[i][LC_COUNT + 1 + c];
+        t = v < t ? v : t;
+      }
+      out.u64[c * out.stride + slot] = t;
+    } else if (c == CL_GABSI || c == CL_GRELI) {
+      const int q = c - CL_GABSI;
+      uint32_t bk = 0;
+      uint64_t bi = kNone;
+      for (int i = 0; i < kWaves; ++i) {
+        if (better(bs.k[i][2 + q], bs.u[i][LC_COUNT + 3 + q], bk, bi)) {
+          bk = bs.k[i][2 + q];
+          bi = bs.u[i][LC_COUNT + 3 + q];
+        }
+      }
+      out.u64[c * out.stride + slot] = bi;
+      out.u32[(CU_GABSK + q) * out.stride + slot] = bk;
+    } else {
+      double t = 0.0;
+      for (int i = 0; i < kWaves; ++i) t += bs.s[i][c - CL_S0];
+      out.u64[c * out.stride + slot] = (uint64_t)__double_as_longlong(t);
+    }
   }
   acc.init();
   __syncthreads();
@@ -1051,8 +1062,9 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   for (int64_t it = i0; it < i1; ++it) {
     if constexpr (BATCH) {
       if (it >= a.table[s].item_begin + a.table[s].item_count) {
+        const int prev_s = s;
         while (it >= a.table[s].item_begin + a.table[s].item_count) ++s;
-        flush_run(acc, sm.wcnt, sm.bs, &a.runs[run_start]);
+        flush_run(acc, sm.wcnt, sm.bs, a.runs, run_slot(a.table[prev_s], run_start));
         run_start = it;
         near_prev = 0;
         loaded = false;
@@ -1089,7 +1101,10 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
     }
     if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, sm, near_prev);
   }
-  flush_run(acc, sm.wcnt, sm.bs, &a.runs[run_start]);
+  {
+    const SegDesc& d = BATCH ? a.table[s] : a.seg0;
+    flush_run(acc, sm.wcnt, sm.bs, a.runs, run_slot(d, run_start));
+  }
 }
 
 // ------------------------------------------------------------ run records
@@ -1104,61 +1119,6 @@ __device__ __forceinline__ double cosine_of(double gr, double gg, double rr) {
   if (gn == 0.0 && rn == 0.0) return 1.0;
   if (gn == 0.0 || rn == 0.0) return 0.0;
   return clamp_cos(gr / (gn * rn));
-}
-
-// Item holding run j of a segment.  Runs start at the segment's first item and
-// at every block-range start (run_base + b * run_ipb) inside the segment.
-__device__ __forceinline__ int64_t run_item(const SegDesc& d, int64_t j, int64_t b_first) {
-  return j == 0 ? d.item_begin : d.run_base + (b_first + j - 1) * d.run_ipb;
-}
-
-// Merge of two partial verdicts: counts add, first indices take the minimum,
-// keys the maximum, (key, index) pairs the argmax, fp64 sums add.
-__device__ __forceinline__ void run_init(RunAcc& r) {
-#pragma unroll
-  for (int c = 0; c < LC_COUNT; ++c) r.cnt[c] = 0;
-  r.mismatch = 0;
-  r.first_mm = r.first_viol = kNone;
-  r.gabs_i = r.grel_i = kNone;
-  r.mm_abs = r.mm_rel = r.gabs_k = r.grel_k = 0;
-#pragma unroll
-  for (int i = 0; i < 7; ++i) r.s[i] = 0.0;
-}
-
-template <typename R>
-__device__ __forceinline__ void run_merge(RunAcc& a, const R& v) {
-#pragma unroll
-  for (int c = 0; c < LC_COUNT; ++c) a.cnt[c] += v.cnt[c];
-  a.mismatch += v.mismatch;
-  a.first_mm = v.first_mm < a.first_mm ? v.first_mm : a.first_mm;
-  a.first_viol = v.first_viol < a.first_viol ? v.first_viol : a.first_viol;
-  a.mm_abs = v.mm_abs > a.mm_abs ? v.mm_abs : a.mm_abs;
-  a.mm_rel = v.mm_rel > a.mm_rel ? v.mm_rel : a.mm_rel;
-  if (better(v.gabs_k, v.gabs_i, a.gabs_k, a.gabs_i)) {
-    a.gabs_k = v.gabs_k;
-    a.gabs_i = v.gabs_i;
-  }
-  if (better(v.grel_k, v.grel_i, a.grel_k, a.grel_i)) {
-    a.grel_k = v.grel_k;
-    a.grel_i = v.grel_i;
-  }
-#pragma unroll
-  for (int i = 0; i < 7; ++i) a.s[i] += v.s[i];
-}
-
-// Fixed-order fold of a RunAcc over the 64 lanes of a wave (result in every lane).
-__device__ __forceinline__ void run_wave_reduce(RunAcc& r) {
-#pragma unroll
-  for (int c = 0; c < LC_COUNT; ++c) r.cnt[c] = wave_total_u64(r.cnt[c]);
-  r.mismatch = wave_total_u64(r.mismatch);
-  r.first_mm = wave_min(r.first_mm);
-  r.first_viol = wave_min(r.first_viol);
-  r.mm_abs = wave_max(r.mm_abs);
-  r.mm_rel = wave_max(r.mm_rel);
-  wave_argmax(r.gabs_k, r.gabs_i);
-  wave_argmax(r.grel_k, r.grel_i);
-#pragma unroll
-  for (int i = 0; i < 7; ++i) r.s[i] = wave_total_f64(r.s[i]);
 }
 
 // ------------------------------------------------------------ near-zero sample

@@ -23,14 +23,15 @@ struct TailArgs {
   const SegDesc* table;
   const int64_t* chunk_seg;   // batch: owning segment of each select chunk
   int32_t nseg;
-  int32_t reduce_blocks;      // leading blocks that fold run records (one per segment), 0 for none
+  int32_t reduce_blocks;      // leading blocks that fold run records (reduce_roles per segment), 0 for none
+  int32_t reduce_roles;       // 3, or 4 with the near-zero prefix
   int32_t level;              // select digit level 0, 1 or 2 (small groups are done at level 0)
   int32_t arr_lo;             // select blocks cover arrays [arr_lo, arr_lo + narr)
   int32_t narr;
   int32_t pad;
   int64_t total_chunks;       // select blocks per array
   kvv_result* res;
-  const RunRec* runs;
+  RunCols runs;
   const float* arr[kArrays];
   uint32_t* slots;            // kArrays * kSlotWords words per large segment
   const uint32_t* item_near;
@@ -39,13 +40,16 @@ struct TailArgs {
 };
 
 struct ReduceLds {
-  RunAcc wred[kWaves];
-  RunAcc fin;
+  uint64_t pu[kBlock];   // per-thread partial folds
+  uint32_t pk[kBlock];
+  double pd[kBlock];
+  uint64_t tu[32];       // per-field totals
+  double td[8];
   uint64_t wsum[kWaves];
 };
 
 // Block histograms hold two 16-bit bin counts per word: a block counts at most
-// kSelChunk (= kSmall) values, so a count never carries into its neighbour.
+// max(kSelChunk, kSmall) values, so a count never carries into its neighbour.
 // Sample counts stay below 2^24 (the host caps max_samples), so ranks and
 // histogram sums fit 32 bits.
 struct SelectLds {
@@ -54,7 +58,7 @@ struct SelectLds {
   uint32_t sh[16];
   uint32_t misc[4];
 };
-static_assert(kSelChunk == kSmall && kSelChunk <= 65535, "16-bit block bin counts");
+static_assert(kSelChunk <= 65535 && kSmall <= 65535, "16-bit block bin counts");
 
 union TailLds {
   ReduceLds r;
@@ -62,183 +66,291 @@ union TailLds {
 };
 
 // ------------------------------------------------------------ run-record fold
-// kvv_result of one segment from its run records: each thread folds a strided
-// subset, waves fold lanes in order, then one thread per field folds the waves
-// in order, and the output fields are written by several threads at once.
-__device__ inline void reduce_segment(const TailArgs& a, int seg, ReduceLds& L) {
-  const SegDesc& d = a.table ? a.table[seg] : a.seg0;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  // runs of this segment: its first item plus the block starts strictly inside it
-  int64_t nruns = 0, b_first = 0;
-  if (d.item_count > 0) {
-    const int64_t rel0 = d.item_begin - d.run_base;                    // >= 0
-    b_first = rel0 / d.run_ipb + 1;                                     // first block start after item_begin
-    const int64_t rel_end = d.item_begin + d.item_count - d.run_base;  // exclusive
-    const int64_t b_end = (rel_end + d.run_ipb - 1) / d.run_ipb;       // block starts < rel_end
-    nruns = 1 + (b_end > b_first ? b_end - b_first : 0);
-  }
-  RunAcc acc;
-  run_init(acc);
-  // two records in flight per step
-  for (int64_t j = tid; j < nruns; j += 2 * kBlock) {
-    const RunRec r0 = a.runs[run_item(d, j, b_first)];
-    const bool two = j + kBlock < nruns;
-    RunRec r1;
-    if (two) r1 = a.runs[run_item(d, j + kBlock, b_first)];
-    run_merge(acc, r0);
-    if (two) run_merge(acc, r1);
-  }
-  run_wave_reduce(acc);
-  if (lane == 0) L.wred[w] = acc;
-  // near-zero: exclusive prefix of the per-item counts, in item order
-  if (d.flags & KVV_FLAG_NEAR_ZERO) {
-    const int64_t per = (d.item_count + kBlock - 1) / kBlock;
-    const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
-    const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
-    uint64_t mine = 0;
-    for (int64_t k = k0; k < k1; ++k) mine += a.item_near[d.item_begin + k];
-    uint64_t incl = mine;
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t v = __shfl_up(incl, o);
-      if (lane >= o) incl += v;
+// kvv_result of one segment from its run columns, split over five blocks
+// (roles) that each own a disjoint set of output fields: 0-2 the counts (finite
+// pattern and near-zero, ULP histogram, mismatches), 3 the first indices and
+// argmaxima, 4 the fp64 sums; role 5 (tolerant policy) writes the near-zero
+// prefix of the per-item counts.  Inside a role,
+// F fields x P parts cover the block; part p of a field folds slots
+// [p*S, (p+1)*S) of the segment (S a multiple of 4, so every thread issues
+// aligned 16-byte loads, all at once), and the parts are folded in order.
+template <int F, int P>
+__device__ __forceinline__ void role_split(int64_t nruns, int& f, int& p, int64_t& j0, int64_t& j1) {
+  const int tid = threadIdx.x;
+  f = tid / P;
+  p = tid % P;
+  int64_t span = (nruns + P - 1) / P;
+  span = (span + 3) & ~int64_t(3);
+  j0 = (int64_t)p * span;
+  j1 = j0 + span < nruns ? j0 + span : nruns;
+  if (f >= F) j0 = j1 = 0;
+}
+
+__device__ __forceinline__ int64_t segment_runs(const SegDesc& d) {
+  if (d.item_count <= 0) return 0;
+  const int64_t rel0 = d.item_begin - d.run_base;                    // >= 0
+  const int64_t b_first = rel0 / d.run_ipb + 1;                       // first block start after item_begin
+  const int64_t rel_end = d.item_begin + d.item_count - d.run_base;  // exclusive
+  const int64_t b_end = (rel_end + d.run_ipb - 1) / d.run_ipb;       // block starts < rel_end
+  return 1 + (b_end > b_first ? b_end - b_first : 0);
+}
+
+// Folds a u32 column part [j0, j1) (sum or max), 4 slots per load, 16 loads in flight.
+template <bool MAX>
+__device__ __forceinline__ uint64_t fold_u32(const uint32_t* col, int64_t j0, int64_t j1) {
+  uint64_t t = 0;
+  for (int64_t j = j0; j < j1; j += 64) {
+    uint4 q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = j + 4 * i < j1 ? *reinterpret_cast<const uint4*>(col + j + 4 * i) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t v[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool in = j + 4 * i + e < j1;
+        const uint64_t x = in ? v[e] : 0u;
+        if (MAX) t = x > t ? x : t; else t += x;
+      }
     }
-    if (lane == 63) L.wsum[w] = incl;
-    __syncthreads();
-    uint64_t base = 0;
-    for (int i = 0; i < w; ++i) base += L.wsum[i];
-    uint64_t run = base + incl - mine;
-    for (int64_t k = k0; k < k1; ++k) {
-      a.item_near_off[d.item_begin + k] = run;
-      run += a.item_near[d.item_begin + k];
+  }
+  return t;
+}
+
+// Count columns [F0, F0 + F) of the segment, folded by one block; the outputs
+// of those counts are written by the same block.
+template <int F0, int F>
+__device__ inline void reduce_counts(const TailArgs& a, const SegDesc& d, int64_t nruns, ReduceLds& L) {
+  constexpr int P = kBlock / F;
+  int f, p;
+  int64_t j0, j1;
+  role_split<F, P>(nruns, f, p, j0, j1);
+  const int col_i = F0 + (f < F ? f : 0);
+  const uint32_t* col = a.runs.u32 + (size_t)col_i * a.runs.stride + d.run_slot0;
+  const bool is_max = col_i == CU_MMABS || col_i == CU_MMREL;
+  L.pu[threadIdx.x] = is_max ? fold_u32<true>(col, j0, j1) : fold_u32<false>(col, j0, j1);
+  __syncthreads();
+  const int tid = threadIdx.x;
+  if (tid < F) {
+    const int c = F0 + tid;
+    uint64_t t = 0;
+    for (int q = 0; q < P; ++q) {
+      const uint64_t v = L.pu[tid * P + q];
+      if (c == CU_MMABS || c == CU_MMREL) t = v > t ? v : t; else t += v;
     }
+    L.tu[c] = t;
   }
   __syncthreads();
-  // fold the wave records: thread f takes field f, waves in order
-  if (tid < LC_COUNT) {
-    uint64_t t = 0;
-    for (int i = 0; i < kWaves; ++i) t += L.wred[i].cnt[tid];
-    L.fin.cnt[tid] = t;
-  } else if (tid < LC_COUNT + 14) {
-    RunAcc& f = L.fin;
-    const int g = tid - LC_COUNT;
-    if (g == 0) {
-      uint64_t t = 0;
-      for (int i = 0; i < kWaves; ++i) t += L.wred[i].mismatch;
-      f.mismatch = t;
-    } else if (g == 1 || g == 2) {
-      uint64_t t = kNone;
-      for (int i = 0; i < kWaves; ++i) {
-        const uint64_t v = g == 1 ? L.wred[i].first_mm : L.wred[i].first_viol;
-        t = v < t ? v : t;
+  kvv_result& o = a.res[d.out_index];
+  const double qnan = __builtin_nan("");
+  auto cnt = [&](int c) { return L.tu[c]; };
+  if (F0 == 0) {  // finite pattern and near-zero counts
+    switch (tid) {
+      case 0:
+        o.finite_violations = (int64_t)cnt(LC_VIOL);
+        o.nan_gen = (int64_t)cnt(LC_NAN_G);
+        o.nan_ref = (int64_t)cnt(LC_NAN_R);
+        o.posinf_gen = (int64_t)cnt(LC_PINF_G);
+        break;
+      case 1:
+        o.posinf_ref = (int64_t)cnt(LC_PINF_R);
+        o.neginf_gen = (int64_t)cnt(LC_NINF_G);
+        o.neginf_ref = (int64_t)cnt(LC_NINF_R);
+        o.nan_pairs = (int64_t)cnt(LC_NANPAIR);
+        break;
+      case 2: {
+        const int64_t c = (int64_t)cnt(LC_NEAR);
+        o.near_zero_count = c;
+        o.far_count = d.n - c;
+        o.far_mismatch_count = (int64_t)cnt(LC_FARMM);
+        o.near_zero_bad_count = (int64_t)cnt(LC_NEARBAD);
+        const int64_t nm = c < d.max_samples ? c : d.max_samples;
+        o.near_zero_sample_count = nm;
+        // the near-zero selection writes these when it has a sample to work on
+        if (!(d.flags & KVV_FLAG_NEAR_ZERO) || nm == 0) o.near_zero_p99_abs = o.near_zero_mean_abs = qnan;
+        break;
       }
-      if (g == 1) f.first_mm = t; else f.first_viol = t;
-    } else if (g == 3 || g == 4) {
-      uint32_t t = 0;
-      for (int i = 0; i < kWaves; ++i) {
-        const uint32_t v = g == 3 ? L.wred[i].mm_abs : L.wred[i].mm_rel;
-        t = v > t ? v : t;
-      }
-      if (g == 3) f.mm_abs = t; else f.mm_rel = t;
-    } else if (g == 5 || g == 6) {
-      uint32_t bk = 0;
-      uint64_t bi = kNone;
-      for (int i = 0; i < kWaves; ++i) {
-        const uint32_t k = g == 5 ? L.wred[i].gabs_k : L.wred[i].grel_k;
-        const uint64_t x = g == 5 ? L.wred[i].gabs_i : L.wred[i].grel_i;
-        if (better(k, x, bk, bi)) {
+      default:
+        break;
+    }
+  } else if (F0 == LC_HIST0) {  // ULP histogram
+    if (tid < kBuckets) o.ulp_hist[tid] = cnt(LC_HIST0 + tid);
+  } else if (tid == 0) {  // mismatches, and the fields of no column
+    const bool imode = d.mode == KVV_MODE_MAX_ABS_DIFF;
+    o.numel = d.n;
+    const uint64_t mm = cnt(CU_MISM);
+    o.mismatch_count = (int64_t)mm;
+    const uint32_t ka = (uint32_t)cnt(CU_MMABS), kr = (uint32_t)cnt(CU_MMREL);
+    o.mismatch_max_abs = mm ? (imode ? (double)ikey_value(ka) : (double)fkey_value(ka)) : 0.0;
+    o.mismatch_max_rel = mm ? (double)fkey_value(kr) : 0.0;
+    o.sample_count = d.m;
+    // an empty sample has no selection to write its quantiles
+    if (d.m == 0) o.p99_abs = o.p99_rel = qnan;
+    o.status = 0;
+    o.reserved = 0;
+  }
+}
+
+__device__ inline void reduce_extrema(const TailArgs& a, const SegDesc& d, int64_t nruns, ReduceLds& L) {
+  // fields: 0 first mismatch, 1 first finite violation (min); 2 abs, 3 rel (argmax)
+  constexpr int F = 4, P = kBlock / F;
+  int f, p;
+  int64_t j0, j1;
+  role_split<F, P>(nruns, f, p, j0, j1);
+  const int tid = threadIdx.x;
+  const uint64_t* ci = a.runs.u64 + (size_t)(f < 2 ? f : CL_GABSI + (f - 2)) * a.runs.stride + d.run_slot0;
+  const uint32_t* ck = a.runs.u32 + (size_t)(CU_GABSK + (f >= 2 ? f - 2 : 0)) * a.runs.stride + d.run_slot0;
+  uint32_t bk = 0;
+  uint64_t bi = kNone;
+  for (int64_t j = j0; j < j1; j += 16) {
+    uint4 qi[8];
+    uint4 qk[4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qi[i] = j + 2 * i < j1 ? *reinterpret_cast<const uint4*>(ci + j + 2 * i) : make_uint4(0, 0, 0, 0);
+    if (f >= 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qk[i] = j + 4 * i < j1 ? *reinterpret_cast<const uint4*>(ck + j + 4 * i) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      if (j + e >= j1) continue;
+      const uint4 wi = qi[e >> 1];
+      const uint64_t idx = (e & 1) ? (((uint64_t)wi.w << 32) | wi.z) : (((uint64_t)wi.y << 32) | wi.x);
+      if (f < 2) {
+        bi = idx < bi ? idx : bi;
+      } else {
+        const uint4 wk = qk[e >> 2];
+        const uint32_t k = (e & 3) == 0 ? wk.x : ((e & 3) == 1 ? wk.y : ((e & 3) == 2 ? wk.z : wk.w));
+        if (better(k, idx, bk, bi)) {
           bk = k;
-          bi = x;
+          bi = idx;
         }
       }
-      if (g == 5) {
-        f.gabs_k = bk;
-        f.gabs_i = bi;
-      } else {
-        f.grel_k = bk;
-        f.grel_i = bi;
-      }
-    } else {
-      double t = 0.0;
-      for (int i = 0; i < kWaves; ++i) t += L.wred[i].s[g - 7];
-      f.s[g - 7] = t;
     }
   }
+  L.pu[tid] = bi;
+  L.pk[tid] = bk;
   __syncthreads();
-  const RunAcc& r = L.fin;
-  kvv_result& o = a.res[d.out_index];
-  const bool imode = d.mode == KVV_MODE_MAX_ABS_DIFF;
-  const double qnan = __builtin_nan("");
-  switch (tid) {
-    case 0:
-      o.numel = d.n;
-      o.mismatch_count = (int64_t)r.mismatch;
-      o.first_mismatch_index = r.first_mm == kNone ? -1 : (int64_t)r.first_mm;
-      o.mismatch_max_abs = r.mismatch ? (imode ? (double)ikey_value(r.mm_abs) : (double)fkey_value(r.mm_abs)) : 0.0;
-      o.mismatch_max_rel = r.mismatch ? (double)fkey_value(r.mm_rel) : 0.0;
-      o.status = 0;
-      o.reserved = 0;
-      break;
-    case 1: {
-      o.sample_count = d.m;
-      o.sample_sum_gg = r.s[4];
-      o.sample_sum_rr = r.s[5];
-      o.sample_sum_gr = r.s[6];
-      o.sample_cosine = cosine_of(r.s[6], r.s[4], r.s[5]);
-      const double gn = sqrt(r.s[4]), rn = sqrt(r.s[5]);
-      o.sample_norm_ratio = (gn == 0.0 && rn == 0.0) ? 1.0 : (gn == 0.0 ? 0.0 : (rn == 0.0 ? __builtin_inf() : gn / rn));
-      break;
-    }
-    case 2:
-      o.finite_violations = (int64_t)r.cnt[LC_VIOL];
-      o.first_finite_violation = r.first_viol == kNone ? -1 : (int64_t)r.first_viol;
-      o.nan_gen = (int64_t)r.cnt[LC_NAN_G];
-      o.nan_ref = (int64_t)r.cnt[LC_NAN_R];
-      o.posinf_gen = (int64_t)r.cnt[LC_PINF_G];
-      o.posinf_ref = (int64_t)r.cnt[LC_PINF_R];
-      o.neginf_gen = (int64_t)r.cnt[LC_NINF_G];
-      o.neginf_ref = (int64_t)r.cnt[LC_NINF_R];
-      break;
-    case 3: {
-      const int64_t c = (int64_t)r.cnt[LC_NEAR];
-      o.near_zero_count = c;
-      o.far_count = d.n - c;
-      o.far_mismatch_count = (int64_t)r.cnt[LC_FARMM];
-      o.near_zero_bad_count = (int64_t)r.cnt[LC_NEARBAD];
-      const int64_t nm = c < d.max_samples ? c : d.max_samples;
-      o.near_zero_sample_count = nm;
-      // the near-zero selection writes these when it has a sample to work on
-      if (!(d.flags & KVV_FLAG_NEAR_ZERO) || nm == 0) o.near_zero_p99_abs = o.near_zero_mean_abs = qnan;
-      break;
-    }
-    case 4:
-      if (d.n > 0) {
-        o.max_abs = imode ? (double)ikey_value(r.gabs_k) : (double)fkey_value(r.gabs_k);
-        o.max_abs_index = (int64_t)r.gabs_i;
-        o.max_rel = (double)fkey_value(r.grel_k);
-        o.max_rel_index = (int64_t)r.grel_i;
-      } else {
-        o.max_abs = o.max_rel = 0.0;
-        o.max_abs_index = o.max_rel_index = -1;
+  if (tid < F) {
+    uint32_t tk = 0;
+    uint64_t ti = kNone;
+    for (int q = 0; q < P; ++q) {
+      const uint64_t vi = L.pu[tid * P + q];
+      const uint32_t vk = L.pk[tid * P + q];
+      if (tid < 2) {
+        ti = vi < ti ? vi : ti;
+      } else if (better(vk, vi, tk, ti)) {
+        tk = vk;
+        ti = vi;
       }
-      break;
-    case 5: {
-      o.nan_pairs = (int64_t)r.cnt[LC_NANPAIR];
-      o.sum_gg = r.s[0];
-      o.sum_rr = r.s[1];
-      o.sum_gr = r.s[2];
-      o.sum_dd = r.s[3];
-      const double dn = sqrt(r.s[3]), rn = sqrt(r.s[1]);
-      o.rel_l2 = rn == 0.0 ? (dn == 0.0 ? 0.0 : __builtin_inf()) : dn / rn;
-      o.cosine = cosine_of(r.s[2], r.s[0], r.s[1]);
-      break;
     }
-    case 6:
-      // an empty sample has no selection to write its quantiles
-      if (d.m == 0) o.p99_abs = o.p99_rel = qnan;
-      break;
-    default:
-      if (tid >= 64 && tid < 64 + kBuckets) o.ulp_hist[tid - 64] = r.cnt[LC_HIST0 + tid - 64];
-      break;
+    kvv_result& o = a.res[d.out_index];
+    const bool imode = d.mode == KVV_MODE_MAX_ABS_DIFF;
+    if (tid == 0) {
+      o.first_mismatch_index = ti == kNone ? -1 : (int64_t)ti;
+    } else if (tid == 1) {
+      o.first_finite_violation = ti == kNone ? -1 : (int64_t)ti;
+    } else if (d.n == 0) {
+      if (tid == 2) {
+        o.max_abs = 0.0;
+        o.max_abs_index = -1;
+      } else {
+        o.max_rel = 0.0;
+        o.max_rel_index = -1;
+      }
+    } else if (tid == 2) {
+      o.max_abs = imode ? (double)ikey_value(tk) : (double)fkey_value(tk);
+      o.max_abs_index = (int64_t)ti;
+    } else {
+      o.max_rel = (double)fkey_value(tk);
+      o.max_rel_index = (int64_t)ti;
+    }
+  }
+}
+
+__device__ inline void reduce_sums(const TailArgs& a, const SegDesc& d, int64_t nruns, ReduceLds& L) {
+  constexpr int F = 7, P = kBlock / F;
+  int f, p;
+  int64_t j0, j1;
+  role_split<F, P>(nruns, f, p, j0, j1);
+  const int tid = threadIdx.x;
+  const uint64_t* col = a.runs.u64 + (size_t)(CL_S0 + (f < F ? f : 0)) * a.runs.stride + d.run_slot0;
+  double t = 0.0;
+  for (int64_t j = j0; j < j1; j += 32) {
+    uint4 q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = j + 2 * i < j1 ? *reinterpret_cast<const uint4*>(col + j + 2 * i) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      if (j + e >= j1) continue;
+      const uint4 w = q[e >> 1];
+      const uint64_t bits = (e & 1) ? (((uint64_t)w.w << 32) | w.z) : (((uint64_t)w.y << 32) | w.x);
+      t += __longlong_as_double((long long)bits);
+    }
+  }
+  L.pd[tid] = t;
+  __syncthreads();
+  if (tid < F) {
+    double u = 0.0;
+    for (int q = 0; q < P; ++q) u += L.pd[tid * P + q];
+    L.td[tid] = u;
+  }
+  __syncthreads();
+  auto sum = [&](int i) { return L.td[i]; };
+  kvv_result& o = a.res[d.out_index];
+  if (tid == 0) {
+    o.sample_sum_gg = sum(4);
+    o.sample_sum_rr = sum(5);
+    o.sample_sum_gr = sum(6);
+    o.sample_cosine = cosine_of(sum(6), sum(4), sum(5));
+    const double gn = sqrt(sum(4)), rn = sqrt(sum(5));
+    o.sample_norm_ratio = (gn == 0.0 && rn == 0.0) ? 1.0 : (gn == 0.0 ? 0.0 : (rn == 0.0 ? __builtin_inf() : gn / rn));
+  } else if (tid == 1) {
+    o.sum_gg = sum(0);
+    o.sum_rr = sum(1);
+    o.sum_gr = sum(2);
+    o.sum_dd = sum(3);
+    const double dn = sqrt(sum(3)), rn = sqrt(sum(1));
+    o.rel_l2 = rn == 0.0 ? (dn == 0.0 ? 0.0 : __builtin_inf()) : dn / rn;
+    o.cosine = cosine_of(sum(2), sum(0), sum(1));
+  }
+}
+
+// Near-zero: exclusive prefix of the per-item counts, in item order.
+__device__ inline void reduce_near_prefix(const TailArgs& a, const SegDesc& d, ReduceLds& L) {
+  if (!(d.flags & KVV_FLAG_NEAR_ZERO)) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t per = (d.item_count + kBlock - 1) / kBlock;
+  const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
+  const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
+  uint64_t mine = 0;
+  for (int64_t k = k0; k < k1; ++k) mine += a.item_near[d.item_begin + k];
+  uint64_t incl = mine;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t v = __shfl_up(incl, o);
+    if (lane >= o) incl += v;
+  }
+  if (lane == 63) L.wsum[w] = incl;
+  __syncthreads();
+  uint64_t base = 0;
+  for (int i = 0; i < w; ++i) base += L.wsum[i];
+  uint64_t run = base + incl - mine;
+  for (int64_t k = k0; k < k1; ++k) {
+    a.item_near_off[d.item_begin + k] = run;
+    run += a.item_near[d.item_begin + k];
+  }
+}
+
+__device__ inline void reduce_segment(const TailArgs& a, int seg, int role, ReduceLds& L) {
+  const SegDesc& d = a.table ? a.table[seg] : a.seg0;
+  const int64_t nruns = segment_runs(d);
+  switch (role) {
+    case 0: reduce_counts<0, LC_HIST0>(a, d, nruns, L); break;
+    case 1: reduce_counts<LC_HIST0, kBuckets>(a, d, nruns, L); break;
+    case 2: reduce_counts<CU_MISM, 3>(a, d, nruns, L); break;
+    case 3: reduce_extrema(a, d, nruns, L); break;
+    case 4: reduce_sums(a, d, nruns, L); break;
+    default: reduce_near_prefix(a, d, L); break;
   }
 }
 
@@ -263,6 +375,22 @@ __device__ __forceinline__ void q99_ranks(int64_t m, uint64_t rank[2], float& w)
 __device__ __forceinline__ void lds_hist_add(uint32_t* h, uint32_t bin, bool act) {
   if (act) atomicAdd(&h[bin >> 1], 1u << ((bin & 1u) << 4));
 }
+
+// Per-lane run-length merge in front of lds_hist_add: consecutive values of a
+// lane that fall in the same bin become one add (skewed data, e.g. mostly
+// identical pairs, then costs a few atomics per lane instead of one per value).
+struct BinRun {
+  uint32_t bin = 0, cnt = 0;
+  __device__ __forceinline__ void add(uint32_t* h, uint32_t b, bool act) {
+    const bool change = act && b != bin;
+    if (change && cnt) atomicAdd(&h[bin >> 1], cnt << ((bin & 1u) << 4));
+    bin = change ? b : bin;
+    cnt = change ? 1u : cnt + (act ? 1u : 0u);
+  }
+  __device__ __forceinline__ void flush(uint32_t* h) {
+    if (cnt) atomicAdd(&h[bin >> 1], cnt << ((bin & 1u) << 4));
+  }
+};
 
 __device__ __forceinline__ uint32_t packed_count(const uint32_t* h, uint32_t bin) {
   return (h[bin >> 1] >> ((bin & 1u) << 4)) & 0xFFFFu;
@@ -518,6 +646,7 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
   for (int i = tid; i < nwords; i += kBlock) (&L.h[0][0])[i] = 0;
   __syncthreads();
   uint32_t nans = 0;
+  BinRun run0;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int64_t idx = c0 + (int64_t)i * kBlock + tid;
@@ -527,14 +656,17 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
     const uint32_t key = fkey(x[i]);
     const uint32_t dig = (key >> DS) & DM;
     if (LEVEL == 0) {
-      lds_hist_add(L.h[0], dig, ok);
+      run0.add(L.h[0], dig, ok);
     } else {
       const uint32_t top = key >> HS;
       lds_hist_add(L.h[0], dig, ok && top == pfx[0]);
       if (!same) lds_hist_add(L.h[1], dig, ok && top == pfx[1]);
     }
   }
-  if (LEVEL == 0) nans = block_sum_nan(nans, L);
+  if (LEVEL == 0) {
+    run0.flush(L.h[0]);
+    nans = block_sum_nan(nans, L);
+  }
   __syncthreads();
   // add the block histogram to the group's: bins 2w and 2w+1 of word w
   uint32_t* gh = slot + (LEVEL == 0 ? kH0 : (LEVEL == 1 ? kH1 : kH2));
@@ -569,7 +701,7 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
   __shared__ TailLds lds;
   const int64_t b = blockIdx.x;
   if (LEVEL == 0 && b < a.reduce_blocks) {
-    reduce_segment(a, (int)b, lds.r);
+    reduce_segment(a, (int)(b / a.reduce_roles), (int)(b % a.reduce_roles), lds.r);
     return;
   }
   const int64_t sb = b - a.reduce_blocks;
