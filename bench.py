@@ -3,10 +3,12 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1]
 
-A step is one complete verdict of one tensor pair that is already resident in
-HBM: every kernel of libkvv's launch sequence plus the copy of the result
-record to the host and the stream synchronisation.  ``value`` is algorithmic
-input bytes (both tensors read once) per second of step time.
+A step is one complete verdict of one tensor pair (or, for c4, one batch of
+pairs) already resident in HBM: every kernel of libkvv's launch sequence, with
+the result record written into pinned host memory.  The K timed steps run back
+to back between two synchronisations; ``value`` is algorithmic input bytes
+(both tensors read once) per second of step time.  ``us_per_verdict_synchronous``
+is the latency of one verdict issued and waited for on its own.
 
 The ``roofline`` object covers the dominant kernel (the main pass): its
 duration is measured live with HIP events recorded by the library around
@@ -15,7 +17,12 @@ steps.  ``cpu_baseline`` times the torch-CPU oracle (a restatement of the
 reference's own torch-CPU verdict) on a bounded slice of the same workload.
 
 Configurations (BASELINE.json ``configs``): c0 fp32 1 Mi, c1 bf16 256 Mi
-(default, the headline), c2 fp16 4096x32768 strided, c3fp8 / c3int8 128 Mi.
+(default, the headline), c2 fp16 4096x32768 strided, c3fp8 / c3int8 128 Mi,
+c4 ragged batch of 4096 fp32/bf16 pairs (events then bracket the whole call).
+
+``roofline.traffic`` is the main pass's HBM bytes per launch from rocprofv3
+FETCH_SIZE / WRITE_SIZE runs scaled by a plain-copy calibration
+(``--copy-calibration``), recorded in PMC_TRAFFIC below; null where not measured.
 """
 
 from __future__ import annotations
@@ -42,11 +49,10 @@ def log(*a):
 
 
 def make_workload(name: str, dev):
-    """(gen, ref, tolerance, description, dtype label) on the device."""
+    """(gen, ref, tolerance, description, dtype label) on the device; the generators are in kernelverse_amd/synth.py."""
     from kernelverse_amd import synth
     if name == "c1":
-        n = 268_435_456
-        g, r = synth.code_flip_pair_device(n, seed=1, device=dev, dtype=torch.bfloat16, std=2.0, p1=0.05, p3=1e-4)
+        g, r = synth.c1_pair(dev)
         return g, r, {"BF16": {"rtol": 1.6e-2, "atol": 1e-2}}, (
             "bf16 pair, 268,435,456 elements (1 GiB read); ref=bf16(N(0,2)); cand = ref with 1-ULP steps at 5% "
             "and 3-ULP steps at 0.01%; atol=1e-2 rtol=1.6e-2; full verdict + 16-bucket ULP histogram"), "bf16"
@@ -55,63 +61,88 @@ def make_workload(name: str, dev):
         return g.to(dev), r.to(dev), {"FP32": {"rtol": 1e-5, "atol": 1e-5}}, (
             "fp32 pair, 1,048,576 elements, contiguous; C0 noise model; atol=rtol=1e-5"), "f32"
     if name == "c2":
-        rows, cols, stride = 4096, 32768, 32896
-        gen = torch.Generator(device=dev)
-        gen.manual_seed(2)
-        base_r = (torch.rand(rows, stride, generator=gen, device=dev) * 120000.0 - 60000.0).to(torch.float16)
-        u = torch.rand(rows, stride, generator=gen, device=dev)
-        base_r[u < 5e-4] = float("nan")
-        base_r[(u >= 5e-4) & (u < 1e-3)] = float("inf")
-        base_g = base_r.clone()
-        flat = base_g.view(-1)
-        pos = torch.randint(0, rows * cols, (17,), generator=gen, device=dev)
-        flat[(pos // cols) * stride + pos % cols] = 1.0
-        return base_g[:, :cols], base_r[:, :cols], {"FP16": {"rtol": 1e-3, "atol": 1e-3}}, (
+        g, r = synth.c2_pair(dev)
+        return g, r, {"FP16": {"rtol": 1e-3, "atol": 1e-3}}, (
             "fp16 pair, 4096x32768 row-major, row stride 32896; U(-60000,60000) with 0.05% NaN and 0.05% Inf; "
             "17 finite-pattern breaks; atol=rtol=1e-3"), "f16"
     if name == "c3fp8":
-        g, r = synth.code_flip_pair_device(134_217_728, seed=3, device=dev, dtype=torch.float8_e4m3fn, std=4.0,
-                                           p1=0.02, p3=0.0, clamp=448.0)
+        g, r = synth.c3_fp8_pair(dev)
         return g, r, None, "fp8 e4m3fn pair, 134,217,728 elements; +-1 code at 2%; ULP histogram over codes", "fp8"
     if name == "c3int8":
-        gen = torch.Generator(device=dev)
-        gen.manual_seed(4)
-        r = torch.randint(-128, 128, (134_217_728,), generator=gen, device=dev, dtype=torch.int8)
-        g = r.clone()
-        pos = torch.randint(0, r.numel(), (1000,), generator=gen, device=dev)
-        g[pos] = (g[pos].to(torch.int16) + 77).to(torch.int8)
+        g, r = synth.c3_int8_pair(dev)
         return g, r, None, "int8 pair, 134,217,728 elements; 1000 changed positions; exact-equality count", "i8"
     raise SystemExit(f"unknown config {name}")
 
 
-def cpu_baseline(g_dev, r_dev, tol, budget_s: float = 20.0):
-    """Torch-CPU oracle verdict on a bounded leading slice of the workload."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(pairs, budget_s: float = 20.0):
+    """Torch-CPU oracle verdicts (the port, oracle/torch_verdict.py) on a bounded leading sample of the workload:
+    the first 16 Mi elements of a single pair, or the leading pairs of a batch up to 16 Mi elements."""
     from oracle import torch_verdict as tv
     threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
-    n = g_dev.numel()
-    sample = min(n, 1 << 24)
-    g = g_dev.reshape(-1)[:sample].cpu() if g_dev.is_contiguous() else g_dev.flatten()[:sample].cpu()
-    r = r_dev.reshape(-1)[:sample].cpu() if r_dev.is_contiguous() else r_dev.flatten()[:sample].cpu()
-    tv.compare_tensors(g, r, "output", tol)  # warm-up
+    cap = 1 << 24
+    host, taken = [], 0
+    t0 = time.perf_counter()
+    for g_dev, r_dev, tol in pairs:
+        k = min(g_dev.numel(), cap - taken)
+        if k <= 0:
+            break
+        g = g_dev.reshape(-1)[:k] if g_dev.is_contiguous() else g_dev.flatten()[:k]
+        r = r_dev.reshape(-1)[:k] if r_dev.is_contiguous() else r_dev.flatten()[:k]
+        host.append((g.cpu(), r.cpu(), tol))
+        taken += k
+    d2h_s = time.perf_counter() - t0
+    bytes_read = sum(2 * g.numel() * g.element_size() for g, _, _ in host)
+
+    def run_all():
+        for g, r, tol in host:
+            # fp8: the reference raises (no isfinite for float8); the port's decode path is what the GPU computes
+            tv.compare_tensors(g, r, "output", tol, fp8_decode=g.dtype in (torch.float8_e4m3fn, torch.float8_e5m2))
+
+    run_all()  # warm-up
     times = []
     t_start = time.perf_counter()
     while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
-        t0 = time.perf_counter()
-        tv.compare_tensors(g, r, "output", tol)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s and len(times) >= 3:
-            break
+        t1 = time.perf_counter()
+        run_all()
+        times.append(time.perf_counter() - t1)
     t = statistics.median(times)
-    bytes_read = 2 * sample * g.element_size()
     return {
         "value": round(bytes_read / t / 1e9, 4),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"torch-CPU oracle compare_tensors (restatement of GCR:672-786) on the first {sample:,} elements "
-                   f"of the same pair, median of {len(times)} runs, {t * 1e3:.1f} ms each; D2H copy excluded"),
+        "sample": (f"torch-CPU oracle compare_tensors (restatement of GCR:672-786) over {taken:,} elements "
+                   f"({len(host)} pair(s)) of the same workload, median of {len(times)} runs, {t * 1e3:.1f} ms each; "
+                   f"{threads} threads of {_cpu_model()}; torch {torch.__version__}; the device-to-host copy the "
+                   f"reference pays first took {d2h_s * 1e3:.1f} ms and is excluded"),
     }
+
+
+# HBM traffic of the main-pass kernel per launch, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (KiB per
+# dispatch) scaled by what the same counters read for a plain 512 MiB device copy (factors below); the runs and
+# commands are in profiles/scan_bf16_c1_traffic.md.  Keyed by config.
+PMC_TRAFFIC = {
+    "c1": {"fetch_kib": 524475.5, "write_kib": 9138.4, "fetch_factor": 524288.0 / 262157.5, "write_factor": 1.0},
+}
+
+
+def traffic_bytes(config: str):
+    t = PMC_TRAFFIC.get(config)
+    if not t or t["fetch_kib"] is None:
+        return None
+    return int(round((t["fetch_kib"] * t["fetch_factor"] + t["write_kib"] * t["write_factor"]) * 1024))
 
 
 def copy_calibration(steps: int):
@@ -152,42 +183,65 @@ def main():
     if args.copy_calibration:
         copy_calibration(args.steps)
         return
-    from kernelverse_amd import _lib, verdict
+    from kernelverse_amd import _lib, synth, verdict
 
     lib = _lib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     log(f"[bench] building workload {args.config}")
-    g, r, tol, desc, dlabel = make_workload(args.config, dev)
+    if args.config == "c4":
+        pairs = synth.c4_batch(dev)
+        desc = ("4096 pairs, dtype alternating fp32/bf16, sizes log-uniform in [1024, 1048576] (seed 5), C0 noise "
+                "model; FP32 atol=rtol=1e-5, BF16 atol=1e-2 rtol=1.6e-2; one batched call (kvv_verdict_batch)")
+        dlabel = "f32+bf16"
+    else:
+        g, r, tol, desc, dlabel = make_workload(args.config, dev)
+        pairs = [(g, r, tol)]
     torch.cuda.synchronize()
-    job = verdict._Job(g, r, "output", tol, None, verdict.MAX_SAMPLES, fp8_errors=False)
-    gt, rt = verdict._kvv_tensor(g), verdict._kvv_tensor(r)
+    jobs = [verdict._Job(g, r, "output", tol, None, verdict.MAX_SAMPLES, fp8_errors=False) for g, r, tol in pairs]
+    n_pairs = len(jobs)
+    gts = [verdict._kvv_tensor(g) for g, _, _ in pairs]
+    rts = [verdict._kvv_tensor(r) for _, r, _ in pairs]
     size = ctypes.c_size_t()
-    _lib.check(lib.kvv_workspace_size(gt, rt, job.kpolicy, ctypes.byref(size)), "kvv_workspace_size")
+    if n_pairs == 1:
+        _lib.check(lib.kvv_workspace_size(gts[0], rts[0], jobs[0].kpolicy, ctypes.byref(size)), "kvv_workspace_size")
+    else:
+        GA, PA = _lib.KvvTensor * n_pairs, _lib.KvvPolicy * n_pairs
+        garr, rarr, parr = GA(*gts), GA(*rts), PA(*[j.kpolicy for j in jobs])
+        _lib.check(lib.kvv_batch_workspace_size(n_pairs, garr, rarr, parr, ctypes.byref(size)),
+                   "kvv_batch_workspace_size")
     ws = torch.empty(size.value, dtype=torch.uint8, device=dev)
-    out = torch.empty(ctypes.sizeof(_lib.KvvResult), dtype=torch.uint8, device=dev)
-    host = torch.empty_like(out, device="cpu").pin_memory()
+    rec_size = ctypes.sizeof(_lib.KvvResult)
+    # results go straight to pinned host memory (the kernels write them over the bus; no copy launch)
+    host = torch.empty(rec_size * n_pairs, dtype=torch.uint8, pin_memory=True)
+    out = host
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
-    n = g.numel()
-    bytes_read = 2 * n * g.element_size()
+    n = sum(g.numel() for g, _, _ in pairs)
+    bytes_read = sum(2 * g.numel() * g.element_size() for g, _, _ in pairs)
 
     flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if bytes_read < (512 << 20) else None
 
     def step(ev0=None, ev1=None):
-        if ev0 is None:
-            rc = lib.kvv_verdict(gt, rt, job.kpolicy, out.data_ptr(), ws.data_ptr(), size.value, sh)
+        if n_pairs > 1:
+            # a batch has several main-pass launches: the events bracket the whole call
+            if ev0 is not None:
+                ev0.record(stream)
+            rc = lib.kvv_verdict_batch(n_pairs, garr, rarr, parr, out.data_ptr(), ws.data_ptr(), size.value, sh)
+            if ev1 is not None:
+                ev1.record(stream)
+        elif ev0 is None:
+            rc = lib.kvv_verdict(gts[0], rts[0], jobs[0].kpolicy, out.data_ptr(), ws.data_ptr(), size.value, sh)
         else:
-            rc = lib.kvv_verdict_timed(gt, rt, job.kpolicy, out.data_ptr(), ws.data_ptr(), size.value, sh,
+            rc = lib.kvv_verdict_timed(gts[0], rts[0], jobs[0].kpolicy, out.data_ptr(), ws.data_ptr(), size.value, sh,
                                        ev0.cuda_event, ev1.cuda_event)
         if rc:
             _lib.check(rc, "kvv_verdict")
-        host.copy_(out, non_blocking=True)
-        stream.synchronize()
 
     log(f"[bench] warmup {args.warmup}")
     for _ in range(args.warmup):
         step()
+        stream.synchronize()
     evs = []
     for _ in range(args.steps):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -196,21 +250,42 @@ def main():
         evs.append((e0, e1))
     torch.cuda.synchronize()
     log(f"[bench] timing {args.steps} steps")
-    step_times = []
-    for i in range(args.steps):
-        if flush is not None:
-            flush.fill_(i & 255)  # evict the 256 MB MALL so small inputs come from HBM
-            stream.synchronize()
+    if flush is None:
+        # back-to-back verdicts, each complete (all launches, result in host memory); one
+        # synchronisation before and after the timed steps
+        torch.cuda.synchronize()
         t0 = time.perf_counter()
-        step(*evs[i])
-        step_times.append(time.perf_counter() - t0)
-    torch.cuda.synchronize()
-    ms_per_step = 1e3 * sum(step_times) / len(step_times)
+        for i in range(args.steps):
+            step(*evs[i])
+        torch.cuda.synchronize()
+        ms_per_step = 1e3 * (time.perf_counter() - t0) / args.steps
+    else:
+        # small inputs: a 512 MiB write before every verdict evicts the 256 MB MALL so the inputs come from
+        # HBM; the write is outside the timed interval, so each verdict is timed on its own
+        step_times = []
+        for i in range(args.steps):
+            flush.fill_(i & 255)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            step(*evs[i])
+            stream.synchronize()
+            step_times.append(time.perf_counter() - t0)
+        ms_per_step = 1e3 * sum(step_times) / len(step_times)
+    # latency of one verdict issued and waited for on its own (the reference's usage: one compare, then read)
+    lat = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step()
+        stream.synchronize()
+        lat.append(time.perf_counter() - t0)
+    us_sync = 1e6 * statistics.median(lat)
     main_ms = [a.elapsed_time(b) for a, b in evs]
     main_avg = sum(main_ms) / len(main_ms)
-    rec = _lib.KvvResult.from_buffer_copy(host.numpy().tobytes())
+    recs = [_lib.KvvResult.from_buffer_copy(host.numpy().tobytes(), i * rec_size) for i in range(n_pairs)]
     value = bytes_read / (ms_per_step * 1e-3) / 1e9
     achieved = bytes_read / (main_avg * 1e-3) / 1e9
+    traffic = traffic_bytes(args.config)
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -220,30 +295,34 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "us_per_verdict": round(ms_per_step * 1e3, 1),
+        "us_per_verdict_synchronous": round(us_sync, 1),
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": dlabel,
         "data": "synthetic (seeded, generated on the device)",
-        "config": {"workload": desc, "config_id": args.config, "numel": n, "bytes_read": bytes_read,
-                   "tolerance": tol, "correctness_policy": "strict"},
+        "config": {"workload": desc, "config_id": args.config, "pairs": n_pairs, "numel": n, "bytes_read": bytes_read,
+                   "correctness_policy": "strict"},
         "roofline": {
             "bound": "hbm",
-            "kernel": "kvv::scan_kernel (main pass)",
+            "kernel": ("kvv::scan_kernel (main pass)" if n_pairs == 1 else "whole kvv_verdict_batch call"),
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel_avg_us": round(main_avg * 1e3, 2),
+            "algorithmic_bytes": bytes_read,
         },
-        "verdict_check": {"mismatch_count": rec.mismatch_count, "ulp_hist_b0_b1_b2": list(rec.ulp_hist)[:3],
-                          "finite_violations": rec.finite_violations, "p99_abs": rec.p99_abs},
+        "verdict_check": {"mismatch_count": sum(r.mismatch_count for r in recs),
+                          "ulp_hist_b0_b1_b2": [sum(r.ulp_hist[k] for r in recs) for k in range(3)],
+                          "finite_violations": sum(r.finite_violations for r in recs),
+                          "p99_abs_first_pair": recs[0].p99_abs},
     }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(g, r, tol)
+        result["cpu_baseline"] = cpu_baseline(pairs)
     print(json.dumps(result), flush=True)
 
 

@@ -144,7 +144,8 @@ KVV_API int kvv_workspace_size(const kvv_tensor* gen, const kvv_tensor* ref, con
  * (generated_correctness_runner.py:672-786) for one tensor pair.
  *   gen, ref    same shape and dtype (checked; the reference returns a
  *               mismatch meta instead, which the host wrapper does first)
- *   out         DEVICE pointer to one kvv_result, written by the stream
+ *   out         one kvv_result in memory the device can write: device memory,
+ *               or pinned host memory (hipHostMalloc) to receive it without a copy
  *   workspace   DEVICE scratch of at least kvv_workspace_size() bytes,
  *               256-byte aligned, owned by this call until the stream passes it
  *   stream      hipStream_t (NULL = default stream) */

@@ -206,3 +206,65 @@ def code_flip_pair_device(n: int, seed: int, device, dtype=torch.bfloat16, std: 
     cand_codes = torch.where(cand_codes > mag_mask, cand_codes - (2 * (mag_mask + 1)), cand_codes)
     cand = cand_codes.to(view).view(dtype)
     return cand, ref
+
+
+# ------------------------------------------------------------ benchmark configurations
+# The five workloads of the verdict benchmark, generated on the device from fixed seeds.
+
+def c1_pair(device):
+    """C1: bf16, 268,435,456 elements; ref = bf16(N(0,2)); cand = ref with 1-ULP steps at 5% and 3-ULP at 0.01%."""
+    return code_flip_pair_device(268_435_456, seed=1, device=device, dtype=torch.bfloat16, std=2.0, p1=0.05, p3=1e-4)
+
+
+def c2_pair(device, rows: int = 4096, cols: int = 32768, stride: int = 32896, seed: int = 2):
+    """C2: fp16 (rows, cols) views with row stride `stride`; ref ~ U(-60000, 60000) with 0.05% NaN and 0.05% Inf;
+    the candidate copies the reference except at 17 seeded non-finite reference positions, where it is 1.0."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    base_r = (torch.rand(rows, stride, generator=gen, device=device) * 120000.0 - 60000.0).to(torch.float16)
+    u = torch.rand(rows, stride, generator=gen, device=device)
+    base_r[u < 5e-4] = float("nan")
+    base_r[(u >= 5e-4) & (u < 1e-3)] = float("inf")
+    del u
+    base_g = base_r.clone()
+    nonfin = torch.nonzero(~torch.isfinite(base_r[:, :cols]).reshape(-1)).reshape(-1)
+    pick = nonfin[torch.randperm(nonfin.numel(), generator=gen, device=device)[:17]]
+    base_g[pick // cols, pick % cols] = 1.0
+    return base_g[:, :cols], base_r[:, :cols]
+
+
+def c3_fp8_pair(device):
+    """C3 fp8: e4m3fn, 134,217,728 elements; ref from N(0,4) clamped to +-448; cand = ref +- 1 code at 2%."""
+    return code_flip_pair_device(134_217_728, seed=3, device=device, dtype=torch.float8_e4m3fn, std=4.0,
+                                 p1=0.02, p3=0.0, clamp=448.0)
+
+
+def c3_int8_pair(device, n: int = 134_217_728, changed: int = 1000, seed: int = 4):
+    """C3 int8: ref ~ U[-128, 127]; cand equal except `changed` distinct seeded positions (each moved by 77)."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    r = torch.randint(-128, 128, (n,), generator=gen, device=device, dtype=torch.int8)
+    g = r.clone()
+    pos = torch.randperm(n, generator=gen, device=device)[:changed]
+    g[pos] = (g[pos].to(torch.int16) + 77).to(torch.int8)
+    return g, r
+
+
+def c4_batch(device, count: int = 4096, seed: int = 5):
+    """C4: `count` pairs, dtype alternating fp32 / bf16, sizes log-uniform in [1024, 2^20], the C0 noise model
+    (ref ~ N(0,1); cand = ref + N(0,1e-6); 0.1% of positions + U(1e-3, 1e-1)); each pair is its own allocation.
+    Returns [(cand, ref, tolerance)]."""
+    sizes = ragged_sizes(count, seed)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    out = []
+    for i, n in enumerate(sizes):
+        ref = torch.randn(n, generator=gen, device=device)
+        cand = ref + 1e-6 * torch.randn(n, generator=gen, device=device)
+        hit = torch.rand(n, generator=gen, device=device) < 1e-3
+        cand = torch.where(hit, cand + (1e-3 + (1e-1 - 1e-3) * torch.rand(n, generator=gen, device=device)), cand)
+        if i % 2:
+            out.append((cand.to(torch.bfloat16), ref.to(torch.bfloat16), {"BF16": {"rtol": 1.6e-2, "atol": 1e-2}}))
+        else:
+            out.append((cand, ref, {"FP32": {"rtol": 1e-5, "atol": 1e-5}}))
+    return out

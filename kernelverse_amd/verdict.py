@@ -298,14 +298,16 @@ def _run_jobs(jobs: List[_Job]) -> None:
             garr, rarr, parr = GA(*gts), GA(*rts), PA(*[j.kpolicy for j in jobs])
             _lib.check(lib.kvv_batch_workspace_size(n, garr, rarr, parr, ctypes.byref(size)), "kvv_batch_workspace_size")
         ws = torch.empty(size.value, dtype=torch.uint8, device=dev)
-        out = torch.empty(rec_size * n, dtype=torch.uint8, device=dev)
+        # the records are written by the kernels straight into pinned host memory
+        out = torch.empty(rec_size * n, dtype=torch.uint8, pin_memory=True)
         if n == 1:
             rc = lib.kvv_verdict(gts[0], rts[0], jobs[0].kpolicy, out.data_ptr(), ws.data_ptr(), size.value, stream)
             _lib.check(rc, "kvv_verdict")
         else:
             rc = lib.kvv_verdict_batch(n, garr, rarr, parr, out.data_ptr(), ws.data_ptr(), size.value, stream)
             _lib.check(rc, "kvv_verdict_batch")
-        host = out.cpu().numpy().tobytes()
+        torch.cuda.current_stream(dev).synchronize()
+        host = out.numpy().tobytes()
     del keep, ws
     for i, j in enumerate(jobs):
         j.record = _lib.KvvResult.from_buffer_copy(host, i * rec_size)

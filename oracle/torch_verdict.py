@@ -313,6 +313,44 @@ def evaluate_tensor_policy(reference, meta, correctness_policy) -> bool:
     return normal
 
 
+def mismatch_parts(generated: torch.Tensor, reference: torch.Tensor, tolerance_policy=None):
+    """GCR:712-730: (abs_diff, rel_diff, mismatch mask, tolerance dict) under the dtype policy of GCR:305-328.
+    Integer mode: int32 casts (int64 wraps) and |g - r| > max_abs_diff; float mode: float32 casts and
+    ~torch.isclose(r, g, rtol, atol); rel_diff = abs_diff / (|r| + 1e-12) in float32."""
+    policy = dtype_policy(reference, tolerance_policy)
+    if "max_abs_diff" in policy:
+        g = generated.to(torch.int32)
+        r = reference.to(torch.int32)
+        abs_diff = (g - r).abs()
+        mismatch = abs_diff > int(policy["max_abs_diff"])
+        tolerance = {"max_abs_diff": int(policy["max_abs_diff"])}
+    else:
+        g = generated.to(torch.float32)
+        r = reference.to(torch.float32)
+        abs_diff = (g - r).abs()
+        rtol = float(policy["rtol"])
+        atol = float(policy["atol"])
+        mismatch = ~torch.isclose(r, g, rtol=rtol, atol=atol)
+        tolerance = {"rtol": rtol, "atol": atol}
+    rel_diff = abs_diff.to(torch.float32) / (reference.to(torch.float32).abs() + 1e-12)
+    return abs_diff, rel_diff, mismatch, tolerance
+
+
+def mismatch_stats(generated: torch.Tensor, reference: torch.Tensor, tolerance_policy=None) -> Dict[str, Any]:
+    """GCR:731-771 without the sampling: the mismatch count, the row-major flat index of the first mismatch
+    (-1 if none), and the NaN-propagating max of abs_diff / rel_diff over the mismatches (None if none)."""
+    g = generated.detach().cpu().reshape(-1)
+    r = reference.detach().cpu().reshape(-1)
+    abs_diff, rel_diff, mismatch, _ = mismatch_parts(g, r, tolerance_policy)
+    count = int(mismatch.sum().item())
+    out = {"mismatch_count": count, "first_mismatch_index": _first_true(mismatch),
+           "mismatch_max_abs": None, "mismatch_max_rel": None}
+    if count:
+        out["mismatch_max_abs"] = float(abs_diff[mismatch].max().item())
+        out["mismatch_max_rel"] = float(rel_diff[mismatch].max().item())
+    return out
+
+
 def compare_tensors(
     generated: torch.Tensor,
     reference: torch.Tensor,
@@ -344,23 +382,7 @@ def compare_tensors(
     meta["cosine_similarity"] = cosine_similarity_meta(generated, reference, max_samples)
     meta["norm_ratio"] = norm_ratio_meta(generated, reference, max_samples)
 
-    policy = dtype_policy(reference, tolerance_policy)
-    if "max_abs_diff" in policy:
-        g = generated.to(torch.int32)
-        r = reference.to(torch.int32)
-        abs_diff = (g - r).abs()
-        mismatch = abs_diff > int(policy["max_abs_diff"])
-        tolerance = {"max_abs_diff": int(policy["max_abs_diff"])}
-    else:
-        g = generated.to(torch.float32)
-        r = reference.to(torch.float32)
-        abs_diff = (g - r).abs()
-        rtol = float(policy["rtol"])
-        atol = float(policy["atol"])
-        mismatch = ~torch.isclose(r, g, rtol=rtol, atol=atol)
-        tolerance = {"rtol": rtol, "atol": atol}
-
-    rel_diff = abs_diff.to(torch.float32) / (reference.to(torch.float32).abs() + 1e-12)
+    abs_diff, rel_diff, mismatch, tolerance = mismatch_parts(generated, reference, tolerance_policy)
     count = int(mismatch.sum().item())
     numel = int(reference.numel())
     allclose = bool(count == 0)

@@ -1,0 +1,219 @@
+"""The benchmark configurations at full size (C1-C4) on the device.
+
+Every record field that decomposes over elements is checked against the CPU
+oracle chunk by chunk (16 Mi elements at a time, merged in order): mismatch
+count and first index, maxima over the mismatches, global argmax of abs and
+rel diff, ULP histogram, NaN/Inf counts, finite-pattern violations, fp64
+sums.  The sampled fields (p99, sampled cosine and norm ratio) are checked
+against the oracle run on the strided sample itself, gathered on the device.
+Where the generator fixes a count (17 finite-pattern breaks, 1000 changed
+int8 positions), that count is asserted too.
+"""
+
+import math
+import sys
+
+import pytest
+import torch
+
+from golden_io import same_value
+from parity_util import SUM_RTOL, close
+from oracle import torch_verdict as tv
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+CHUNK = 1 << 24
+COUNT_FIELDS = ("mismatch_count", "nan_pairs", "finite_violations", "nan_gen", "nan_ref", "posinf_gen", "posinf_ref",
+                "neginf_gen", "neginf_ref")
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def kv():
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible: the gpu tests must run on the MI355X box")
+    from kernelverse_amd import _lib, verdict
+    _lib.load()
+    return verdict
+
+
+def _nan_max(a, b):
+    """torch's max over a concatenation: NaN if either part has one."""
+    if a is None:
+        return b
+    if b is None:
+        return a
+    if math.isnan(a) or math.isnan(b):
+        return float("nan")
+    return max(a, b)
+
+
+def _argmax_merge(best, cand):
+    """(value, index) pairs in index order: NaN is maximal, ties keep the earlier index."""
+    if best is None:
+        return cand
+    bv, cv = best[0], cand[0]
+    if math.isnan(bv):
+        return best
+    if math.isnan(cv) or cv > bv:
+        return cand
+    return best
+
+
+def chunked_oracle(g_dev, r_dev, tol):
+    """Oracle fields over all elements of a (possibly strided) device pair, 16 Mi elements at a time."""
+    gf, rf = g_dev.reshape(-1), r_dev.reshape(-1)
+    n = rf.numel()
+    out = {k: 0 for k in COUNT_FIELDS}
+    out.update(ulp_hist=[0] * tv.HIST_BUCKETS, first_mismatch_index=-1, first_finite_violation=-1,
+               mismatch_max_abs=None, mismatch_max_rel=None, sum_gg=0.0, sum_rr=0.0, sum_gr=0.0, sum_dd=0.0)
+    best_abs = best_rel = None
+    for s in range(0, n, CHUNK):
+        gc, rc = gf[s:s + CHUNK].cpu(), rf[s:s + CHUNK].cpu()
+        ext = tv.extension_record(gc, rc, tol)
+        mm = tv.mismatch_stats(gc, rc, tol)
+        for k in COUNT_FIELDS:
+            out[k] += (mm if k == "mismatch_count" else ext)[k]
+        out["ulp_hist"] = [a + b for a, b in zip(out["ulp_hist"], ext["ulp_hist"])]
+        if out["first_mismatch_index"] < 0 and mm["first_mismatch_index"] >= 0:
+            out["first_mismatch_index"] = s + mm["first_mismatch_index"]
+        if out["first_finite_violation"] < 0 and ext["first_finite_violation"] >= 0:
+            out["first_finite_violation"] = s + ext["first_finite_violation"]
+        out["mismatch_max_abs"] = _nan_max(out["mismatch_max_abs"], mm["mismatch_max_abs"])
+        out["mismatch_max_rel"] = _nan_max(out["mismatch_max_rel"], mm["mismatch_max_rel"])
+        best_abs = _argmax_merge(best_abs, (ext["max_abs"], s + ext["max_abs_index"]))
+        best_rel = _argmax_merge(best_rel, (ext["max_rel"], s + ext["max_rel_index"]))
+        for k in ("sum_gg", "sum_rr", "sum_gr", "sum_dd"):
+            out[k] += ext[k]
+    out["max_abs"], out["max_abs_index"] = best_abs
+    out["max_rel"], out["max_rel_index"] = best_rel
+    out["rel_l2"] = tv.rel_l2_from_sums(out["sum_dd"], out["sum_rr"])
+    out["cosine"] = tv.cosine_from_sums(out["sum_gr"], out["sum_gg"], out["sum_rr"])
+    return out
+
+
+def sampled_oracle(g_dev, r_dev, tol, m=tv.MAX_SAMPLES):
+    """p99 of abs/rel diff, sampled cosine and norm ratio: the oracle on the strided sample of GCR:338-348."""
+    gf, rf = g_dev.reshape(-1), r_dev.reshape(-1)
+    n = rf.numel()
+    if n > m:
+        idx = torch.arange(m, device=rf.device, dtype=torch.int64) * (n - 1) // (m - 1)
+        gf, rf = gf[idx], rf[idx]
+    gs, rs = gf.cpu(), rf.cpu()
+    abs_d, rel_d, _, _ = tv.mismatch_parts(gs, rs, tol)
+    return {"p99_abs": tv.p99_meta(abs_d), "p99_rel": tv.p99_meta(rel_d),
+            "sample_cosine": tv.cosine_similarity_meta(gs, rs), "sample_norm_ratio": tv.norm_ratio_meta(gs, rs)}
+
+
+def check_record(rec, g_dev, r_dev, tol):
+    exp = chunked_oracle(g_dev, r_dev, tol)
+    bad = []
+    exact = COUNT_FIELDS + ("ulp_hist", "first_mismatch_index", "first_finite_violation", "max_abs_index",
+                            "max_rel_index")
+    for k in exact:
+        if not same_value(rec[k], exp[k]):
+            bad.append(f"{k}: device {rec[k]!r} != oracle {exp[k]!r}")
+    for k in ("max_abs", "max_rel"):
+        if not same_value(float(rec[k]), float(exp[k])):
+            bad.append(f"{k}: device {rec[k]!r} != oracle {exp[k]!r}")
+    if exp["mismatch_count"]:
+        for k in ("mismatch_max_abs", "mismatch_max_rel"):
+            if not same_value(float(rec[k]), float(exp[k])):
+                bad.append(f"{k}: device {rec[k]!r} != oracle {exp[k]!r}")
+    for k in ("sum_gg", "sum_rr", "sum_gr", "sum_dd", "rel_l2", "cosine"):
+        if not close(rec[k], exp[k], SUM_RTOL):
+            bad.append(f"{k}: device {rec[k]!r} vs oracle {exp[k]!r}")
+    smp = sampled_oracle(g_dev, r_dev, tol)
+    for k in ("p99_abs", "p99_rel"):
+        if not same_value(float(rec[k]), float(smp[k])):
+            bad.append(f"{k}: device {rec[k]!r} != oracle {smp[k]!r}")
+    # the meta rounds these to 4 places; the unrounded values agree to 1e-6
+    for k in ("sample_cosine", "sample_norm_ratio"):
+        if smp[k] is None or same_value(float(rec[k]), float(smp[k])):
+            continue
+        if not (abs(round(rec[k], 4) - smp[k]) <= 1e-4 + 1e-12):
+            bad.append(f"{k}: device {rec[k]!r} vs oracle {smp[k]!r}")
+    n = r_dev.numel()
+    if sum(rec["ulp_hist"]) + rec["nan_pairs"] != n:
+        bad.append("ulp_hist + nan_pairs != numel")
+    return bad, exp
+
+
+def test_c1_bf16_256mi(kv):
+    from kernelverse_amd import synth
+    _say("C1 bf16 268,435,456")
+    g, r = synth.c1_pair(DEV)
+    tol = {"BF16": {"rtol": 1.6e-2, "atol": 1e-2}}
+    rec = kv.verdict_record(g, r, tolerance_policy=tol)
+    bad, exp = check_record(rec, g, r, tol)
+    assert not bad, bad
+    # by construction: only 1-ULP and 3-ULP steps, no non-finite values
+    assert rec["ulp_hist"][3:] == [0] * 13 and rec["nan_pairs"] == 0 and rec["finite_violations"] == 0
+    assert 0.049 < rec["ulp_hist"][1] / rec["numel"] < 0.051
+    assert 0.8e-4 < rec["ulp_hist"][2] / rec["numel"] < 1.2e-4
+
+
+def test_c2_fp16_strided(kv):
+    from kernelverse_amd import synth
+    _say("C2 fp16 4096x32768 stride 32896")
+    g, r = synth.c2_pair(DEV)
+    assert not g.is_contiguous() and g.stride() == (32896, 1)
+    tol = {"FP16": {"rtol": 1e-3, "atol": 1e-3}}
+    rec = kv.verdict_record(g, r, tolerance_policy=tol)
+    bad, _ = check_record(rec, g, r, tol)
+    assert not bad, bad
+    assert rec["finite_violations"] == 17
+
+
+def test_c3_fp8_codes(kv):
+    from kernelverse_amd import synth
+    _say("C3 fp8 e4m3fn 134,217,728")
+    g, r = synth.c3_fp8_pair(DEV)
+    rec = kv.verdict_record(g, r)
+    bad, _ = check_record(rec, g, r, None)
+    assert not bad, bad
+    changed = int((g.view(torch.uint8) != r.view(torch.uint8)).sum().item())
+    assert rec["ulp_hist"][1] == changed and sum(rec["ulp_hist"][2:]) == 0
+
+
+def test_c3_int8_equality(kv):
+    from kernelverse_amd import synth
+    _say("C3 int8 134,217,728")
+    g, r = synth.c3_int8_pair(DEV)
+    rec = kv.verdict_record(g, r)
+    bad, _ = check_record(rec, g, r, None)
+    assert not bad, bad
+    assert rec["mismatch_count"] == 1000
+    assert rec["ulp_hist"][0] == r.numel() - 1000
+
+
+def test_c4_ragged_batch(kv):
+    from kernelverse_amd import synth
+    _say("C4 4096 ragged pairs")
+    pairs = synth.c4_batch(DEV)
+    tol_all = {}
+    for _, _, t in pairs:
+        tol_all.update(t)
+    # one batched call; the tolerance table is per dtype, so each pair gets its own
+    got = kv.verdict_records([(g, r) for g, r, _ in pairs], tolerance_policy=tol_all)
+    recs = list(enumerate(got))
+    assert len(recs) == len(pairs)
+    # every 97th pair against the oracle, every 16th against a single-pair device call
+    for i, rec in recs[::97]:
+        g, r, tol = pairs[i]
+        bad, _ = check_record(rec, g, r, tol)
+        assert not bad, (i, g.numel(), g.dtype, bad)
+    for i, rec in recs[::16]:
+        g, r, tol = pairs[i]
+        single = kv.verdict_record(g, r, tolerance_policy=tol)
+        # the fp64 sums depend on how the launch cut the pair into runs (1e-6 contract); all else is exact
+        summed = ("sample_sum_gg", "sample_sum_rr", "sample_sum_gr", "sample_cosine", "sample_norm_ratio",
+                  "sum_gg", "sum_rr", "sum_gr", "sum_dd", "rel_l2", "cosine")
+        diff = [k for k in single if k not in summed and not same_value(single[k], rec[k])]
+        diff += [k for k in summed if not close(single[k], rec[k], SUM_RTOL)]
+        assert not diff, (i, diff)
