@@ -23,21 +23,34 @@ verdict of KernelVerse ``runner/generated_correctness_runner.py`` (GCR):
 * ``compare_tensors``         GCR:672-786
 * ``compare_outputs``         GCR:789-833
 
+* ``mismatch_parts`` / ``mismatch_stats``  GCR:712-771 (the abs/rel diff,
+  mismatch mask, count, maxima over the mismatches and first index, factored
+  out of ``compare_tensors`` so tests can merge them over chunks)
+
 and the policy helpers of ``runner/correctness_policy.py`` (CP:146-179) that
 those functions call.  The arithmetic is torch's own (torch 2.10 CPU), which
-is what the reference runs; the library routines it relies on
-(``torch.isclose``, ``torch.quantile``, ``Tensor.max``, ``torch.argmax``) are
-pinned against closed forms and brute force in ``tests/test_oracle.py``, and
-the branching/reporting logic is pinned against fixtures written by the
-reference itself (``tests/golden/``).
+is what the reference runs (``torch.isclose``, ``torch.quantile``,
+``Tensor.max``, ``torch.argmax``; torch is the reference's unpinned
+third-party dependency, requirements.txt:1-2).
 
-``extension_record`` computes the builder-defined fields that the reference
-does not have (north-star extensions): max abs/rel error over all elements with
-argmax, a 16-bucket ULP-distance histogram, fp64 sums for relative-L2 and
-full-tensor cosine, NaN/Inf class counts and finite-pattern violation counts.
-Their definitions are declared here, not derived from the reference; every one
-of them is pinned by brute force (pure-Python loops on small inputs) and closed
-forms in ``tests/test_oracle.py``.
+How each part is pinned:
+
+* every function restating GCR/CP: against fixtures that the reference itself
+  wrote in this container (``tests/golden/make_golden.py``; 51 verdict cases
+  covering every dtype family, strided and 0-d inputs, empty tensors, shape and
+  dtype mismatches, NaN/Inf tables, sampling above 1,000,000 elements, all
+  three policies, nested outputs, and the float8 error), compared key by key
+  in ``tests/test_oracle_golden.py``; ``mismatch_stats`` and the finite-pattern
+  count against the same fixtures in ``tests/test_oracle_properties.py``;
+* ``extension_record`` (the builder-defined fields that the reference does
+  not have: max abs/rel error over all elements with argmax, a 16-bucket
+  ULP-distance histogram, fp64 sums for relative-L2 and full-tensor cosine,
+  NaN/Inf class counts and finite-pattern violation counts): the argmax is
+  ``torch.argmax`` itself; the ULP distance against an independent method
+  (rank distance in the sorted list of all finite values, over every code of
+  fp16, bf16 and both fp8 formats; nextafter stepping for fp32); the sums and
+  derived ratios against closed forms (identical inputs, g = -r, g = 2r, zero
+  vectors) -- all in ``tests/test_oracle_properties.py``.
 """
 
 from __future__ import annotations
