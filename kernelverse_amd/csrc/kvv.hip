@@ -207,7 +207,19 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
     const uint64_t num = (uint64_t)n - 1, den = (uint64_t)d.m - 1;
     d.s_div = num / den;
     d.s_mod = num % den;
-    d.s_inv = 1.0 / (double)den;
+    // floor(t / den) = mulhi(t, s_magic) >> s_shift for every t < 64 * den (the
+    // cursor's dividends): with l = ceil(log2 den) and N = max(6 + l, 32 - l),
+    // magic = ceil(2^(N+l) / den) < 2^32 and the rounding error stays below 1/den.
+    d.s_magic = 0;
+    d.s_shift = 0;
+    if (den > 1) {
+      int l = 0;
+      while ((1ull << l) < den) ++l;
+      const int N = 6 + l > 32 - l ? 6 + l : 32 - l;
+      const int k = N + l;
+      d.s_magic = (uint32_t)(((1ull << k) + den - 1) / den);
+      d.s_shift = (uint32_t)(k - 32);
+    }
   }
   return KVV_OK;
 }

@@ -37,8 +37,8 @@ constexpr int kSlotWords = kMisc + 64;
 enum Layout { L_CONTIG = 0, L_ROWS = 1, L_GENERIC = 2 };
 enum ScanKind { K_CONTIG = 0, K_ROWS = 1, K_SCALAR = 2 };
 
-// Wave-level counters kept in LDS (one row per wave).
-enum WaveCounter { WC_MISM = LC_COUNT, WC_COUNT };
+// Wave-level counters kept in LDS (one row per wave): the LdsCounter set.
+constexpr int WC_COUNT = LC_COUNT;
 
 struct Dims {
   int32_t ndim;
@@ -63,7 +63,8 @@ struct SegDesc {
   int64_t run_base;       // first item of the scan launch holding this segment
   int64_t run_ipb;        // items per block of that launch
   uint64_t s_div, s_mod;  // (n-1) = s_div*(m-1) + s_mod: sample i sits at i*s_div + floor(i*s_mod/(m-1))
-  double s_inv;           // 1/(m-1)
+  uint32_t s_magic;       // floor(t/(m-1)) = mulhi(t, s_magic) >> s_shift for t < 64*(m-1)
+  uint32_t s_shift;
   int32_t layout;         // enum Layout
   int32_t vec;            // 16-byte vector access allowed
   int32_t mode;           // enum kvv_mode
@@ -115,6 +116,7 @@ struct Acc {
   uint32_t mm_abs, mm_rel;
   uint32_t gabs_k, grel_k;
   uint32_t nfast;          // bit-identical finite pairs (ULP bucket 0, never a mismatch)
+  uint32_t nmm;            // mismatches
   uint32_t nnear_fast;     // ... of which near zero
   float rel_thr;           // rel-max filter: only rel >= ~rel_thr can still win
   uint64_t first_mm, first_viol;
@@ -125,7 +127,7 @@ struct Acc {
   __device__ void init() {
     mm_abs = mm_rel = 0;
     gabs_k = grel_k = 0;
-    nfast = nnear_fast = 0;
+    nfast = nnear_fast = nmm = 0;
     rel_thr = -__builtin_inff();
     first_mm = first_viol = kNone;
     gabs_i = grel_i = kNone;
@@ -216,12 +218,26 @@ __device__ __forceinline__ void elem_test(typename Elem<DT>::T gc, typename Elem
 }
 
 // Lower bound below which a rel_diff can no longer beat `best` (conservative:
-// the caller skips an element only when abs_diff < thr * (|r| + 1e-12)).
+// the caller skips an element only when abs_diff < thr * (|r| + 1e-12)).  A
+// best of +inf keeps a finite bound: a finite abs_diff over a small enough
+// denominator also divides to +inf, and such a tie at a lower index must be
+// seen.  NaN (the largest key) admits only NaN and +-inf abs_diff, for which
+// the comparison fails.
 __device__ __forceinline__ float rel_threshold(float best) {
   if (best != best) return __builtin_inff();
+  if (best == __builtin_inff()) return 3.4028234e38f * 0.99999f;
   if (best > 0.0f) return best * 0.99999f;
   if (best < 0.0f) return best * 1.00001f;
   return 0.0f;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float w = __shfl_xor(v, o);
+    v = w > v ? w : v;
+  }
+  return v;
 }
 
 // Full treatment of one element for the lanes with `act` set.  Every lane of
@@ -236,7 +252,7 @@ __device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem
   elem_test<DT, MODE>(gc, rc, d, adf, abs_key, mm, rf);
   const float den = fabsf(rf) + 1e-12f;
   mm = mm && act;
-  wave_add(wc, WC_MISM, mm);
+  acc.nmm += mm ? 1u : 0u;
   if (mm) {
     const float rel = adf / den;
     const uint32_t rk = fkey(rel);
@@ -248,15 +264,21 @@ __device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem
     acc.gabs_k = abs_key;
     acc.gabs_i = idx;
   }
+  // rel argmax: an element below the wave's best so far cannot be the argmax,
+  // so the bound is shared by the wave's lanes (the division is then rare)
+  bool raised = false;
   if (act && !(adf < acc.rel_thr * den)) {
     const float rel = adf / den;
     const uint32_t rk = fkey(rel);
     if (better(rk, idx, acc.grel_k, acc.grel_i)) {
       acc.grel_k = rk;
       acc.grel_i = idx;
-      acc.rel_thr = rel_threshold(rel);
+      const float t = rel_threshold(rel);
+      raised = !(t <= acc.rel_thr);
+      acc.rel_thr = raised ? t : acc.rel_thr;
     }
   }
+  if (__ballot(raised)) acc.rel_thr = wave_max_f32(acc.rel_thr);
   bool nan_pair = false;
   if constexpr (E::is_float) {
     const bool nf = act && !(E::finite(gc) && E::finite(rc));
@@ -362,6 +384,23 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint4 nt_load16(const void* p) {
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// The item's LDS stage, addressed as LDS explicitly: reads of it must stay
+// ds_read instructions.  Through a generic pointer the compiler may merge an
+// LDS read and a global read of the same value into one flat load, whose wait
+// also waits for the next item's loads in flight.
+#define KVV_LDS __attribute__((address_space(3)))
+typedef const KVV_LDS uint4* StageP;
+
+template <typename T>
+__device__ __forceinline__ T stage_elem(StageP stage, int slot, int e) {
+  return ((const KVV_LDS T*)(stage + slot))[e];
+}
+
+__device__ __forceinline__ uint4 stage_vec(StageP stage, int slot) {
+  const u32x4 v = *(const KVV_LDS u32x4*)(stage + slot);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
@@ -560,11 +599,27 @@ __device__ __forceinline__ void dword_fast_sums(uint32_t gz, float nz_abs, doubl
   }
 }
 
+// Lowest logical index of a fast element of the item (vectors in order, then
+// elements): an abs/rel argmax candidate of value 0 until a positive one exists.
+template <int DT>
+__device__ __forceinline__ void track_first_fast(int64_t L0, uint32_t full, uint64_t slow, Acc& acc) {
+  constexpr int V = VecIO<DT>::V;
+  uint64_t ff = acc.first_fast;
+  for (int p = 0; p < V * kUnroll; ++p) {
+    int u, e;
+    slot_of<Elem<DT>::width>(p, u, e);
+    if (!((full >> u) & 1u) || ((slow >> p) & 1u)) continue;
+    const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + (int)threadIdx.x) * V + e);
+    if (idx < ff) ff = idx;
+  }
+  acc.first_fast = ff;
+}
+
 // Phase A over the stage copy of one item: bit-identical finite pairs are
 // finished here (count; g*g into e_sq, which feeds gg, rr and gr since g == r);
 // returns the lane's slow mask in the layout above.
-template <int DT, bool NEAR, bool TRACK>
-__device__ __forceinline__ uint64_t phase_a(const SegDesc& d, int64_t L0, const uint4* stage, uint32_t full,
+template <int DT, bool NEAR>
+__device__ __forceinline__ uint64_t phase_a(const SegDesc& d, int64_t L0, StageP stage, uint32_t full,
                                             Acc& acc) {
   using E = Elem<DT>;
   using IO = VecIO<DT>;
@@ -579,8 +634,8 @@ __device__ __forceinline__ uint64_t phase_a(const SegDesc& d, int64_t L0, const 
   for (int u = 0; u < kUnroll; ++u) {
     if (!((full >> u) & 1u)) continue;
     ++nvec;
-    const uint4 gq = stage[(2 * u) * kBlock + tid];
-    const uint4 rq = stage[(2 * u + 1) * kBlock + tid];
+    const uint4 gq = stage_vec(stage, (2 * u) * kBlock + tid);
+    const uint4 rq = stage_vec(stage, (2 * u + 1) * kBlock + tid);
     const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w};
     const uint32_t rw[4] = {rq.x, rq.y, rq.z, rq.w};
     if constexpr (W == 64) {
@@ -619,18 +674,137 @@ __device__ __forceinline__ uint64_t phase_a(const SegDesc& d, int64_t L0, const 
     // zeroed slow elements were counted as near when 0 <= nz_abs
     acc.nnear_fast += nnear - (0.0f <= nz_abs ? nslow : 0u);
   }
-  if constexpr (TRACK) {
-    // lowest logical index of a fast element (vectors in order, then elements)
-    uint64_t ff = acc.first_fast;
-    for (int p = 0; p < V * kUnroll; ++p) {
-      int u, e;
-      slot_of<W>(p, u, e);
-      if (!((full >> u) & 1u) || ((slow >> p) & 1u)) continue;
-      const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + tid) * V + e);
-      if (idx < ff) ff = idx;
-    }
-    acc.first_fast = ff;
+  return slow;
+}
+
+// ------------------------------------------------------------ phase A, dot form
+// For 8- and 16-bit codes the squares of the bit-identical pairs are summed
+// with the packed dot instructions (two bf16/f16 squares, or four int8 squares,
+// per instruction) instead of one fp64 multiply-add per element.
+//
+// * bf16 / f16 (v_dot2_f32_bf16 / v_dot2_f32_f16): products of two 8- or
+//   11-bit significands are exact in fp32; each instruction then rounds the
+//   (non-negative) sum downward by at most 1.5 ulp (measured over 2^20 cases per
+//   format).  Every accumulator takes kUnroll instructions, so a lane's partial
+//   sum is low by at most 4 * 1.5 * 2^-23 < 7.2e-7 relative before it joins the
+//   fp64 accumulator.
+// * f8 codes become f16 halves: e5m2 is the high byte of an f16; e4m3fn's
+//   magnitude bits placed at bits 7..13 of an f16 read as value * 2^-8 (the
+//   sum is scaled back by 2^16, exactly).  Signs do not matter for squares.
+// * int8 / uint8 (v_dot4_i32_i8 / v_dot4_u32_u8): exact integer sums.
+//
+// Bit-identical is the only test of the quick form: a lane whose partial sum is
+// not finite (an identical NaN or Inf pair, or a bf16 square beyond fp32's
+// range), or is below 2^-60 while its values are not all zero (a bf16 square
+// below fp32's normal range), re-runs the item with the exact per-element
+// classification and fp64 squares (phase_a).  The careful form (CAREFUL) also
+// tests finiteness per element, as phase_a does, so only bf16's range can
+// still send a lane to phase_a; a wave uses it for a few items after a re-run
+// (data with scattered NaN/Inf).  e4m3fn has no infinity and its NaN code is
+// part of the identity test, so it never re-runs.
+template <int DT>
+struct DotForm {
+  static constexpr bool on = DT == KVV_BF16 || DT == KVV_F16 || DT == KVV_F8E4M3FN || DT == KVV_F8E5M2 ||
+                             DT == KVV_I8 || DT == KVV_U8;
+  static constexpr bool is_int = DT == KVV_I8 || DT == KVV_U8;
+  static constexpr int NA = Elem<DT>::width == 8 && !is_int ? 8 : 4;  // accumulators per lane
+  using A = typename std::conditional<is_int, int32_t, float>::type;
+};
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_sq_f16(uint32_t h, float a) {
+  const f16x2_t v = __builtin_bit_cast(f16x2_t, h);
+  return __builtin_amdgcn_fdot2(v, v, a, false);
+}
+
+// Adds the squares of the (zeroed-where-slow) codes of dword j into the accumulators.
+template <int DT>
+__device__ __forceinline__ void dot_sq(uint32_t z, typename DotForm<DT>::A* a, int j) {
+  if constexpr (DT == KVV_BF16) {
+    const bf16x2_t v = __builtin_bit_cast(bf16x2_t, z);
+    a[j] = __builtin_amdgcn_fdot2_f32_bf16(v, v, a[j], false);
+  } else if constexpr (DT == KVV_F16) {
+    a[j] = dot2_sq_f16(z, a[j]);
+  } else if constexpr (DT == KVV_F8E5M2) {
+    a[j] = dot2_sq_f16((z << 8) & 0xFF00FF00u, a[j]);     // bytes 0 and 2
+    a[j + 4] = dot2_sq_f16(z & 0xFF00FF00u, a[j + 4]);    // bytes 1 and 3
+  } else if constexpr (DT == KVV_F8E4M3FN) {
+    a[j] = dot2_sq_f16((z << 7) & 0x3F803F80u, a[j]);     // bytes 0 and 2, value * 2^-8
+    a[j + 4] = dot2_sq_f16((z >> 1) & 0x3F803F80u, a[j + 4]);  // bytes 1 and 3
+  } else if constexpr (DT == KVV_I8) {
+    a[j] = __builtin_amdgcn_sdot4((int)z, (int)z, a[j], false);
+  } else {
+    a[j] = (int32_t)__builtin_amdgcn_udot4(z, z, (uint32_t)a[j], false);
   }
+}
+
+// Per-element slow flags (layout of dword_flags) from bitwise identity alone;
+// for e4m3fn also the NaN code, which the f16 mapping above would not expose.
+template <int DT>
+__device__ __forceinline__ uint32_t ident_flags(uint32_t g, uint32_t r) {
+  if constexpr (Elem<DT>::width == 8) {
+    const uint32_t x = g ^ r;
+    uint32_t t = ((x & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | x;
+    if constexpr (DT == KVV_F8E4M3FN) t |= (g & 0x7F7F7F7Fu) + 0x01010101u;
+    return (t >> 7) & 0x01010101u;
+  } else {
+    return pk_nonzero16(g ^ r);
+  }
+}
+
+template <int DT, bool CAREFUL>
+__device__ __forceinline__ uint64_t phase_a_dot(const SegDesc& d, int64_t L0, StageP stage, uint32_t full,
+                                                Acc& acc, bool& redone) {
+  using DF = DotForm<DT>;
+  using A = typename DF::A;
+  constexpr int V = VecIO<DT>::V;
+  constexpr int W = Elem<DT>::width;
+  const int tid = threadIdx.x;
+  uint32_t m0 = 0, m1 = 0, orz = 0;
+  A a[DF::NA];
+#pragma unroll
+  for (int k = 0; k < DF::NA; ++k) a[k] = 0;
+  // vectors that were not full loads hold zeros in the stage (load_item): they
+  // read as identical pairs of squares 0 and are left out of the count below
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint4 gq = stage_vec(stage, (2 * u) * kBlock + tid);
+    const uint4 rq = stage_vec(stage, (2 * u + 1) * kBlock + tid);
+    const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w};
+    const uint32_t rw[4] = {rq.x, rq.y, rq.z, rq.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int dd = u * 4 + j;
+      const uint32_t f = CAREFUL ? dword_flags<DT>(gw[j], rw[j]) : ident_flags<DT>(gw[j], rw[j]);
+      if constexpr (W == 8) {
+        if (dd < 8) m0 |= f << dd; else m1 |= f << (dd - 8);
+      } else {
+        m0 |= f << dd;
+      }
+      const uint32_t z = gw[j] & ~flag_mask<W>(f);
+      if constexpr (DT == KVV_BF16) orz |= z;
+      dot_sq<DT>(z, a, j);
+    }
+  }
+  bool redo = false;
+  if constexpr (!DF::is_int && DT != KVV_F8E4M3FN) {
+    float t = 0.0f;
+#pragma unroll
+    for (int k = 0; k < DF::NA; ++k) t += a[k];
+    redo = !(t <= 3.4028234e38f);
+    if constexpr (DT == KVV_BF16) redo = redo || (t < 0x1p-60f && (orz & 0x7FFF7FFFu) != 0u);
+  }
+  redone = __ballot(redo) != 0;
+  if (redone && redo) return phase_a<DT, false>(d, L0, stage, full, acc);
+  const uint64_t slow = ((uint64_t)m1 << 32) | m0;
+  double e = 0.0;
+#pragma unroll
+  for (int k = 0; k < DF::NA; ++k) e += (double)a[k];
+  if constexpr (DT == KVV_F8E4M3FN) e *= 65536.0;
+  acc.e_sq += e;
+  acc.nfast += (uint32_t)__popc(full) * V - (uint32_t)__popcll(slow);
   return slow;
 }
 
@@ -639,22 +813,30 @@ __device__ __forceinline__ uint64_t phase_a(const SegDesc& d, int64_t L0, const 
 template <int NE>
 __device__ __forceinline__ uint32_t build_queue(uint64_t slow, uint16_t* queue) {
   const int lane = lane_id();
+  // a lane holds at most NE entries (slots 0..NE-1) and the queue has room for 64 * NE
+  if constexpr (NE < 64) slow &= (1ull << NE) - 1;
   const uint32_t cnt = (uint32_t)__popcll(slow);
   const uint32_t incl = wave_incl_scan(cnt);
   const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
   uint32_t at = incl - cnt;
-  while (slow) {
-    const int k = __builtin_ctzll(slow);
-    slow &= slow - 1;
-    if (at < 64u * NE) queue[at] = (uint16_t)((lane << 6) | k);
-    ++at;
+  if constexpr (NE <= 32) {
+    uint32_t m = (uint32_t)slow;
+    while (m) {
+      queue[at++] = (uint16_t)((lane << 6) | __builtin_ctz(m));
+      m &= m - 1;
+    }
+  } else {
+    while (slow) {
+      queue[at++] = (uint16_t)((lane << 6) | __builtin_ctzll(slow));
+      slow &= slow - 1;
+    }
   }
-  return total < 64u * NE ? total : 64u * NE;
+  return total;
 }
 
 // Phase B: the wave's queued elements, 64 at a time, from the LDS stage.
 template <int DT, int MODE>
-__device__ __forceinline__ void phase_b(const SegDesc& d, int64_t L0, uint32_t total, const uint4* stage,
+__device__ __forceinline__ void phase_b(const SegDesc& d, int64_t L0, uint32_t total, StageP stage,
                                         const uint16_t* queue, Acc& acc, uint32_t* wc) {
   using IO = VecIO<DT>;
   using T = typename IO::T;
@@ -671,8 +853,8 @@ __device__ __forceinline__ void phase_b(const SegDesc& d, int64_t L0, uint32_t t
     int u, e;
     slot_of<Elem<DT>::width>((int)(ent & 63), u, e);
     const int t = w * 64 + src;
-    const T gc = reinterpret_cast<const T*>(&stage[(2 * u) * kBlock + t])[e];
-    const T rc = reinterpret_cast<const T*>(&stage[(2 * u + 1) * kBlock + t])[e];
+    const T gc = stage_elem<T>(stage, (2 * u) * kBlock + t, e);
+    const T rc = stage_elem<T>(stage, (2 * u + 1) * kBlock + t, e);
     const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + t) * V + e);
     slow_elem<DT, MODE>(gc, rc, act, idx, d, acc, wc);
   }
@@ -705,7 +887,7 @@ __device__ __forceinline__ SampleCursor cursor_at(const SegDesc& d, int64_t L0) 
 // The pair at logical index idx of a vector item: from the stage when its
 // vector was a full 16-byte load, else (partial last vector) from memory.
 template <int DT>
-__device__ __forceinline__ void stage_pair(const SegDesc& d, int64_t L0, int64_t L1, int64_t idx, const uint4* stage,
+__device__ __forceinline__ void stage_pair(const SegDesc& d, int64_t L0, int64_t L1, int64_t idx, StageP stage,
                                            typename Elem<DT>::T& gc, typename Elem<DT>::T& rc) {
   using IO = VecIO<DT>;
   using T = typename IO::T;
@@ -715,8 +897,8 @@ __device__ __forceinline__ void stage_pair(const SegDesc& d, int64_t L0, int64_t
   if (vstart + V <= L1) {
     const int vec = (int)(q / V);
     const int u = vec / kBlock, t = vec % kBlock, e = (int)(q % V);
-    gc = reinterpret_cast<const T*>(&stage[(2 * u) * kBlock + t])[e];
-    rc = reinterpret_cast<const T*>(&stage[(2 * u + 1) * kBlock + t])[e];
+    gc = stage_elem<T>(stage, (2 * u) * kBlock + t, e);
+    rc = stage_elem<T>(stage, (2 * u + 1) * kBlock + t, e);
   } else {
     int64_t og, orr;
     elem_offsets(d, idx, og, orr);
@@ -725,33 +907,62 @@ __device__ __forceinline__ void stage_pair(const SegDesc& d, int64_t L0, int64_t
   }
 }
 
+// abs_diff and rel_diff of one sampled pair; its values join the sampled fp64 sums.
 template <int DT, int MODE>
-__device__ __forceinline__ void sample_write(const SegDesc& d, typename Elem<DT>::T gc, typename Elem<DT>::T rc,
-                                             uint64_t i, Acc& acc, float* sabs, float* srel) {
+__device__ __forceinline__ void sample_value(const SegDesc& d, typename Elem<DT>::T gc, typename Elem<DT>::T rc,
+                                             Acc& acc, float& adf, float& rel) {
   using E = Elem<DT>;
-  float adf, rf;
+  float rf;
   uint32_t kk;
   bool mm;
   elem_test<DT, MODE>(gc, rc, d, adf, kk, mm, rf);
-  sabs[d.sample_off + i] = adf;
-  srel[d.sample_off + i] = adf / (fabsf(rf) + 1e-12f);
+  // abs_diff == 0 leaves rel_diff == +0 (the denominator is then finite and positive)
+  rel = adf == 0.0f ? 0.0f : adf / (fabsf(rf) + 1e-12f);
   const double g64 = E::f64(gc), r64 = E::f64(rc);
   acc.s[4] = fma(g64, g64, acc.s[4]);
   acc.s[5] = fma(r64, r64, acc.s[5]);
   acc.s[6] = fma(g64, r64, acc.s[6]);
 }
 
+template <int DT, int MODE>
+__device__ __forceinline__ void sample_write(const SegDesc& d, typename Elem<DT>::T gc, typename Elem<DT>::T rc,
+                                             uint64_t i, Acc& acc, float* sabs, float* srel) {
+  float adf, rel;
+  sample_value<DT, MODE>(d, gc, rc, acc, adf, rel);
+  sabs[d.sample_off + i] = adf;
+  srel[d.sample_off + i] = rel;
+}
+
+// The sample a lane computed in the last cursor step of an item.  It is stored
+// at the next item, after that item's stage write and before its loads are
+// issued: a store issued after the loads would make the wait for them (vmcnt
+// counts loads and stores in issue order) wait for the store as well.
+struct PendingSample {
+  uint64_t at;  // position in the sample arrays, kNone if none
+  float abs, rel;
+};
+
+__device__ __forceinline__ void store_pending(PendingSample& p, float* sabs, float* srel) {
+  if (p.at != kNone) {
+    sabs[p.at] = p.abs;
+    srel[p.at] = p.rel;
+    p.at = kNone;
+  }
+}
+
 // Samples of a vector item (GCR:346-347).  Every wave walks the same cursor, 64
 // samples per step (lane l takes sample cursor.i + l), and a lane handles its
 // sample only when the element sits in its own wave's stage slots, so no
-// barrier is needed.  When n <= max_samples every element is a sample and each
-// lane simply takes its own slots.
+// barrier is needed.  Positions inside a full item are 32-bit offsets from L0.
+// When n <= max_samples every element is a sample and each lane simply takes
+// its own slots.
 template <int DT, int MODE>
-__device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_t L1, const uint4* stage, Acc& acc,
-                                            float* sabs, float* srel, SampleCursor& cur) {
+__device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_t L1, StageP stage, Acc& acc,
+                                            float* sabs, float* srel, SampleCursor& cur, PendingSample& pend) {
   using IO = VecIO<DT>;
   using T = typename IO::T;
   constexpr int V = IO::V;
+  constexpr int LV = V == 16 ? 4 : (V == 8 ? 3 : (V == 4 ? 2 : 1));  // log2(V)
   const int lane = lane_id(), w = threadIdx.x >> 6;
   if (d.n <= d.max_samples) {
 #pragma unroll 1
@@ -767,48 +978,58 @@ __device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_
     return;
   }
   const uint32_t den = (uint32_t)(d.m - 1);
+  const uint32_t len = (uint32_t)(L1 - L0);
+  const bool whole = len == (uint32_t)(kUnroll * kBlock * V);  // every vector of the item is a full load
+  // lane * s_div only matters while it stays inside the item; clamping keeps the
+  // 32-bit offsets exact for the lanes that can be in range
+  const uint32_t sdiv = d.s_div < (1ull << 20) ? (uint32_t)d.s_div : (1u << 20);
+  const uint32_t smod = (uint32_t)d.s_mod;
   for (;;) {
     if (cur.i >= (uint64_t)d.m || cur.idx >= (uint64_t)L1) return;
-    const uint32_t t = cur.rem + (uint32_t)lane * (uint32_t)d.s_mod;  // < 64 * den < 2^30
-    uint32_t q = (uint32_t)((double)t * d.s_inv);
-    if (q * den > t) --q;
-    if ((q + 1) * den <= t) ++q;
+    const uint64_t left = (uint64_t)d.m - cur.i;
+    const uint32_t t = cur.rem + (uint32_t)lane * smod;  // < 64 * den < 2^30
+    const uint32_t q = __umulhi(t, d.s_magic) >> d.s_shift;
     const uint32_t rem = t - q * den;
-    const uint64_t i = cur.i + (uint64_t)lane;
-    const uint64_t idx = cur.idx + (uint64_t)lane * d.s_div + q;
-    const bool in = i < (uint64_t)d.m && idx < (uint64_t)L1;
-    if (in) {
-      const int64_t qq = (int64_t)idx - L0;
-      const int owner = (int)((qq / V) % kBlock) >> 6;
-      if (owner == w) {
-        T gc, rc;
-        stage_pair<DT>(d, L0, L1, (int64_t)idx, stage, gc, rc);
-        sample_write<DT, MODE>(d, gc, rc, i, acc, sabs, srel);
+    const uint32_t off = (uint32_t)(cur.idx - (uint64_t)L0) + (uint32_t)lane * sdiv + q;
+    const bool in = (uint64_t)lane < left && off < len;
+    // the in-range lanes are a prefix; the cursor moves past the last of them
+    const int c = (int)__popcll(__ballot(in));
+    if (c == 0) return;
+    const uint32_t vi = off >> LV;
+    if (in && ((vi >> 6) & 3u) == (uint32_t)w) {
+      T gc, rc;
+      if (whole) {
+        const int u = (int)(vi >> 8), tt = (int)(vi & 255u), e = (int)(off & (V - 1));
+        gc = stage_elem<T>(stage, (2 * u) * kBlock + tt, e);
+        rc = stage_elem<T>(stage, (2 * u + 1) * kBlock + tt, e);
+      } else {
+        stage_pair<DT>(d, L0, L1, L0 + (int64_t)off, stage, gc, rc);
+      }
+      float adf, rel;
+      sample_value<DT, MODE>(d, gc, rc, acc, adf, rel);
+      const uint64_t at = d.sample_off + cur.i + (uint64_t)lane;
+      if (c < 64) {
+        // the item's last step: held until the next item (the lane's previous
+        // pending sample was stored at this item's start)
+        pend.at = at;
+        pend.abs = adf;
+        pend.rel = rel;
+      } else {
+        sabs[at] = adf;
+        srel[at] = rel;
       }
     }
-    const uint64_t inb = __ballot(in);
-    const int c = (int)__popcll(inb);  // the in-range lanes are a prefix
-    if (c < 64) {
-      // the first out-of-range lane holds the next sample
-      cur.i += (uint64_t)c;
-      cur.idx = (uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)idx, c) |
-                ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(idx >> 32), c) << 32);
-      cur.rem = (uint32_t)__builtin_amdgcn_readlane((int)rem, c);
-      return;
-    }
-    // all 64 in range: step past lane 63
-    const uint64_t idx63 = (uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)idx, 63) |
-                           ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(idx >> 32), 63) << 32);
-    const uint32_t rem63 = (uint32_t)__builtin_amdgcn_readlane((int)rem, 63);
-    uint32_t nr = rem63 + (uint32_t)d.s_mod;
-    uint64_t nidx = idx63 + d.s_div;
+    const uint32_t offl = (uint32_t)__builtin_amdgcn_readlane((int)off, c - 1);
+    uint32_t nr = (uint32_t)__builtin_amdgcn_readlane((int)rem, c - 1) + smod;
+    uint64_t nidx = (uint64_t)L0 + offl + d.s_div;
     if (nr >= den) {
       nr -= den;
       nidx += 1;
     }
-    cur.i += 64;
+    cur.i += (uint64_t)c;
     cur.idx = nidx;
     cur.rem = nr;
+    if (c < 64) return;
   }
 }
 
@@ -881,6 +1102,7 @@ __device__ inline void flush_run(Acc& acc, uint32_t (*wcnt)[WC_COUNT], BlockScra
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __syncthreads();
   const uint64_t nfast = wave_sum((uint64_t)acc.nfast);
+  const uint64_t nmm = wave_sum((uint64_t)acc.nmm);
   const uint64_t nnear = wave_sum((uint64_t)acc.nnear_fast);
   uint64_t fmm = wave_min(acc.first_mm), fvi = wave_min(acc.first_viol);
   uint32_t mma = wave_max(acc.mm_abs), mmr = wave_max(acc.mm_rel);
@@ -907,7 +1129,7 @@ __device__ inline void flush_run(Acc& acc, uint32_t (*wcnt)[WC_COUNT], BlockScra
     for (int c = 0; c < LC_COUNT; ++c) bs.u[w][c] = wcnt[w][c];
     bs.u[w][LC_HIST0] += nfast;
     bs.u[w][LC_NEAR] += nnear;
-    bs.u[w][LC_COUNT + 0] = wcnt[w][WC_MISM];
+    bs.u[w][LC_COUNT + 0] = nmm;
     for (int c = 0; c < WC_COUNT; ++c) wcnt[w][c] = 0;
     bs.u[w][LC_COUNT + 1] = fmm;
     bs.u[w][LC_COUNT + 2] = fvi;
@@ -996,11 +1218,12 @@ __device__ __forceinline__ void near_item_count(const ScanArgs& a, int64_t item,
   near_prev = now;
 }
 
-// Phase A variant by wave-uniform conditions: near-zero counting, and tracking
-// of the lowest bit-identical index while it can still be an argmax.
+// Phase A variant by wave-uniform conditions (near-zero counting; the quick or
+// careful dot form), then the lowest bit-identical index while it can still be
+// an argmax.  `careful` counts the items left in the careful form.
 template <int DT>
-__device__ __forceinline__ uint64_t phase_a_any(const SegDesc& d, int64_t L0, const uint4* stage, uint32_t full,
-                                                Acc& acc) {
+__device__ __forceinline__ uint64_t phase_a_any(const SegDesc& d, int64_t L0, StageP stage, uint32_t full,
+                                                Acc& acc, uint32_t& careful) {
   if (!d.fast) {
     // no element can take the fast path: all elements of the full vectors are slow
     uint64_t all = 0;
@@ -1011,12 +1234,24 @@ __device__ __forceinline__ uint64_t phase_a_any(const SegDesc& d, int64_t L0, co
     }
     return all;
   }
-  const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
   const bool track = __ballot(acc.first_fast == kNone && (acc.gabs_k <= 0x80000000u || acc.grel_k <= 0x80000000u)) != 0;
-  if (near) {
-    return track ? phase_a<DT, true, true>(d, L0, stage, full, acc) : phase_a<DT, true, false>(d, L0, stage, full, acc);
+  uint64_t slow;
+  if (d.flags & KVV_FLAG_NEAR_ZERO) {
+    slow = phase_a<DT, true>(d, L0, stage, full, acc);
+  } else if constexpr (DotForm<DT>::on) {
+    bool redone = false;
+    if (careful) {
+      --careful;
+      slow = phase_a_dot<DT, true>(d, L0, stage, full, acc, redone);
+    } else {
+      slow = phase_a_dot<DT, false>(d, L0, stage, full, acc, redone);
+      if (redone) careful = 8;
+    }
+  } else {
+    slow = phase_a<DT, false>(d, L0, stage, full, acc);
   }
-  return track ? phase_a<DT, false, true>(d, L0, stage, full, acc) : phase_a<DT, false, false>(d, L0, stage, full, acc);
+  if (track) track_first_fast<DT>(L0, full, slow, acc);
+  return slow;
 }
 
 template <int DT, int MODE, int KIND, bool BATCH>
@@ -1052,8 +1287,10 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   int64_t run_start = i0;
   uint32_t near_prev = 0;
   uint4 gv[kUnroll], rv[kUnroll];
-  uint32_t full = 0;
+  uint32_t full = 0, careful = 0;
   bool loaded = false;
+  PendingSample pend;
+  pend.at = kNone;
   SampleCursor cur;
   {
     const SegDesc& d = BATCH ? a.table[s] : a.seg0;
@@ -1085,6 +1322,8 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
         sm.stage[(2 * u + 1) * kBlock + tid] = rv[u];
       }
       const uint32_t full_now = full;
+      StageP stage = (StageP)sm.stage;
+      store_pending(pend, a.sample_abs, a.sample_rel);
       // next item of the same segment: its loads fly while this one finishes
       loaded = false;
       if (it + 1 < i1 && it + 1 < d.item_begin + d.item_count) {
@@ -1093,14 +1332,15 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
         full = load_item<DT, KIND>(d, N0, N1, gv, rv);
         loaded = true;
       }
-      const uint64_t slow = phase_a_any<DT>(d, L0, sm.stage, full_now, acc);
+      sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, pend);
+      const uint64_t slow = phase_a_any<DT>(d, L0, stage, full_now, acc, careful);
       const uint32_t nslow = __ballot(slow != 0) ? build_queue<VecIO<DT>::NE>(slow, sm.queue[w]) : 0u;
-      if (nslow) phase_b<DT, MODE>(d, L0, nslow, sm.stage, sm.queue[w], acc, wc);
+      if (nslow) phase_b<DT, MODE>(d, L0, nslow, stage, sm.queue[w], acc, wc);
       if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, full_now, acc, wc);
-      sample_item<DT, MODE>(d, L0, L1, sm.stage, acc, a.sample_abs, a.sample_rel, cur);
     }
     if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, sm, near_prev);
   }
+  store_pending(pend, a.sample_abs, a.sample_rel);
   {
     const SegDesc& d = BATCH ? a.table[s] : a.seg0;
     flush_run(acc, sm.wcnt, sm.bs, a.runs, run_slot(d, run_start));

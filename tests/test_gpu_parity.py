@@ -114,6 +114,60 @@ def _pairs():
     out.append(("fp32_specials", sg, sr, {"FP32": {"rtol": 1e-3, "atol": 1e-3}}))
     out.append(("bf16_specials", sg.to(torch.bfloat16), sr.to(torch.bfloat16), None))
     out.append(("fp32_specials_int_mode", sg, sr, {"FP32": {"max_abs_diff": 3}}))
+    out += _dot_form_edges(rng)
+    return out
+
+
+def _flip_codes(codes: torch.Tensor, rng, p: float) -> torch.Tensor:
+    """A copy of integer codes with a fraction p of positions moved by +-1."""
+    out = codes.clone()
+    pos = torch.from_numpy(rng.random(codes.numel()) < p)
+    step = torch.from_numpy(rng.choice(np.array([-1, 1]), size=codes.numel()))
+    out[pos] = (out[pos].to(torch.int32) + step[pos].to(torch.int32)).to(codes.dtype)
+    return out
+
+
+def _dot_form_edges(rng):
+    """Pairs at the edges of the packed-dot sums of bit-identical elements: squares
+    below or above fp32's range (bf16), identical NaN/Inf pairs (re-run and careful
+    form), all-zero and signed-zero lanes, f8 NaN/Inf codes, int8/uint8 extremes."""
+    out = []
+    n = 131_101
+    scale = torch.from_numpy(2.0 ** rng.integers(-100, 101, n)).to(torch.float32)
+    for name, mag in (("tiny", 2.0 ** -70), ("huge", 2.0 ** 70), ("wide", None)):
+        v = torch.from_numpy(rng.standard_normal(n).astype(np.float32))
+        v = v * (scale if mag is None else mag)
+        r = v.to(torch.bfloat16)
+        g = _flip_codes(r.view(torch.int16), rng, 0.02).view(torch.bfloat16)
+        out.append((f"bf16_{name}_identical", g, r, None))
+    z = torch.zeros(n, dtype=torch.bfloat16)
+    z[::7] = -0.0
+    z[5::1013] = torch.tensor(1e-40, dtype=torch.bfloat16)   # bf16 denormal
+    out.append(("bf16_zeros_signed_denormal", z.clone(), z, None))
+    out.append(("bf16_all_zero", torch.zeros(n, dtype=torch.bfloat16), torch.zeros(n, dtype=torch.bfloat16), None))
+    for dt, nm in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+        r = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(dt)
+        spots = torch.from_numpy(rng.random(n) < 0.004)
+        kinds = torch.from_numpy(rng.integers(0, 3, n))
+        r[spots & (kinds == 0)] = float("nan")
+        r[spots & (kinds == 1)] = float("inf")
+        r[spots & (kinds == 2)] = float("-inf")
+        g = r.clone()
+        flip = torch.from_numpy(rng.random(n) < 0.03) & ~spots
+        g[flip] = _flip_codes(r.view(torch.int16), rng, 1.0).view(dt)[flip]
+        out.append((f"{nm}_identical_nonfinite", g, r, None))
+    codes = torch.from_numpy(rng.integers(0, 256, n).astype(np.uint8))
+    codes[::501] = 0x7F
+    codes[3::499] = 0xFF
+    g = codes.clone()
+    g[::31] ^= 1
+    out.append(("fp8_e4m3fn_nan_codes", g.view(torch.float8_e4m3fn), codes.view(torch.float8_e4m3fn), None))
+    out.append(("fp8_e5m2_nonfinite_codes", g.view(torch.float8_e5m2), codes.view(torch.float8_e5m2), None))
+    ext = torch.from_numpy(rng.choice(np.array([0, 1, 127, 128, 129, 254, 255], dtype=np.uint8), n))
+    ge = ext.clone()
+    ge[::57] = 255 - ge[::57]
+    out.append(("uint8_extremes", ge, ext, None))
+    out.append(("int8_extremes", ge.view(torch.int8), ext.view(torch.int8), None))
     return out
 
 
