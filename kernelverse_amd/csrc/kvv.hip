@@ -47,7 +47,8 @@ bool is_float_dtype(int dt) {
   return dt == KVV_F32 || dt == KVV_F16 || dt == KVV_BF16 || dt == KVV_F64 || dt == KVV_F8E4M3FN || dt == KVV_F8E5M2;
 }
 
-int item_elems_for(int dt) { return kBlock * (16 / elem_size(dt)) * kUnroll; }
+// One item is one wave's unit of work: 64 lanes x kUnroll 16-byte vectors of each tensor.
+int item_elems_for(int dt) { return 64 * (16 / elem_size(dt)) * kUnroll; }
 
 int device_cus() {
   static thread_local int cached_dev = -1, cached_cus = 0;
@@ -203,6 +204,10 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
   // select blocks per array: one for a small group, one per kSelChunk samples otherwise
   d.chunk_count = d.m == 0 ? 0 : (d.m <= kSmall ? 1 : (d.m + kSelChunk - 1) / kSelChunk);
   d.lslot = -1;
+  d.s_div = 1;  // n <= max_samples: every element is a sample (stride 1)
+  d.s_mod = 0;
+  d.s_magic = 0;
+  d.s_shift = 0;
   if (n > p->max_samples) {
     const uint64_t num = (uint64_t)n - 1, den = (uint64_t)d.m - 1;
     d.s_div = num / den;
@@ -233,10 +238,11 @@ struct WsLayout {
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Run slots a segment may need: one per block range it meets, at most one per
-// item and at most one per block of a launch (the grid is capped at 4096).
+// Run slots a segment may need: one per wave range it meets, at most one per
+// item and at most one per wave of a launch (the grid is capped at 4096 blocks).
 int64_t run_slot_bound(int64_t item_count) {
-  const int64_t b = item_count < 4096 ? item_count : 4096;
+  const int64_t units = 4096 * kWaves;
+  const int64_t b = item_count < units ? item_count : units;
   return (b + 3) & ~int64_t(3);
 }
 
@@ -386,11 +392,11 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   const int kind = scan_kind(d);
   ScanFn scan = scan_fn(d.dtype, d.mode, kind, false);
   if (!scan) return fail(KVV_E_INVALID, "no kernel for dtype");
-  const int64_t target = blocks_target(scan);
+  const int64_t target = blocks_target(scan) * kWaves;  // waves of the grid
   d.run_base = 0;
-  d.run_ipb = d.item_count > 0 ? (d.item_count + target - 1) / target : 1;
+  d.run_ipb = d.item_count > 0 ? (d.item_count + target - 1) / target : 1;  // items per wave
   if ((uint64_t)d.run_ipb * (uint64_t)d.item_elems >= (1ull << 32))
-    return fail(KVV_E_UNSUPPORTED, "tensor too large for 32-bit per-block counts");
+    return fail(KVV_E_UNSUPPORTED, "tensor too large for 32-bit per-wave counts");
   if (d.item_count > 0) {
     ScanArgs a{};
     a.seg0 = d;
@@ -398,14 +404,15 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     a.nseg = 1;
     a.item_lo = 0;
     a.items = d.item_count;
-    a.items_per_block = d.run_ipb;
+    a.items_per_wave = d.run_ipb;
     a.runs = run_cols(L, ws);
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);
     a.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
     a.zero_ptr = at<uint4>(ws, L.slots);
     a.zero_n4 = (int64_t)(L.slot_bytes / 16);
-    const int64_t grid = (d.item_count + a.items_per_block - 1) / a.items_per_block;
+    const int64_t per_block = a.items_per_wave * kWaves;
+    const int64_t grid = (d.item_count + per_block - 1) / per_block;
     if (ev_begin) KVV_HIP(hipEventRecord(ev_begin, st));
     hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
     KVV_HIP(hipGetLastError());
@@ -456,7 +463,7 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     const int s = (int)bp.table.size();
     for (int64_t c = 0; c < d.chunk_count; ++c) bp.chunk_seg.push_back((int64_t)s);
     item += d.item_count;
-    sample += d.m;
+    sample += (d.m + 63) & ~int64_t(63);  // each segment's samples start on a 256-byte line
     chunk += d.chunk_count;
     bp.near = bp.near || (d.flags & KVV_FLAG_NEAR_ZERO);
     if (bp.groups.empty() || bp.groups.back().dt != d.dtype || bp.groups.back().mode != d.mode ||
@@ -469,10 +476,10 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     bp.table.push_back(d);
   }
   for (auto& gr : bp.groups) {
-    const int64_t target = blocks_target(scan_fn(gr.dt, gr.mode, gr.kind, true));
-    gr.ipb = gr.items > 0 ? (gr.items + target - 1) / target : 1;
+    const int64_t target = blocks_target(scan_fn(gr.dt, gr.mode, gr.kind, true)) * kWaves;  // waves
+    gr.ipb = gr.items > 0 ? (gr.items + target - 1) / target : 1;  // items per wave
     if ((uint64_t)gr.ipb * (uint64_t)item_elems_for(gr.dt) >= (1ull << 32))
-      return fail(KVV_E_UNSUPPORTED, "batch group too large for 32-bit per-block counts");
+      return fail(KVV_E_UNSUPPORTED, "batch group too large for 32-bit per-wave counts");
     for (int s = gr.seg_lo; s < gr.seg_hi; ++s) {
       bp.table[s].run_base = gr.item_lo;
       bp.table[s].run_ipb = gr.ipb;
@@ -507,7 +514,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     a.nseg = gr.seg_hi - gr.seg_lo;
     a.item_lo = gr.item_lo;
     a.items = gr.items;
-    a.items_per_block = gr.ipb;
+    a.items_per_wave = gr.ipb;
     a.runs = run_cols(L, ws);
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);
@@ -518,7 +525,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
       a.zero_n4 = (int64_t)(L.slot_bytes / 16);
       zeroed = true;
     }
-    const int64_t grid = (gr.items + a.items_per_block - 1) / a.items_per_block;
+    const int64_t grid = (gr.items + gr.ipb * kWaves - 1) / (gr.ipb * kWaves);
     hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
     KVV_HIP(hipGetLastError());
   }

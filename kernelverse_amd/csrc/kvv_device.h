@@ -15,6 +15,7 @@ constexpr int kBlock = 256;           // threads per block (4 waves of 64)
 constexpr int kWaves = kBlock / 64;
 constexpr int kBuckets = KVV_HIST_BUCKETS;
 constexpr uint64_t kNone = ~0ull;     // "no index yet"
+constexpr uint32_t kNone32 = ~0u;     // the same for 32-bit offsets
 
 // Per-thread LDS counters (one column per thread, so increments never collide).
 enum LdsCounter {
@@ -253,7 +254,21 @@ __device__ __forceinline__ void wave_argmax(uint32_t& key, uint64_t& idx) {
     }
   }
 }
+__device__ __forceinline__ void wave_argmax32(uint32_t& key, uint32_t& idx) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t k = __shfl_xor(key, o);
+    const uint32_t i = __shfl_xor(idx, o);
+    if (k > key || (k == key && i < idx)) {
+      key = k;
+      idx = i;
+    }
+  }
+}
 __device__ __forceinline__ bool better(uint32_t k, uint64_t i, uint32_t bk, uint64_t bi) {
+  return k > bk || (k == bk && i < bi);
+}
+__device__ __forceinline__ bool better32(uint32_t k, uint32_t i, uint32_t bk, uint32_t bi) {
   return k > bk || (k == bk && i < bi);
 }
 

@@ -102,7 +102,7 @@ struct ScanArgs {
   int32_t pad;
   int64_t item_lo;         // items of this launch: [item_lo, item_lo + items)
   int64_t items;
-  int64_t items_per_block;
+  int64_t items_per_wave;  // each wave of the grid owns this many consecutive items
   RunCols runs;            // one slot per run (see run_slot)
   float* sample_abs;
   float* sample_rel;
@@ -119,9 +119,11 @@ struct Acc {
   uint32_t nmm;            // mismatches
   uint32_t nnear_fast;     // ... of which near zero
   float rel_thr;           // rel-max filter: only rel >= ~rel_thr can still win
-  uint64_t first_mm, first_viol;
-  uint64_t gabs_i, grel_i;
-  uint64_t first_fast;     // lowest index of such a pair (an abs/rel argmax candidate of value 0)
+  // element indices are offsets from the run's first element (a run spans
+  // fewer than 2^32 - 1 elements), kNone32 for none
+  uint32_t first_mm, first_viol;
+  uint32_t gabs_i, grel_i;
+  uint32_t first_fast;     // lowest index of such a pair (an abs/rel argmax candidate of value 0)
   double e_sq;             // sum of g*g over those pairs (there g == r: it feeds gg, rr and gr)
   double s[7];             // other pairs: gg rr gr dd | sampled gg rr gr
   __device__ void init() {
@@ -129,9 +131,9 @@ struct Acc {
     gabs_k = grel_k = 0;
     nfast = nnear_fast = nmm = 0;
     rel_thr = -__builtin_inff();
-    first_mm = first_viol = kNone;
-    gabs_i = grel_i = kNone;
-    first_fast = kNone;
+    first_mm = first_viol = kNone32;
+    gabs_i = grel_i = kNone32;
+    first_fast = kNone32;
     e_sq = 0.0;
 #pragma unroll
     for (int i = 0; i < 7; ++i) s[i] = 0.0;
@@ -139,6 +141,12 @@ struct Acc {
 };
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
+
+// Wave-uniform values, stated as such so that they live in scalar registers.
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ uint64_t uniform(uint64_t v) {
+  return (uint64_t)uniform((uint32_t)v) | ((uint64_t)uniform((uint32_t)(v >> 32)) << 32);
+}
 
 // Adds the number of lanes where `pred` holds to a per-wave LDS counter
 // (one ds_add by one lane, whatever the number of lanes).
@@ -243,7 +251,7 @@ __device__ __forceinline__ float wave_max_f32(float v) {
 // Full treatment of one element for the lanes with `act` set.  Every lane of
 // the wave calls it (it uses ballots); counts go to the wave's LDS row `wc`.
 template <int DT, int MODE>
-__device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem<DT>::T rc, bool act, uint64_t idx,
+__device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem<DT>::T rc, bool act, uint32_t idx,
                                           const SegDesc& d, Acc& acc, uint32_t* wc) {
   using E = Elem<DT>;
   float adf, rf;
@@ -260,7 +268,7 @@ __device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem
     acc.mm_abs = abs_key > acc.mm_abs ? abs_key : acc.mm_abs;
     acc.mm_rel = rk > acc.mm_rel ? rk : acc.mm_rel;
   }
-  if (act && better(abs_key, idx, acc.gabs_k, acc.gabs_i)) {
+  if (act && better32(abs_key, idx, acc.gabs_k, acc.gabs_i)) {
     acc.gabs_k = abs_key;
     acc.gabs_i = idx;
   }
@@ -270,7 +278,7 @@ __device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem
   if (act && !(adf < acc.rel_thr * den)) {
     const float rel = adf / den;
     const uint32_t rk = fkey(rel);
-    if (better(rk, idx, acc.grel_k, acc.grel_i)) {
+    if (better32(rk, idx, acc.grel_k, acc.grel_i)) {
       acc.grel_k = rk;
       acc.grel_i = idx;
       const float t = rel_threshold(rel);
@@ -356,12 +364,12 @@ template <int DT, int MODE>
 __device__ __forceinline__ void sample_range(const SegDesc& d, int64_t L0, int64_t L1, Acc& acc, float* sabs,
                                              float* srel) {
   if (d.n <= d.max_samples) {
-    for (int64_t idx = L0 + threadIdx.x; idx < L1; idx += kBlock) sample_one<DT, MODE>(d, idx, idx, acc, sabs, srel);
+    for (int64_t idx = L0 + lane_id(); idx < L1; idx += 64) sample_one<DT, MODE>(d, idx, idx, acc, sabs, srel);
     return;
   }
   const uint64_t num = (uint64_t)d.n - 1, den = (uint64_t)d.m - 1;
-  uint64_t i = ((uint64_t)L0 * den + num - 1) / num + threadIdx.x;
-  for (; i < (uint64_t)d.m; i += kBlock) {
+  uint64_t i = ((uint64_t)L0 * den + num - 1) / num + (uint64_t)lane_id();
+  for (; i < (uint64_t)d.m; i += 64) {
     const uint64_t idx = i * num / den;
     if (idx >= (uint64_t)L1) break;
     sample_one<DT, MODE>(d, (int64_t)idx, (int64_t)i, acc, sabs, srel);
@@ -413,7 +421,7 @@ __device__ __forceinline__ uint32_t load_item(const SegDesc& d, int64_t L0, int6
   uint32_t full = 0;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t v = L0 + (int64_t)(u * kBlock + threadIdx.x) * V;
+    const int64_t v = L0 + (int64_t)(u * 64 + lane_id()) * V;
     if (v + V <= L1) {
       full |= 1u << u;
       int64_t og, orr;
@@ -430,11 +438,52 @@ __device__ __forceinline__ uint32_t load_item(const SegDesc& d, int64_t L0, int6
       gv[u] = nt_load16(reinterpret_cast<const T*>(d.g) + og);
       rv[u] = nt_load16(reinterpret_cast<const T*>(d.r) + orr);
     } else {
-      gv[u] = make_uint4(0, 0, 0, 0);
+      gv[u] = make_uint4(0, 0, 0, 0);  // a partial last vector: patch_partial fills it
       rv[u] = make_uint4(0, 0, 0, 0);
     }
   }
   return full;
+}
+
+// Puts the elements of a lane's partial last vector (numel not a multiple of
+// the vector width; load_item left it zero) into its registers before the
+// stage write, so that every element of the item is in the stage and the
+// item's later steps read LDS only.  It runs before the next item's loads are
+// issued: a global load among the later steps would make the compiler wait
+// (vmcnt counts in issue order) for those loads as well.
+template <int DT, int KIND>
+__device__ __forceinline__ void patch_partial(const SegDesc& d, int64_t L0, int64_t L1, uint32_t full, uint4* gv,
+                                              uint4* rv) {
+  using T = typename Elem<DT>::T;
+  constexpr int V = VecIO<DT>::V;
+  constexpr int W = 8 * (int)sizeof(T);
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t v = L0 + (int64_t)(u * 64 + lane_id()) * V;
+    const int ne = ((full >> u) & 1u) || v >= L1 ? 0 : (int)(L1 - v);  // < V
+    if (ne == 0) continue;
+    uint64_t g0 = 0, g1 = 0, r0 = 0, r1 = 0;
+#pragma unroll 1
+    for (int e = 0; e < ne; ++e) {
+      int64_t og, orr;
+      if constexpr (KIND == K_CONTIG) {
+        og = orr = v + e;
+      } else {
+        elem_offsets(d, v + e, og, orr);
+      }
+      const uint64_t gx = (uint64_t)load_elem<DT>(d.g, og), rx = (uint64_t)load_elem<DT>(d.r, orr);
+      const int b = e * W;
+      if (b < 64) {
+        g0 |= gx << b;
+        r0 |= rx << b;
+      } else {
+        g1 |= gx << (b - 64);
+        r1 |= rx << (b - 64);
+      }
+    }
+    gv[u] = make_uint4((uint32_t)g0, (uint32_t)(g0 >> 32), (uint32_t)g1, (uint32_t)(g1 >> 32));
+    rv[u] = make_uint4((uint32_t)r0, (uint32_t)(r0 >> 32), (uint32_t)r1, (uint32_t)(r1 >> 32));
+  }
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave with DPP moves only (no LDS):
@@ -599,17 +648,28 @@ __device__ __forceinline__ void dword_fast_sums(uint32_t gz, float nz_abs, doubl
   }
 }
 
+// What phase A settled for one lane and item: the slow mask, the number of
+// fast (bit-identical finite) pairs, the sum of their squares and, with the
+// tolerant policy, how many of them are near zero.  The caller adds them to
+// the accumulators once (updates of the accumulators inside the variants were
+// merged by the compiler through an address select, which kept them in scratch).
+struct PhaseA {
+  uint64_t slow;
+  uint32_t nfast, nnear;
+  double esq;
+};
+
 // Lowest logical index of a fast element of the item (vectors in order, then
 // elements): an abs/rel argmax candidate of value 0 until a positive one exists.
 template <int DT>
-__device__ __forceinline__ void track_first_fast(int64_t L0, uint32_t full, uint64_t slow, Acc& acc) {
+__device__ __forceinline__ void track_first_fast(uint32_t R0, uint32_t full, uint64_t slow, Acc& acc) {
   constexpr int V = VecIO<DT>::V;
-  uint64_t ff = acc.first_fast;
+  uint32_t ff = acc.first_fast;
   for (int p = 0; p < V * kUnroll; ++p) {
     int u, e;
     slot_of<Elem<DT>::width>(p, u, e);
     if (!((full >> u) & 1u) || ((slow >> p) & 1u)) continue;
-    const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + (int)threadIdx.x) * V + e);
+    const uint32_t idx = R0 + (uint32_t)((u * 64 + lane_id()) * V + e);
     if (idx < ff) ff = idx;
   }
   acc.first_fast = ff;
@@ -619,13 +679,12 @@ __device__ __forceinline__ void track_first_fast(int64_t L0, uint32_t full, uint
 // finished here (count; g*g into e_sq, which feeds gg, rr and gr since g == r);
 // returns the lane's slow mask in the layout above.
 template <int DT, bool NEAR>
-__device__ __forceinline__ uint64_t phase_a(const SegDesc& d, int64_t L0, StageP stage, uint32_t full,
-                                            Acc& acc) {
+__device__ __forceinline__ PhaseA phase_a(const SegDesc& d, StageP stage, uint32_t full) {
   using E = Elem<DT>;
   using IO = VecIO<DT>;
   constexpr int V = IO::V;
   constexpr int W = E::width;
-  const int tid = threadIdx.x;
+  const int lane = lane_id();
   uint32_t m0 = 0, m1 = 0;  // slow mask, low and high 32 bits
   double s0 = 0.0, s1 = 0.0;
   uint32_t nnear = 0, nvec = 0;
@@ -634,8 +693,8 @@ __device__ __forceinline__ uint64_t phase_a(const SegDesc& d, int64_t L0, StageP
   for (int u = 0; u < kUnroll; ++u) {
     if (!((full >> u) & 1u)) continue;
     ++nvec;
-    const uint4 gq = stage_vec(stage, (2 * u) * kBlock + tid);
-    const uint4 rq = stage_vec(stage, (2 * u + 1) * kBlock + tid);
+    const uint4 gq = stage_vec(stage, (2 * u) * 64 + lane);
+    const uint4 rq = stage_vec(stage, (2 * u + 1) * 64 + lane);
     const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w};
     const uint32_t rw[4] = {rq.x, rq.y, rq.z, rq.w};
     if constexpr (W == 64) {
@@ -666,15 +725,14 @@ __device__ __forceinline__ uint64_t phase_a(const SegDesc& d, int64_t L0, StageP
       }
     }
   }
-  const uint64_t slow = ((uint64_t)m1 << 32) | m0;
-  const uint32_t nslow = (uint32_t)__popcll(slow);
-  acc.e_sq += s0 + s1;
-  acc.nfast += nvec * V - nslow;
-  if constexpr (NEAR) {
-    // zeroed slow elements were counted as near when 0 <= nz_abs
-    acc.nnear_fast += nnear - (0.0f <= nz_abs ? nslow : 0u);
-  }
-  return slow;
+  PhaseA o;
+  o.slow = ((uint64_t)m1 << 32) | m0;
+  const uint32_t nslow = (uint32_t)__popcll(o.slow);
+  o.esq = s0 + s1;
+  o.nfast = nvec * V - nslow;
+  // zeroed slow elements were counted as near when 0 <= nz_abs
+  o.nnear = NEAR ? nnear - (0.0f <= nz_abs ? nslow : 0u) : 0u;
+  return o;
 }
 
 // ------------------------------------------------------------ phase A, dot form
@@ -755,23 +813,22 @@ __device__ __forceinline__ uint32_t ident_flags(uint32_t g, uint32_t r) {
 }
 
 template <int DT, bool CAREFUL>
-__device__ __forceinline__ uint64_t phase_a_dot(const SegDesc& d, int64_t L0, StageP stage, uint32_t full,
-                                                Acc& acc, bool& redone) {
+__device__ __forceinline__ PhaseA phase_a_dot(const SegDesc& d, StageP stage, uint32_t full, bool& redone) {
   using DF = DotForm<DT>;
   using A = typename DF::A;
   constexpr int V = VecIO<DT>::V;
   constexpr int W = Elem<DT>::width;
-  const int tid = threadIdx.x;
+  const int lane = lane_id();
   uint32_t m0 = 0, m1 = 0, orz = 0;
   A a[DF::NA];
 #pragma unroll
   for (int k = 0; k < DF::NA; ++k) a[k] = 0;
-  // vectors that were not full loads hold zeros in the stage (load_item): they
-  // read as identical pairs of squares 0 and are left out of the count below
-#pragma unroll
+  // every vector of the item is a full load here (phase_a_any); one vector per
+  // iteration keeps the LDS reads in flight (and their registers) few
+#pragma unroll 1
   for (int u = 0; u < kUnroll; ++u) {
-    const uint4 gq = stage_vec(stage, (2 * u) * kBlock + tid);
-    const uint4 rq = stage_vec(stage, (2 * u + 1) * kBlock + tid);
+    const uint4 gq = stage_vec(stage, (2 * u) * 64 + lane);
+    const uint4 rq = stage_vec(stage, (2 * u + 1) * 64 + lane);
     const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w};
     const uint32_t rw[4] = {rq.x, rq.y, rq.z, rq.w};
 #pragma unroll
@@ -797,15 +854,17 @@ __device__ __forceinline__ uint64_t phase_a_dot(const SegDesc& d, int64_t L0, St
     if constexpr (DT == KVV_BF16) redo = redo || (t < 0x1p-60f && (orz & 0x7FFF7FFFu) != 0u);
   }
   redone = __ballot(redo) != 0;
-  if (redone && redo) return phase_a<DT, false>(d, L0, stage, full, acc);
-  const uint64_t slow = ((uint64_t)m1 << 32) | m0;
+  if (redone && redo) return phase_a<DT, false>(d, stage, full);
+  PhaseA o;
+  o.slow = ((uint64_t)m1 << 32) | m0;
   double e = 0.0;
 #pragma unroll
   for (int k = 0; k < DF::NA; ++k) e += (double)a[k];
   if constexpr (DT == KVV_F8E4M3FN) e *= 65536.0;
-  acc.e_sq += e;
-  acc.nfast += (uint32_t)__popc(full) * V - (uint32_t)__popcll(slow);
-  return slow;
+  o.esq = e;
+  o.nfast = (uint32_t)(kUnroll * V) - (uint32_t)__popcll(o.slow);
+  o.nnear = 0;
+  return o;
 }
 
 // Appends the lanes' remaining elements to the wave's queue in lane order
@@ -836,12 +895,12 @@ __device__ __forceinline__ uint32_t build_queue(uint64_t slow, uint16_t* queue) 
 
 // Phase B: the wave's queued elements, 64 at a time, from the LDS stage.
 template <int DT, int MODE>
-__device__ __forceinline__ void phase_b(const SegDesc& d, int64_t L0, uint32_t total, StageP stage,
+__device__ __forceinline__ void phase_b(const SegDesc& d, uint32_t R0, uint32_t total, StageP stage,
                                         const uint16_t* queue, Acc& acc, uint32_t* wc) {
   using IO = VecIO<DT>;
   using T = typename IO::T;
   constexpr int V = IO::V;
-  const int lane = lane_id(), w = threadIdx.x >> 6;
+  const int lane = lane_id();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -852,10 +911,9 @@ __device__ __forceinline__ void phase_b(const SegDesc& d, int64_t L0, uint32_t t
     const int src = (int)(ent >> 6);
     int u, e;
     slot_of<Elem<DT>::width>((int)(ent & 63), u, e);
-    const int t = w * 64 + src;
-    const T gc = stage_elem<T>(stage, (2 * u) * kBlock + t, e);
-    const T rc = stage_elem<T>(stage, (2 * u + 1) * kBlock + t, e);
-    const uint64_t idx = (uint64_t)(L0 + ((int64_t)u * kBlock + t) * V + e);
+    const T gc = stage_elem<T>(stage, (2 * u) * 64 + src, e);
+    const T rc = stage_elem<T>(stage, (2 * u + 1) * 64 + src, e);
+    const uint32_t idx = R0 + (uint32_t)((u * 64 + src) * V + e);
     slow_elem<DT, MODE>(gc, rc, act, idx, d, acc, wc);
   }
 }
@@ -884,27 +942,18 @@ __device__ __forceinline__ SampleCursor cursor_at(const SegDesc& d, int64_t L0) 
   return c;
 }
 
-// The pair at logical index idx of a vector item: from the stage when its
-// vector was a full 16-byte load, else (partial last vector) from memory.
+// The pair at logical index idx (L0 <= idx < L1) of a vector item, from the
+// stage (load_item filled a partial last vector element by element).
 template <int DT>
-__device__ __forceinline__ void stage_pair(const SegDesc& d, int64_t L0, int64_t L1, int64_t idx, StageP stage,
-                                           typename Elem<DT>::T& gc, typename Elem<DT>::T& rc) {
-  using IO = VecIO<DT>;
-  using T = typename IO::T;
-  constexpr int V = IO::V;
-  const int64_t q = idx - L0;
-  const int64_t vstart = idx - q % V;
-  if (vstart + V <= L1) {
-    const int vec = (int)(q / V);
-    const int u = vec / kBlock, t = vec % kBlock, e = (int)(q % V);
-    gc = stage_elem<T>(stage, (2 * u) * kBlock + t, e);
-    rc = stage_elem<T>(stage, (2 * u + 1) * kBlock + t, e);
-  } else {
-    int64_t og, orr;
-    elem_offsets(d, idx, og, orr);
-    gc = load_elem<DT>(d.g, og);
-    rc = load_elem<DT>(d.r, orr);
-  }
+__device__ __forceinline__ void stage_pair(int64_t L0, int64_t idx, StageP stage, typename Elem<DT>::T& gc,
+                                           typename Elem<DT>::T& rc) {
+  using T = typename Elem<DT>::T;
+  constexpr int V = VecIO<DT>::V;
+  const int q = (int)(idx - L0);
+  const int vec = q / V;
+  const int u = vec >> 6, t = vec & 63, e = q % V;
+  gc = stage_elem<T>(stage, (2 * u) * 64 + t, e);
+  rc = stage_elem<T>(stage, (2 * u + 1) * 64 + t, e);
 }
 
 // abs_diff and rel_diff of one sampled pair; its values join the sampled fp64 sums.
@@ -933,53 +982,79 @@ __device__ __forceinline__ void sample_write(const SegDesc& d, typename Elem<DT>
   srel[d.sample_off + i] = rel;
 }
 
-// The sample a lane computed in the last cursor step of an item.  It is stored
-// at the next item, after that item's stage write and before its loads are
-// issued: a store issued after the loads would make the wait for them (vmcnt
-// counts loads and stores in issue order) wait for the store as well.
-struct PendingSample {
-  uint64_t at;  // position in the sample arrays, kNone if none
+// A wave's line buffer of sample values.  Lane l holds the values of sample
+// position sb0 + l (positions in the sample arrays; sb0 is a multiple of 64)
+// and lanes [lo, fill) are valid.  A full buffer is written as one 256-byte
+// store per array, so the sample arrays are written in whole lines: scattered
+// 4-byte stores of partial lines cost HBM bandwidth well beyond their bytes.
+struct SampleLine {
+  uint64_t sb0;       // kNone: empty
+  uint32_t lo, fill;
   float abs, rel;
 };
 
-__device__ __forceinline__ void store_pending(PendingSample& p, float* sabs, float* srel) {
-  if (p.at != kNone) {
-    sabs[p.at] = p.abs;
-    srel[p.at] = p.rel;
-    p.at = kNone;
+__device__ __forceinline__ void line_store(SampleLine& b, float* sabs, float* srel) {
+  const uint32_t lane = (uint32_t)lane_id();
+  if (b.sb0 != kNone && lane >= b.lo && lane < b.fill) {
+    sabs[b.sb0 + lane] = b.abs;
+    srel[b.sb0 + lane] = b.rel;
   }
+  b.sb0 = kNone;
 }
 
-// Samples of a vector item (GCR:346-347).  Every wave walks the same cursor, 64
-// samples per step (lane l takes sample cursor.i + l), and a lane handles its
-// sample only when the element sits in its own wave's stage slots, so no
-// barrier is needed.  Positions inside a full item are 32-bit offsets from L0.
-// When n <= max_samples every element is a sample and each lane simply takes
-// its own slots.
+// Places the values of c consecutive samples, held by lanes 0..c-1 (c <= 64),
+// at positions [at, at + c) of the buffer, writing it out when it fills.
+__device__ __forceinline__ void line_put(SampleLine& b, uint64_t at, int c, float va, float vr, float* sabs,
+                                         float* srel) {
+  const uint32_t lane = (uint32_t)lane_id();
+  if (b.sb0 != kNone && at != b.sb0 + b.fill) line_store(b, sabs, srel);  // not contiguous (a new segment)
+  if (b.sb0 == kNone) {
+    b.sb0 = at & ~63ull;
+    b.lo = b.fill = (uint32_t)(at - b.sb0);
+  }
+  const uint32_t k = b.fill;
+  // lane l of the buffer takes walk lane (l - k) mod 64
+  const int src = (int)((lane - k) & 63u);
+  const float ra = __shfl(va, src), rr = __shfl(vr, src);
+  const uint32_t end = k + (uint32_t)c;  // < 128
+  if (lane >= k && lane < end) {
+    b.abs = ra;
+    b.rel = rr;
+  }
+  if (end >= 64) {
+    b.fill = 64;
+    line_store(b, sabs, srel);
+    b.sb0 = (at & ~63ull) + 64;
+    b.lo = 0;
+    b.fill = end - 64;
+    if (lane < b.fill) {
+      b.abs = ra;
+      b.rel = rr;
+    }
+    if (b.fill == 0) b.sb0 = kNone;
+  } else {
+    b.fill = end;
+  }
+  b.sb0 = uniform(b.sb0);
+  b.lo = uniform(b.lo);
+  b.fill = uniform(b.fill);
+}
+
+// Samples of a vector item (GCR:346-347): the wave walks its cursor 64 samples
+// per step (lane l takes sample cursor.i + l); every sample of the item lies in
+// the wave's own stage slots.  Positions inside the item are 32-bit offsets
+// from L0.  The values go through the wave's line buffer.  When n <=
+// max_samples every element is a sample (the host sets the stride to 1).
 template <int DT, int MODE>
 __device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_t L1, StageP stage, Acc& acc,
-                                            float* sabs, float* srel, SampleCursor& cur, PendingSample& pend) {
+                                            float* sabs, float* srel, SampleCursor& cur, SampleLine& line) {
   using IO = VecIO<DT>;
   using T = typename IO::T;
   constexpr int V = IO::V;
   constexpr int LV = V == 16 ? 4 : (V == 8 ? 3 : (V == 4 ? 2 : 1));  // log2(V)
-  const int lane = lane_id(), w = threadIdx.x >> 6;
-  if (d.n <= d.max_samples) {
-#pragma unroll 1
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t v = L0 + (int64_t)(u * kBlock + threadIdx.x) * V;
-      for (int e = 0; e < V; ++e) {
-        if (v + e >= L1) break;
-        T gc, rc;
-        stage_pair<DT>(d, L0, L1, v + e, stage, gc, rc);
-        sample_write<DT, MODE>(d, gc, rc, (uint64_t)(v + e), acc, sabs, srel);
-      }
-    }
-    return;
-  }
+  const int lane = lane_id();
   const uint32_t den = (uint32_t)(d.m - 1);
   const uint32_t len = (uint32_t)(L1 - L0);
-  const bool whole = len == (uint32_t)(kUnroll * kBlock * V);  // every vector of the item is a full load
   // lane * s_div only matters while it stays inside the item; clamping keeps the
   // 32-bit offsets exact for the lanes that can be in range
   const uint32_t sdiv = d.s_div < (1ull << 20) ? (uint32_t)d.s_div : (1u << 20);
@@ -995,30 +1070,15 @@ __device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_
     // the in-range lanes are a prefix; the cursor moves past the last of them
     const int c = (int)__popcll(__ballot(in));
     if (c == 0) return;
-    const uint32_t vi = off >> LV;
-    if (in && ((vi >> 6) & 3u) == (uint32_t)w) {
-      T gc, rc;
-      if (whole) {
-        const int u = (int)(vi >> 8), tt = (int)(vi & 255u), e = (int)(off & (V - 1));
-        gc = stage_elem<T>(stage, (2 * u) * kBlock + tt, e);
-        rc = stage_elem<T>(stage, (2 * u + 1) * kBlock + tt, e);
-      } else {
-        stage_pair<DT>(d, L0, L1, L0 + (int64_t)off, stage, gc, rc);
-      }
-      float adf, rel;
+    float adf = 0.0f, rel = 0.0f;
+    if (in) {
+      const uint32_t vi = off >> LV;
+      const int u = (int)(vi >> 6), tt = (int)(vi & 63u), e = (int)(off & (V - 1));
+      const T gc = stage_elem<T>(stage, (2 * u) * 64 + tt, e);
+      const T rc = stage_elem<T>(stage, (2 * u + 1) * 64 + tt, e);
       sample_value<DT, MODE>(d, gc, rc, acc, adf, rel);
-      const uint64_t at = d.sample_off + cur.i + (uint64_t)lane;
-      if (c < 64) {
-        // the item's last step: held until the next item (the lane's previous
-        // pending sample was stored at this item's start)
-        pend.at = at;
-        pend.abs = adf;
-        pend.rel = rel;
-      } else {
-        sabs[at] = adf;
-        srel[at] = rel;
-      }
     }
+    line_put(line, d.sample_off + cur.i, c, adf, rel, sabs, srel);
     const uint32_t offl = (uint32_t)__builtin_amdgcn_readlane((int)off, c - 1);
     uint32_t nr = (uint32_t)__builtin_amdgcn_readlane((int)rem, c - 1) + smod;
     uint64_t nidx = (uint64_t)L0 + offl + d.s_div;
@@ -1026,195 +1086,142 @@ __device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_
       nr -= den;
       nidx += 1;
     }
-    cur.i += (uint64_t)c;
-    cur.idx = nidx;
-    cur.rem = nr;
+    cur.i = uniform(cur.i + (uint64_t)c);
+    cur.idx = uniform(nidx);
+    cur.rem = uniform(nr);
     if (c < 64) return;
   }
 }
 
-// Elements of a partial last vector (numel not a multiple of the vector width).
+// Elements of a partial last vector (numel not a multiple of the vector width),
+// from the stage.
 template <int DT, int MODE>
-__device__ __forceinline__ void vec_tail(const SegDesc& d, int64_t L0, int64_t L1, uint32_t full, Acc& acc,
-                                         uint32_t* wc) {
+__device__ __forceinline__ void vec_tail(const SegDesc& d, int64_t L0, int64_t L1, uint32_t R0, uint32_t full,
+                                         StageP stage, Acc& acc, uint32_t* wc) {
+  using T = typename Elem<DT>::T;
   constexpr int V = VecIO<DT>::V;
+  const int lane = lane_id();
 #pragma unroll 1
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t v = L0 + (int64_t)(u * kBlock + threadIdx.x) * V;
+    const int64_t v = L0 + (int64_t)(u * 64 + lane) * V;
     const bool part = !((full >> u) & 1u) && v < L1;
     if (__ballot(part) == 0) continue;
     for (int e = 0; e < V; ++e) {
       const bool act = part && v + e < L1;
-      int64_t og = 0, orr = 0;
-      if (act) elem_offsets(d, v + e, og, orr);
-      const auto gc = act ? load_elem<DT>(d.g, og) : (typename Elem<DT>::T)0;
-      const auto rc = act ? load_elem<DT>(d.r, orr) : (typename Elem<DT>::T)0;
-      slow_elem<DT, MODE>(gc, rc, act, (uint64_t)(v + e), d, acc, wc);
+      const T gc = stage_elem<T>(stage, (2 * u) * 64 + lane, e);
+      const T rc = stage_elem<T>(stage, (2 * u + 1) * 64 + lane, e);
+      slow_elem<DT, MODE>(gc, rc, act, R0 + (uint32_t)((u * 64 + lane) * V + e), d, acc, wc);
     }
   }
 }
 
 // Scalar path: any strides, one element per thread per step.
 template <int DT, int MODE>
-__device__ __forceinline__ void scan_item_scalar(const SegDesc& d, int64_t L0, int64_t L1, Acc& acc, uint32_t* wc) {
-  for (int64_t base = L0; base < L1; base += kBlock) {
-    const int64_t idx = base + threadIdx.x;
+__device__ __forceinline__ void scan_item_scalar(const SegDesc& d, int64_t L0, int64_t L1, int64_t base, Acc& acc,
+                                                 uint32_t* wc) {
+  for (int64_t at = L0; at < L1; at += 64) {
+    const int64_t idx = at + lane_id();
     const bool act = idx < L1;
     int64_t og = 0, orr = 0;
     if (act) elem_offsets(d, idx, og, orr);
     const auto gc = act ? load_elem<DT>(d.g, og) : (typename Elem<DT>::T)0;
     const auto rc = act ? load_elem<DT>(d.r, orr) : (typename Elem<DT>::T)0;
-    slow_elem<DT, MODE>(gc, rc, act, (uint64_t)idx, d, acc, wc);
+    slow_elem<DT, MODE>(gc, rc, act, (uint32_t)(idx - base), d, acc, wc);
   }
 }
 
-// ------------------------------------------------------------ block reductions
-struct BlockScratch {
-  uint64_t u[kWaves][LC_COUNT + 8];
-  uint32_t k[kWaves][4];
-  double s[kWaves][7];
-};
-
-__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
-  v = wave_sum(v);
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __syncthreads();
-  if (lane == 0) red[w] = v;
-  __syncthreads();
-  uint32_t t = 0;
-#pragma unroll
-  for (int i = 0; i < kWaves; ++i) t += red[i];
-  return t;
-}
-
+// ------------------------------------------------------------ run records
 // Run slot of the run that starts at item `it` of segment d: runs start at the
-// segment's first item and at every block-range start inside it.
+// segment's first item and at every wave-range start inside it.
 __device__ __forceinline__ int64_t run_slot(const SegDesc& d, int64_t it) {
   if (it == d.item_begin) return d.run_slot0;
   const int64_t b_first = (d.item_begin - d.run_base) / d.run_ipb + 1;
   return d.run_slot0 + (it - d.run_base) / d.run_ipb - b_first + 1;
 }
 
-// Reduces the block's accumulators and wave counters into the run's columns
-// (one thread per column, waves in order) and resets them for the next run.
-__device__ inline void flush_run(Acc& acc, uint32_t (*wcnt)[WC_COUNT], BlockScratch& bs, const RunCols& out,
-                                 int64_t slot) {
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  __syncthreads();
-  const uint64_t nfast = wave_sum((uint64_t)acc.nfast);
-  const uint64_t nmm = wave_sum((uint64_t)acc.nmm);
-  const uint64_t nnear = wave_sum((uint64_t)acc.nnear_fast);
-  uint64_t fmm = wave_min(acc.first_mm), fvi = wave_min(acc.first_viol);
-  uint32_t mma = wave_max(acc.mm_abs), mmr = wave_max(acc.mm_rel);
+// Reduces the wave's accumulators and LDS counters into the run's columns (lane
+// c writes u32 column c, lane 32 + c u64 column c) and resets them for the next
+// run.  `base` is the logical index of the run's first element (the origin of
+// the accumulators' 32-bit offsets).
+static_assert(kColU32 == 32 && kColU64 <= 32, "one lane per run column");
+__device__ inline void flush_run(Acc& acc, uint32_t* wc, const RunCols& out, int64_t slot, int64_t base) {
+  const int lane = lane_id();
+  const uint32_t nfast = wave_sum(acc.nfast);
+  const uint32_t nmm = wave_sum(acc.nmm);
+  const uint32_t nnear = wave_sum(acc.nnear_fast);
+  const uint32_t fmm32 = wave_min(acc.first_mm), fvi32 = wave_min(acc.first_viol);
+  const uint32_t mma = wave_max(acc.mm_abs), mmr = wave_max(acc.mm_rel);
   // bit-identical pairs have abs_diff = rel_diff = +0, whose key is 0x80000000 in both modes
   uint32_t gak = acc.gabs_k, grk = acc.grel_k;
-  uint64_t gai = acc.gabs_i, gri = acc.grel_i;
-  if (better(0x80000000u, acc.first_fast, gak, gai)) {
+  uint32_t gai32 = acc.gabs_i, gri32 = acc.grel_i;
+  if (better32(0x80000000u, acc.first_fast, gak, gai32)) {
     gak = 0x80000000u;
-    gai = acc.first_fast;
+    gai32 = acc.first_fast;
   }
-  if (better(0x80000000u, acc.first_fast, grk, gri)) {
+  if (better32(0x80000000u, acc.first_fast, grk, gri32)) {
     grk = 0x80000000u;
-    gri = acc.first_fast;
+    gri32 = acc.first_fast;
   }
-  wave_argmax(gak, gai);
-  wave_argmax(grk, gri);
-  double s[7];
-  s[0] = wave_sum(acc.e_sq + acc.s[0]);
-  s[1] = wave_sum(acc.e_sq + acc.s[1]);
-  s[2] = wave_sum(acc.e_sq + acc.s[2]);
+  wave_argmax32(gak, gai32);
+  wave_argmax32(grk, gri32);
+  auto absolute = [base](uint32_t r) -> uint64_t { return r == kNone32 ? kNone : (uint64_t)(base + (int64_t)r); };
+  double sm[7];
+  sm[0] = wave_sum(acc.e_sq + acc.s[0]);
+  sm[1] = wave_sum(acc.e_sq + acc.s[1]);
+  sm[2] = wave_sum(acc.e_sq + acc.s[2]);
 #pragma unroll
-  for (int i = 3; i < 7; ++i) s[i] = wave_sum(acc.s[i]);
-  if (lane == 0) {
-    for (int c = 0; c < LC_COUNT; ++c) bs.u[w][c] = wcnt[w][c];
-    bs.u[w][LC_HIST0] += nfast;
-    bs.u[w][LC_NEAR] += nnear;
-    bs.u[w][LC_COUNT + 0] = nmm;
-    for (int c = 0; c < WC_COUNT; ++c) wcnt[w][c] = 0;
-    bs.u[w][LC_COUNT + 1] = fmm;
-    bs.u[w][LC_COUNT + 2] = fvi;
-    bs.u[w][LC_COUNT + 3] = gai;
-    bs.u[w][LC_COUNT + 4] = gri;
-    bs.k[w][0] = mma;
-    bs.k[w][1] = mmr;
-    bs.k[w][2] = gak;
-    bs.k[w][3] = grk;
-#pragma unroll
-    for (int i = 0; i < 7; ++i) bs.s[w][i] = s[i];
-  }
-  __syncthreads();
-  if (tid < kColU32) {
-    if (tid < CU_GABSK) {
-      uint64_t t = 0;
-      if (tid <= CU_MISM) {
-        const int src = tid < LC_COUNT ? tid : LC_COUNT + 0;
-        for (int i = 0; i < kWaves; ++i) t += bs.u[i][src];
-      } else {
-        for (int i = 0; i < kWaves; ++i) {
-          const uint64_t k = bs.k[i][tid - CU_MMABS];
-          t = k > t ? k : t;
-        }
-      }
-      out.u32[tid * out.stride + slot] = (uint32_t)t;
-    }
-  } else if (tid >= 64 && tid < 64 + kColU64) {
-    const int c = tid - 64;
-    if (c == CL_FIRSTMM || c == CL_FIRSTVIOL) {
-      uint64_t t = kNone;
-      for (int i = 0; i < kWaves; ++i) {
-        const uint64_t v = bs.u[i][LC_COUNT + 1 + c];
-        t = v < t ? v : t;
-      }
-      out.u64[c * out.stride + slot] = t;
-    } else if (c == CL_GABSI || c == CL_GRELI) {
-      const int q = c - CL_GABSI;
-      uint32_t bk = 0;
-      uint64_t bi = kNone;
-      for (int i = 0; i < kWaves; ++i) {
-        if (better(bs.k[i][2 + q], bs.u[i][LC_COUNT + 3 + q], bk, bi)) {
-          bk = bs.k[i][2 + q];
-          bi = bs.u[i][LC_COUNT + 3 + q];
-        }
-      }
-      out.u64[c * out.stride + slot] = bi;
-      out.u32[(CU_GABSK + q) * out.stride + slot] = bk;
+  for (int i = 3; i < 7; ++i) sm[i] = wave_sum(acc.s[i]);
+  if (lane < kColU32) {
+    uint32_t v;
+    if (lane < LC_COUNT) {
+      v = wc[lane] + (lane == LC_HIST0 ? nfast : 0u) + (lane == LC_NEAR ? nnear : 0u);
+      wc[lane] = 0;
     } else {
-      double t = 0.0;
-      for (int i = 0; i < kWaves; ++i) t += bs.s[i][c - CL_S0];
-      out.u64[c * out.stride + slot] = (uint64_t)__double_as_longlong(t);
+      v = lane == CU_MISM ? nmm : lane == CU_MMABS ? mma : lane == CU_MMREL ? mmr : lane == CU_GABSK ? gak : grk;
     }
+    out.u32[lane * out.stride + slot] = v;
+  } else if (lane < 32 + kColU64) {
+    const int c = lane - 32;
+    uint64_t v;
+    if (c == CL_FIRSTMM) v = absolute(fmm32);
+    else if (c == CL_FIRSTVIOL) v = absolute(fvi32);
+    else if (c == CL_GABSI) v = absolute(gai32);
+    else if (c == CL_GRELI) v = absolute(gri32);
+    else {
+      double x = sm[0];
+#pragma unroll
+      for (int i = 1; i < 7; ++i) x = (c - CL_S0 == i) ? sm[i] : x;
+      v = (uint64_t)__double_as_longlong(x);
+    }
+    out.u64[c * out.stride + slot] = v;
   }
   acc.init();
-  __syncthreads();
 }
 
 // ------------------------------------------------------------ scan kernel
-// LDS of one scan block: the item's vectors (NS uint4 per tensor-vector slot)
-// and the per-wave queues of stage positions (NQ = 64 lanes x elements per lane).
-template <int NS, int NQ>
+// LDS of one scan block: per wave, its item's vectors (SW uint4: kUnroll
+// vectors of each tensor per lane), its queue of stage positions (NQ = 64 lanes
+// x elements per lane) and its counters.  Waves never touch each other's part.
+template <int SW, int NQ>
 struct ScanShared {
-  uint4 stage[NS];
+  uint4 stage[kWaves][SW];
   uint16_t queue[kWaves][NQ];
   uint32_t wcnt[kWaves][WC_COUNT];
-  uint32_t red[kWaves];
-  BlockScratch bs;
 };
 
 template <int DT, int KIND>
 struct ScanLds {
   static constexpr bool vec = KIND != K_SCALAR;
-  using type = ScanShared<vec ? 2 * kUnroll * kBlock : 1, vec ? 64 * VecIO<DT>::NE : 2>;
+  using type = ScanShared<vec ? 2 * kUnroll * 64 : 1, vec ? 64 * VecIO<DT>::NE : 2>;
 };
 
-// Per-item near-zero count (feeds the compacted-rank prefix of near_kernel).
-template <typename SM>
-__device__ __forceinline__ void near_item_count(const ScanArgs& a, int64_t item, Acc& acc, SM& sm,
+// Per-item near-zero count of the wave (feeds the compacted-rank prefix of near_kernel).
+__device__ __forceinline__ void near_item_count(const ScanArgs& a, int64_t item, Acc& acc, const uint32_t* wc,
                                                 uint32_t& near_prev) {
-  const int w = threadIdx.x >> 6;
   uint32_t mine = acc.nnear_fast;
-  if (lane_id() == 0) mine += sm.wcnt[w][LC_NEAR];
-  const uint32_t now = block_sum_u32(mine, sm.red);
-  if (threadIdx.x == 0) a.item_near[item] = now - near_prev;
+  if (lane_id() == 0) mine += wc[LC_NEAR];
+  const uint32_t now = wave_sum(mine);
+  if (lane_id() == 0) a.item_near[item] = now - near_prev;
   near_prev = now;
 }
 
@@ -1222,8 +1229,8 @@ __device__ __forceinline__ void near_item_count(const ScanArgs& a, int64_t item,
 // careful dot form), then the lowest bit-identical index while it can still be
 // an argmax.  `careful` counts the items left in the careful form.
 template <int DT>
-__device__ __forceinline__ uint64_t phase_a_any(const SegDesc& d, int64_t L0, StageP stage, uint32_t full,
-                                                Acc& acc, uint32_t& careful) {
+__device__ __forceinline__ uint64_t phase_a_any(const SegDesc& d, int64_t L0, uint32_t R0, StageP stage,
+                                                uint32_t full, Acc& acc, uint32_t& careful) {
   if (!d.fast) {
     // no element can take the fast path: all elements of the full vectors are slow
     uint64_t all = 0;
@@ -1234,31 +1241,40 @@ __device__ __forceinline__ uint64_t phase_a_any(const SegDesc& d, int64_t L0, St
     }
     return all;
   }
-  const bool track = __ballot(acc.first_fast == kNone && (acc.gabs_k <= 0x80000000u || acc.grel_k <= 0x80000000u)) != 0;
-  uint64_t slow;
+  const bool track =
+      __ballot(acc.first_fast == kNone32 && (acc.gabs_k <= 0x80000000u || acc.grel_k <= 0x80000000u)) != 0;
+  PhaseA o;
   if (d.flags & KVV_FLAG_NEAR_ZERO) {
-    slow = phase_a<DT, true>(d, L0, stage, full, acc);
+    o = phase_a<DT, true>(d, stage, full);
   } else if constexpr (DotForm<DT>::on) {
     bool redone = false;
-    if (careful) {
+    if (__ballot(full != (1u << kUnroll) - 1) != 0) {
+      // a partial last vector (its elements are left to vec_tail): per-vector form
+      o = phase_a<DT, false>(d, stage, full);
+    } else if (careful) {
       --careful;
-      slow = phase_a_dot<DT, true>(d, L0, stage, full, acc, redone);
+      o = phase_a_dot<DT, true>(d, stage, full, redone);
     } else {
-      slow = phase_a_dot<DT, false>(d, L0, stage, full, acc, redone);
+      o = phase_a_dot<DT, false>(d, stage, full, redone);
       if (redone) careful = 8;
     }
   } else {
-    slow = phase_a<DT, false>(d, L0, stage, full, acc);
+    o = phase_a<DT, false>(d, stage, full);
   }
-  if (track) track_first_fast<DT>(L0, full, slow, acc);
+  acc.e_sq += o.esq;
+  acc.nfast += o.nfast;
+  acc.nnear_fast += o.nnear;
+  const uint64_t slow = o.slow;
+  if (track) track_first_fast<DT>(R0, full, slow, acc);
   return slow;
 }
 
 template <int DT, int MODE, int KIND, bool BATCH>
 __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   __shared__ typename ScanLds<DT, KIND>::type sm;
-  const int tid = threadIdx.x, w = tid >> 6;
-  if (tid < kWaves * WC_COUNT) (&sm.wcnt[0][0])[tid] = 0;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  uint32_t* wc = sm.wcnt[w];
+  if (lane < WC_COUNT) wc[lane] = 0;
   if (a.zero_n4) {
     // the select histograms and counters of this call start at zero (the later
     // launches accumulate into them; nothing in this kernel touches them)
@@ -1267,14 +1283,14 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
     const int64_t z1 = z0 + per < a.zero_n4 ? z0 + per : a.zero_n4;
     for (int64_t i = z0 + tid; i < z1; i += kBlock) a.zero_ptr[i] = make_uint4(0, 0, 0, 0);
   }
-  const int64_t i0 = a.item_lo + (int64_t)blockIdx.x * a.items_per_block;
-  int64_t i1 = i0 + a.items_per_block;
+  // each wave owns a contiguous range of items; the waves of a block never wait
+  // for each other
+  const int64_t i0 = a.item_lo + ((int64_t)blockIdx.x * kWaves + w) * a.items_per_wave;
+  int64_t i1 = i0 + a.items_per_wave;
   if (i1 > a.item_lo + a.items) i1 = a.item_lo + a.items;
   if (i0 >= i1) return;
-  __syncthreads();
   Acc acc;
   acc.init();
-  uint32_t* wc = sm.wcnt[w];
   int s = 0;
   if constexpr (BATCH) {
     int lo = 0, hi = a.nseg - 1;
@@ -1289,8 +1305,10 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   uint4 gv[kUnroll], rv[kUnroll];
   uint32_t full = 0, careful = 0;
   bool loaded = false;
-  PendingSample pend;
-  pend.at = kNone;
+  SampleLine line;
+  line.sb0 = kNone;
+  line.lo = line.fill = 0;
+  line.abs = line.rel = 0.0f;
   SampleCursor cur;
   {
     const SegDesc& d = BATCH ? a.table[s] : a.seg0;
@@ -1301,7 +1319,8 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
       if (it >= a.table[s].item_begin + a.table[s].item_count) {
         const int prev_s = s;
         while (it >= a.table[s].item_begin + a.table[s].item_count) ++s;
-        flush_run(acc, sm.wcnt, sm.bs, a.runs, run_slot(a.table[prev_s], run_start));
+        flush_run(acc, wc, a.runs, run_slot(a.table[prev_s], run_start),
+                  (run_start - a.table[prev_s].item_begin) * (int64_t)a.table[prev_s].item_elems);
         run_start = it;
         near_prev = 0;
         loaded = false;
@@ -1311,19 +1330,21 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
     const SegDesc& d = BATCH ? a.table[s] : a.seg0;
     const int64_t L0 = (it - d.item_begin) * (int64_t)d.item_elems;
     const int64_t L1 = L0 + d.item_elems < d.n ? L0 + d.item_elems : d.n;
+    const int64_t base = (run_start - d.item_begin) * (int64_t)d.item_elems;  // the run's first element
+    const uint32_t R0 = (uint32_t)(L0 - base);
     if constexpr (KIND == K_SCALAR) {
-      scan_item_scalar<DT, MODE>(d, L0, L1, acc, wc);
+      scan_item_scalar<DT, MODE>(d, L0, L1, base, acc, wc);
       sample_range<DT, MODE>(d, L0, L1, acc, a.sample_abs, a.sample_rel);
     } else {
       if (!loaded) full = load_item<DT, KIND>(d, L0, L1, gv, rv);
+      if (full != (1u << kUnroll) - 1) patch_partial<DT, KIND>(d, L0, L1, full, gv, rv);
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        sm.stage[(2 * u) * kBlock + tid] = gv[u];
-        sm.stage[(2 * u + 1) * kBlock + tid] = rv[u];
+        sm.stage[w][(2 * u) * 64 + lane] = gv[u];
+        sm.stage[w][(2 * u + 1) * 64 + lane] = rv[u];
       }
       const uint32_t full_now = full;
-      StageP stage = (StageP)sm.stage;
-      store_pending(pend, a.sample_abs, a.sample_rel);
+      StageP stage = (StageP)sm.stage[w];
       // next item of the same segment: its loads fly while this one finishes
       loaded = false;
       if (it + 1 < i1 && it + 1 < d.item_begin + d.item_count) {
@@ -1332,18 +1353,18 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
         full = load_item<DT, KIND>(d, N0, N1, gv, rv);
         loaded = true;
       }
-      sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, pend);
-      const uint64_t slow = phase_a_any<DT>(d, L0, stage, full_now, acc, careful);
+      sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, line);
+      const uint64_t slow = phase_a_any<DT>(d, L0, R0, stage, full_now, acc, careful);
       const uint32_t nslow = __ballot(slow != 0) ? build_queue<VecIO<DT>::NE>(slow, sm.queue[w]) : 0u;
-      if (nslow) phase_b<DT, MODE>(d, L0, nslow, stage, sm.queue[w], acc, wc);
-      if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, full_now, acc, wc);
+      if (nslow) phase_b<DT, MODE>(d, R0, nslow, stage, sm.queue[w], acc, wc);
+      if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, R0, full_now, stage, acc, wc);
     }
-    if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, sm, near_prev);
+    if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, wc, near_prev);
   }
-  store_pending(pend, a.sample_abs, a.sample_rel);
+  line_store(line, a.sample_abs, a.sample_rel);
   {
     const SegDesc& d = BATCH ? a.table[s] : a.seg0;
-    flush_run(acc, sm.wcnt, sm.bs, a.runs, run_slot(d, run_start));
+    flush_run(acc, wc, a.runs, run_slot(d, run_start), (run_start - d.item_begin) * (int64_t)d.item_elems);
   }
 }
 

@@ -163,6 +163,19 @@ def _dot_form_edges(rng):
     g[::31] ^= 1
     out.append(("fp8_e4m3fn_nan_codes", g.view(torch.float8_e4m3fn), codes.view(torch.float8_e4m3fn), None))
     out.append(("fp8_e5m2_nonfinite_codes", g.view(torch.float8_e5m2), codes.view(torch.float8_e5m2), None))
+    # rel_diff = +inf from finite abs_diff (huge gen over a zero reference) at many
+    # positions: the argmax is the lowest of them, whichever order a lane meets them in
+    for dt, nm in ((torch.bfloat16, "bf16"), (torch.float32, "fp32")):
+        r = torch.from_numpy(rng.standard_normal(40_000).astype(np.float32)).to(dt)
+        g = _flip_codes(r.view(torch.int16 if dt == torch.bfloat16 else torch.int32), rng, 0.1).view(dt)
+        v = 8 if dt == torch.bfloat16 else 4
+        # lane 63 of the first wave (queued last, after the 10% flips of lanes
+        # 0..62 fill earlier rounds) holds the lowest one; lane 0 holds a higher one
+        inf_at = torch.cat([torch.tensor([63 * v, 256 * v, 256 * v + 1]),
+                            torch.from_numpy(rng.choice(np.arange(3000, 40_000), 300, replace=False))])
+        r[inf_at] = 0.0
+        g[inf_at] = 1e30
+        out.append((f"{nm}_rel_inf_ties", g, r, None))
     ext = torch.from_numpy(rng.choice(np.array([0, 1, 127, 128, 129, 254, 255], dtype=np.uint8), n))
     ge = ext.clone()
     ge[::57] = 255 - ge[::57]
