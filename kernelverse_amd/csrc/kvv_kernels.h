@@ -867,28 +867,35 @@ __device__ __forceinline__ PhaseA phase_a_dot(const SegDesc& d, StageP stage, ui
   return o;
 }
 
-// Appends the lanes' remaining elements to the wave's queue in lane order
-// (entry = (lane << 6) | slot); returns the number of entries.
-template <int NE>
-__device__ __forceinline__ uint32_t build_queue(uint64_t slow, uint16_t* queue) {
+// The wave's queue holds 64 * kQSlots entries (entry = (lane << 6) | slot, in
+// lane order).  queue_all appends every slow element of the lanes when they
+// fit and returns their number, else returns it without writing anything;
+// queue_part then appends the slots [p0, p0 + kQSlots) of every lane.
+constexpr int kQSlots = 16;
+__device__ __forceinline__ uint32_t queue_all(uint64_t slow, uint16_t* queue) {
   const int lane = lane_id();
-  // a lane holds at most NE entries (slots 0..NE-1) and the queue has room for 64 * NE
-  if constexpr (NE < 64) slow &= (1ull << NE) - 1;
   const uint32_t cnt = (uint32_t)__popcll(slow);
   const uint32_t incl = wave_incl_scan(cnt);
   const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  if (total > 64u * kQSlots) return total;
   uint32_t at = incl - cnt;
-  if constexpr (NE <= 32) {
-    uint32_t m = (uint32_t)slow;
-    while (m) {
-      queue[at++] = (uint16_t)((lane << 6) | __builtin_ctz(m));
-      m &= m - 1;
-    }
-  } else {
-    while (slow) {
-      queue[at++] = (uint16_t)((lane << 6) | __builtin_ctzll(slow));
-      slow &= slow - 1;
-    }
+  while (slow) {
+    queue[at++] = (uint16_t)((lane << 6) | __builtin_ctzll(slow));
+    slow &= slow - 1;
+  }
+  return total;
+}
+
+__device__ __forceinline__ uint32_t queue_part(uint32_t part, int p0, uint16_t* queue) {
+  const int lane = lane_id();
+  part &= (1u << kQSlots) - 1;
+  const uint32_t cnt = (uint32_t)__popc(part);
+  const uint32_t incl = wave_incl_scan(cnt);
+  const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  uint32_t at = incl - cnt;
+  while (part) {
+    queue[at++] = (uint16_t)((lane << 6) | (p0 + __builtin_ctz(part)));
+    part &= part - 1;
   }
   return total;
 }
@@ -982,62 +989,47 @@ __device__ __forceinline__ void sample_write(const SegDesc& d, typename Elem<DT>
   srel[d.sample_off + i] = rel;
 }
 
-// A wave's line buffer of sample values.  Lane l holds the values of sample
-// position sb0 + l (positions in the sample arrays; sb0 is a multiple of 64)
-// and lanes [lo, fill) are valid.  A full buffer is written as one 256-byte
-// store per array, so the sample arrays are written in whole lines: scattered
-// 4-byte stores of partial lines cost HBM bandwidth well beyond their bytes.
-struct SampleLine {
-  uint64_t sb0;       // kNone: empty
-  uint32_t lo, fill;
-  float abs, rel;
+// A wave's buffer of sample values in LDS: abs and rel of the consecutive
+// sample positions [at0, at0 + fill).  It is written out (coalesced) when full,
+// when the positions stop being consecutive (a new segment) and at the end of
+// the wave's range.  Sample values written to HBM while the scan streams its
+// inputs cost far more read bandwidth than their bytes, so a wave whose samples
+// fit (kSampleBuf) writes them all at the end.
+constexpr int kSampleBuf = 384;
+struct SampleBuf {
+  uint64_t at0;  // kNone: empty
+  uint32_t fill;
 };
 
-__device__ __forceinline__ void line_store(SampleLine& b, float* sabs, float* srel) {
-  const uint32_t lane = (uint32_t)lane_id();
-  if (b.sb0 != kNone && lane >= b.lo && lane < b.fill) {
-    sabs[b.sb0 + lane] = b.abs;
-    srel[b.sb0 + lane] = b.rel;
+__device__ __forceinline__ void sbuf_store(SampleBuf& b, KVV_LDS float* ba, KVV_LDS float* br, float* sabs,
+                                           float* srel) {
+  if (b.at0 != kNone) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (uint32_t k = (uint32_t)lane_id(); k < b.fill; k += 64) {
+      sabs[b.at0 + k] = ba[k];
+      srel[b.at0 + k] = br[k];
+    }
   }
-  b.sb0 = kNone;
+  b.at0 = kNone;
+  b.fill = 0;
 }
 
-// Places the values of c consecutive samples, held by lanes 0..c-1 (c <= 64),
-// at positions [at, at + c) of the buffer, writing it out when it fills.
-__device__ __forceinline__ void line_put(SampleLine& b, uint64_t at, int c, float va, float vr, float* sabs,
-                                         float* srel) {
-  const uint32_t lane = (uint32_t)lane_id();
-  if (b.sb0 != kNone && at != b.sb0 + b.fill) line_store(b, sabs, srel);  // not contiguous (a new segment)
-  if (b.sb0 == kNone) {
-    b.sb0 = at & ~63ull;
-    b.lo = b.fill = (uint32_t)(at - b.sb0);
+// Adds the values of c consecutive sample positions [at, at + c), held by lanes
+// 0..c-1 (c <= 64).
+__device__ __forceinline__ void sbuf_put(SampleBuf& b, uint64_t at, int c, float va, float vr, KVV_LDS float* ba,
+                                         KVV_LDS float* br, float* sabs, float* srel) {
+  if (b.at0 != kNone && (at != b.at0 + b.fill || b.fill + (uint32_t)c > (uint32_t)kSampleBuf))
+    sbuf_store(b, ba, br, sabs, srel);
+  if (b.at0 == kNone) b.at0 = at;
+  const int lane = lane_id();
+  if (lane < c) {
+    ba[b.fill + lane] = va;
+    br[b.fill + lane] = vr;
   }
-  const uint32_t k = b.fill;
-  // lane l of the buffer takes walk lane (l - k) mod 64
-  const int src = (int)((lane - k) & 63u);
-  const float ra = __shfl(va, src), rr = __shfl(vr, src);
-  const uint32_t end = k + (uint32_t)c;  // < 128
-  if (lane >= k && lane < end) {
-    b.abs = ra;
-    b.rel = rr;
-  }
-  if (end >= 64) {
-    b.fill = 64;
-    line_store(b, sabs, srel);
-    b.sb0 = (at & ~63ull) + 64;
-    b.lo = 0;
-    b.fill = end - 64;
-    if (lane < b.fill) {
-      b.abs = ra;
-      b.rel = rr;
-    }
-    if (b.fill == 0) b.sb0 = kNone;
-  } else {
-    b.fill = end;
-  }
-  b.sb0 = uniform(b.sb0);
-  b.lo = uniform(b.lo);
-  b.fill = uniform(b.fill);
+  b.fill = uniform(b.fill + (uint32_t)c);
+  b.at0 = uniform(b.at0);
 }
 
 // Samples of a vector item (GCR:346-347): the wave walks its cursor 64 samples
@@ -1047,7 +1039,8 @@ __device__ __forceinline__ void line_put(SampleLine& b, uint64_t at, int c, floa
 // max_samples every element is a sample (the host sets the stride to 1).
 template <int DT, int MODE>
 __device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_t L1, StageP stage, Acc& acc,
-                                            float* sabs, float* srel, SampleCursor& cur, SampleLine& line) {
+                                            float* sabs, float* srel, SampleCursor& cur, SampleBuf& sb,
+                                            KVV_LDS float* ba, KVV_LDS float* br) {
   using IO = VecIO<DT>;
   using T = typename IO::T;
   constexpr int V = IO::V;
@@ -1078,7 +1071,7 @@ __device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_
       const T rc = stage_elem<T>(stage, (2 * u + 1) * 64 + tt, e);
       sample_value<DT, MODE>(d, gc, rc, acc, adf, rel);
     }
-    line_put(line, d.sample_off + cur.i, c, adf, rel, sabs, srel);
+    sbuf_put(sb, d.sample_off + cur.i, c, adf, rel, ba, br, sabs, srel);
     const uint32_t offl = (uint32_t)__builtin_amdgcn_readlane((int)off, c - 1);
     uint32_t nr = (uint32_t)__builtin_amdgcn_readlane((int)rem, c - 1) + smod;
     uint64_t nidx = (uint64_t)L0 + offl + d.s_div;
@@ -1201,18 +1194,20 @@ __device__ inline void flush_run(Acc& acc, uint32_t* wc, const RunCols& out, int
 // ------------------------------------------------------------ scan kernel
 // LDS of one scan block: per wave, its item's vectors (SW uint4: kUnroll
 // vectors of each tensor per lane), its queue of stage positions (NQ = 64 lanes
-// x elements per lane) and its counters.  Waves never touch each other's part.
+// x kQSlots), its sample buffer (abs and rel values of kSampleBuf consecutive
+// sample positions) and its counters.  Waves never touch each other's part.
 template <int SW, int NQ>
 struct ScanShared {
   uint4 stage[kWaves][SW];
   uint16_t queue[kWaves][NQ];
+  float sbuf[kWaves][2][kSampleBuf];
   uint32_t wcnt[kWaves][WC_COUNT];
 };
 
 template <int DT, int KIND>
 struct ScanLds {
   static constexpr bool vec = KIND != K_SCALAR;
-  using type = ScanShared<vec ? 2 * kUnroll * 64 : 1, vec ? 64 * VecIO<DT>::NE : 2>;
+  using type = ScanShared<vec ? 2 * kUnroll * 64 : 1, vec ? 64 * kQSlots : 2>;
 };
 
 // Per-item near-zero count of the wave (feeds the compacted-rank prefix of near_kernel).
@@ -1305,10 +1300,11 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   uint4 gv[kUnroll], rv[kUnroll];
   uint32_t full = 0, careful = 0;
   bool loaded = false;
-  SampleLine line;
-  line.sb0 = kNone;
-  line.lo = line.fill = 0;
-  line.abs = line.rel = 0.0f;
+  SampleBuf sb;
+  sb.at0 = kNone;
+  sb.fill = 0;
+  KVV_LDS float* ba = (KVV_LDS float*)sm.sbuf[w][0];
+  KVV_LDS float* br = (KVV_LDS float*)sm.sbuf[w][1];
   SampleCursor cur;
   {
     const SegDesc& d = BATCH ? a.table[s] : a.seg0;
@@ -1353,15 +1349,24 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
         full = load_item<DT, KIND>(d, N0, N1, gv, rv);
         loaded = true;
       }
-      sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, line);
+      sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, sb, ba, br);
       const uint64_t slow = phase_a_any<DT>(d, L0, R0, stage, full_now, acc, careful);
-      const uint32_t nslow = __ballot(slow != 0) ? build_queue<VecIO<DT>::NE>(slow, sm.queue[w]) : 0u;
-      if (nslow) phase_b<DT, MODE>(d, R0, nslow, stage, sm.queue[w], acc, wc);
+      if (__ballot(slow != 0)) {
+        uint32_t nq = queue_all(slow, sm.queue[w]);
+        // more than the queue holds: kQSlots slots of every lane at a time
+        const bool split = nq > 64u * kQSlots;
+#pragma unroll 1
+        for (int p0 = 0;; p0 += kQSlots) {
+          if (split) nq = queue_part((uint32_t)(slow >> p0), p0, sm.queue[w]);
+          if (nq) phase_b<DT, MODE>(d, R0, nq, stage, sm.queue[w], acc, wc);
+          if (!split || p0 + kQSlots >= VecIO<DT>::NE) break;
+        }
+      }
       if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, R0, full_now, stage, acc, wc);
     }
     if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, wc, near_prev);
   }
-  line_store(line, a.sample_abs, a.sample_rel);
+  if constexpr (KIND != K_SCALAR) sbuf_store(sb, ba, br, a.sample_abs, a.sample_rel);
   {
     const SegDesc& d = BATCH ? a.table[s] : a.seg0;
     flush_run(acc, wc, a.runs, run_slot(d, run_start), (run_start - d.item_begin) * (int64_t)d.item_elems);
