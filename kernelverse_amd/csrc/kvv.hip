@@ -393,10 +393,12 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   ScanFn scan = scan_fn(d.dtype, d.mode, kind, false);
   if (!scan) return fail(KVV_E_INVALID, "no kernel for dtype");
   const int64_t target = blocks_target(scan) * kWaves;  // waves of the grid
+  const int64_t ipw = d.item_count > 0 ? (d.item_count + target - 1) / target : 1;  // items per wave
+  // one run record per block: its waves fold theirs (a single-segment launch)
   d.run_base = 0;
-  d.run_ipb = d.item_count > 0 ? (d.item_count + target - 1) / target : 1;  // items per wave
+  d.run_ipb = ipw * kWaves;
   if ((uint64_t)d.run_ipb * (uint64_t)d.item_elems >= (1ull << 32))
-    return fail(KVV_E_UNSUPPORTED, "tensor too large for 32-bit per-wave counts");
+    return fail(KVV_E_UNSUPPORTED, "tensor too large for 32-bit per-block counts");
   if (d.item_count > 0) {
     ScanArgs a{};
     a.seg0 = d;
@@ -404,7 +406,7 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     a.nseg = 1;
     a.item_lo = 0;
     a.items = d.item_count;
-    a.items_per_wave = d.run_ipb;
+    a.items_per_wave = ipw;
     a.runs = run_cols(L, ws);
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);

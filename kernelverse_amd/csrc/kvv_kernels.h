@@ -1137,7 +1137,22 @@ __device__ __forceinline__ int64_t run_slot(const SegDesc& d, int64_t it) {
 // run.  `base` is the logical index of the run's first element (the origin of
 // the accumulators' 32-bit offsets).
 static_assert(kColU32 == 32 && kColU64 <= 32, "one lane per run column");
-__device__ inline void flush_run(Acc& acc, uint32_t* wc, const RunCols& out, int64_t slot, int64_t base) {
+// Where a run record goes: the run columns in global memory, or (a wave's part
+// of a block record) an LDS record of kColU32 + kColU64 words.
+struct ColSink {
+  const RunCols* out;
+  int64_t slot;
+  __device__ void put32(int c, uint32_t v) const { out->u32[c * out->stride + slot] = v; }
+  __device__ void put64(int c, uint64_t v) const { out->u64[c * out->stride + slot] = v; }
+};
+struct LdsRecord {
+  KVV_LDS uint32_t* u32;
+  KVV_LDS uint64_t* u64;
+  __device__ void put32(int c, uint32_t v) const { u32[c] = v; }
+  __device__ void put64(int c, uint64_t v) const { u64[c] = v; }
+};
+template <class Sink>
+__device__ inline void flush_run(Acc& acc, uint32_t* wc, const Sink& out, int64_t base) {
   const int lane = lane_id();
   const uint32_t nfast = wave_sum(acc.nfast);
   const uint32_t nmm = wave_sum(acc.nmm);
@@ -1172,7 +1187,7 @@ __device__ inline void flush_run(Acc& acc, uint32_t* wc, const RunCols& out, int
     } else {
       v = lane == CU_MISM ? nmm : lane == CU_MMABS ? mma : lane == CU_MMREL ? mmr : lane == CU_GABSK ? gak : grk;
     }
-    out.u32[lane * out.stride + slot] = v;
+    out.put32(lane, v);
   } else if (lane < 32 + kColU64) {
     const int c = lane - 32;
     uint64_t v;
@@ -1186,9 +1201,52 @@ __device__ inline void flush_run(Acc& acc, uint32_t* wc, const RunCols& out, int
       for (int i = 1; i < 7; ++i) x = (c - CL_S0 == i) ? sm[i] : x;
       v = (uint64_t)__double_as_longlong(x);
     }
-    out.u64[c * out.stride + slot] = v;
+    out.put64(c, v);
   }
   acc.init();
+}
+
+// The last wave of a block to finish folds the block's kWaves wave records
+// (LDS, waves in order, so fp64 sums are reproducible) into one run record.
+__device__ inline void fold_block_record(const LdsRecord* rec, const RunCols& out, int64_t slot) {
+  const int lane = lane_id();
+  if (lane < kColU32) {
+    if (lane == CU_GABSK || lane == CU_GRELK) {
+      const int ci = lane == CU_GABSK ? CL_GABSI : CL_GRELI;
+      uint32_t bk = rec[0].u32[lane];
+      uint64_t bi = rec[0].u64[ci];
+      for (int w = 1; w < kWaves; ++w) {
+        const uint32_t k = rec[w].u32[lane];
+        const uint64_t i = rec[w].u64[ci];
+        if (better(k, i, bk, bi)) {
+          bk = k;
+          bi = i;
+        }
+      }
+      out.u32[lane * out.stride + slot] = bk;
+      out.u64[ci * out.stride + slot] = bi;
+    } else {
+      const bool mx = lane == CU_MMABS || lane == CU_MMREL;
+      uint32_t v = rec[0].u32[lane];
+      for (int w = 1; w < kWaves; ++w) {
+        const uint32_t x = rec[w].u32[lane];
+        v = mx ? (x > v ? x : v) : v + x;
+      }
+      out.u32[lane * out.stride + slot] = v;
+    }
+  } else if (lane < 32 + kColU64) {
+    const int c = lane - 32;
+    if (c == CL_GABSI || c == CL_GRELI) return;  // written with their keys
+    if (c == CL_FIRSTMM || c == CL_FIRSTVIOL) {
+      uint64_t v = rec[0].u64[c];
+      for (int w = 1; w < kWaves; ++w) v = rec[w].u64[c] < v ? rec[w].u64[c] : v;
+      out.u64[c * out.stride + slot] = v;
+    } else {
+      double v = __longlong_as_double((long long)rec[0].u64[c]);
+      for (int w = 1; w < kWaves; ++w) v += __longlong_as_double((long long)rec[w].u64[c]);
+      out.u64[c * out.stride + slot] = (uint64_t)__double_as_longlong(v);
+    }
+  }
 }
 
 // ------------------------------------------------------------ scan kernel
@@ -1198,6 +1256,7 @@ __device__ inline void flush_run(Acc& acc, uint32_t* wc, const RunCols& out, int
 // sample positions) and its counters.  Waves never touch each other's part.
 template <int SW, int NQ>
 struct ScanShared {
+  uint32_t done;  // waves of the block that have left their record (single-segment launches)
   uint4 stage[kWaves][SW];
   uint16_t queue[kWaves][NQ];
   float sbuf[kWaves][2][kSampleBuf];
@@ -1207,7 +1266,8 @@ struct ScanShared {
 template <int DT, int KIND>
 struct ScanLds {
   static constexpr bool vec = KIND != K_SCALAR;
-  using type = ScanShared<vec ? 2 * kUnroll * 64 : 1, vec ? 64 * kQSlots : 2>;
+  // (the scalar kind stages nothing, but its waves leave their run records there)
+  using type = ScanShared<vec ? 2 * kUnroll * 64 : (kColU32 * 4 + kColU64 * 8 + 15) / 16, vec ? 64 * kQSlots : 2>;
 };
 
 // Per-item near-zero count of the wave (feeds the compacted-rank prefix of near_kernel).
@@ -1264,12 +1324,37 @@ __device__ __forceinline__ uint64_t phase_a_any(const SegDesc& d, int64_t L0, ui
   return slow;
 }
 
+// A wave of a single-segment launch leaves its run record in its own stage
+// region (its items are done) and checks in; the last wave of the block folds
+// the block's records into the block's run slot (runs are per block there).
+template <class SM>
+__device__ inline void block_record_part(const ScanArgs& a, SM& sm, Acc& acc, uint32_t* wc, int w, int64_t base) {
+  auto rec_of = [&sm](int x) {
+    KVV_LDS uint64_t* r = (KVV_LDS uint64_t*)(KVV_LDS uint4*)sm.stage[x];
+    return LdsRecord{(KVV_LDS uint32_t*)(r + kColU64), r};
+  };
+  flush_run(acc, wc, rec_of(w), base);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  uint32_t old = 0;
+  if (lane_id() == 0) old = atomicAdd(&sm.done, 1u);
+  old = uniform(old);
+  if (old != kWaves - 1) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  LdsRecord rec[kWaves];
+  for (int x = 0; x < kWaves; ++x) rec[x] = rec_of(x);
+  fold_block_record(rec, a.runs, blockIdx.x);
+}
+
 template <int DT, int MODE, int KIND, bool BATCH>
 __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   __shared__ typename ScanLds<DT, KIND>::type sm;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   uint32_t* wc = sm.wcnt[w];
   if (lane < WC_COUNT) wc[lane] = 0;
+  if constexpr (!BATCH) {
+    if (tid == 0) sm.done = 0;
+    __syncthreads();
+  }
   if (a.zero_n4) {
     // the select histograms and counters of this call start at zero (the later
     // launches accumulate into them; nothing in this kernel touches them)
@@ -1283,9 +1368,14 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   const int64_t i0 = a.item_lo + ((int64_t)blockIdx.x * kWaves + w) * a.items_per_wave;
   int64_t i1 = i0 + a.items_per_wave;
   if (i1 > a.item_lo + a.items) i1 = a.item_lo + a.items;
-  if (i0 >= i1) return;
   Acc acc;
   acc.init();
+  if (i0 >= i1) {
+    // a single-segment launch folds one record per block: an empty wave still
+    // leaves its (empty) part
+    if constexpr (!BATCH) block_record_part(a, sm, acc, wc, w, a.seg0.item_begin);
+    return;
+  }
   int s = 0;
   if constexpr (BATCH) {
     int lo = 0, hi = a.nseg - 1;
@@ -1315,8 +1405,8 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
       if (it >= a.table[s].item_begin + a.table[s].item_count) {
         const int prev_s = s;
         while (it >= a.table[s].item_begin + a.table[s].item_count) ++s;
-        flush_run(acc, wc, a.runs, run_slot(a.table[prev_s], run_start),
-                  (run_start - a.table[prev_s].item_begin) * (int64_t)a.table[prev_s].item_elems);
+        const ColSink out{&a.runs, run_slot(a.table[prev_s], run_start)};
+        flush_run(acc, wc, out, (run_start - a.table[prev_s].item_begin) * (int64_t)a.table[prev_s].item_elems);
         run_start = it;
         near_prev = 0;
         loaded = false;
@@ -1367,9 +1457,13 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
     if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, wc, near_prev);
   }
   if constexpr (KIND != K_SCALAR) sbuf_store(sb, ba, br, a.sample_abs, a.sample_rel);
-  {
-    const SegDesc& d = BATCH ? a.table[s] : a.seg0;
-    flush_run(acc, wc, a.runs, run_slot(d, run_start), (run_start - d.item_begin) * (int64_t)d.item_elems);
+  const SegDesc& d = BATCH ? a.table[s] : a.seg0;
+  const int64_t base = (run_start - d.item_begin) * (int64_t)d.item_elems;
+  if constexpr (BATCH) {
+    const ColSink out{&a.runs, run_slot(d, run_start)};
+    flush_run(acc, wc, out, base);
+  } else {
+    block_record_part(a, sm, acc, wc, w, base);
   }
 }
 
