@@ -1,24 +1,26 @@
 // Verdict kernels for gfx950 (wave64).
 //
-//   scan_kernel     one HBM pass over both tensors.  Every block owns a
-//                   contiguous range of "items" (fixed-size chunks of one
-//                   segment) and writes one partial record per run of items
-//                   of the same segment.  Inside an item, phase A settles the
-//                   bit-identical finite pairs with packed-integer tests on
-//                   whole dwords; the other pairs are compacted per wave into
-//                   an LDS queue and processed densely (phase B).  The next
-//                   item's loads are in flight meanwhile.  The strided sample
-//                   of the reference's p99/cosine/norm-ratio comes from the
-//                   item's LDS copy.
-//   reduce_kernel   one block per segment: folds its run records in a fixed
-//                   order (bit-reproducible) into kvv_result and clears the
-//                   select histograms, state and counters.
-//   near_kernel     tolerant-policy near-zero diagnostics: the rank-strided
-//                   sample of the compacted near-zero abs_diff array.
-//   select_kernel   exact order statistics of the sample arrays: 4 launches
-//                   of an 8-bit radix select over shared histograms; the last
-//                   block of each (segment, array) advances the prefix, and
-//                   after the last digit interpolates like torch.quantile.
+//   scan_kernel   one HBM pass over both tensors.  Every wave owns a
+//                 contiguous range of "items" (64 lanes x kUnroll 16-byte
+//                 vectors of each tensor) and streams it with no block
+//                 barrier; the next item's loads are in flight while the
+//                 current one, staged in the wave's LDS region, is processed:
+//                   phase A  bit-identical finite pairs settled with packed
+//                            dot products (their squares feed the fp64 sums);
+//                            an exact per-element form re-runs an item whose
+//                            dot sums leave the range where they are exact;
+//                   phase B  the other pairs, compacted into a per-wave LDS
+//                            queue, get the full per-element treatment;
+//                   samples  the strided sample of p99 / cosine / norm ratio,
+//                            gathered from the stage into a per-wave LDS
+//                            buffer that is written out at the end.
+//                 A single-pair launch folds its four wave records into one
+//                 block record (last wave of the block); a batch launch
+//                 writes one record per wave and segment run.
+//   near_kernel   tolerant-policy near-zero diagnostics: the rank-strided
+//                 sample of the compacted near-zero abs_diff array.
+//   tail_kernel   (kvv_tail.h) the fold of the run records into kvv_result
+//                 and the radix selection of the p99 order statistics.
 #pragma once
 
 #include "kvv_device.h"

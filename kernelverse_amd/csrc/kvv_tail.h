@@ -24,7 +24,7 @@ struct TailArgs {
   const int64_t* chunk_seg;   // batch: owning segment of each select chunk
   int32_t nseg;
   int32_t reduce_blocks;      // leading blocks that fold run records (reduce_roles per segment), 0 for none
-  int32_t reduce_roles;       // 3, or 4 with the near-zero prefix
+  int32_t reduce_roles;       // 5, or 6 with the near-zero prefix
   int32_t level;              // select digit level 0, 1 or 2 (small groups are done at level 0)
   int32_t arr_lo;             // select blocks cover arrays [arr_lo, arr_lo + narr)
   int32_t narr;
