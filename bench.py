@@ -22,6 +22,10 @@ Configurations (BASELINE.json ``configs``): c0 fp32 1 Mi, c1 bf16 256 Mi
 (default, the headline), c2 fp16 4096x32768 strided, c3fp8 / c3int8 128 Mi,
 c4 ragged batch of 4096 fp32/bf16 pairs (events then bracket the whole call).
 
+``--trial`` instead times the correctness trial's verdict stage on C1-shaped
+outputs: the device trial driver (kernelverse_amd/trial.py) against the
+reference's host copies plus the torch-CPU compare.
+
 ``roofline.traffic`` is the main pass's HBM bytes per launch from rocprofv3
 FETCH_SIZE / WRITE_SIZE runs scaled by a plain-copy calibration
 (``--copy-calibration``), recorded in PMC_TRAFFIC below; null where not measured.
@@ -165,6 +169,75 @@ def copy_calibration(steps: int):
           flush=True)
 
 
+def trial_measurement(args):
+    """The correctness trial's verdict stage on C1-shaped outputs (GCR:1281-1322).
+
+    Device side: ``kernelverse_amd.trial._run_correctness_trial_once`` end to
+    end; the operator pair returns the resident C1 pair, so the time is the
+    trial's own work: seeding, model construction, the verdict on the device
+    outputs and the meta assembly.  Reference side (its CPU baseline leg): the
+    same outputs copied to the host as the reference does (``_to_cpu``,
+    GCR:1315-1316), then the torch-CPU oracle ``compare_outputs`` over them, once.
+    """
+    from kernelverse_amd import _lib, synth, trial
+    from oracle import torch_verdict as tv
+
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    g, r = synth.c1_pair(dev)
+    tol = {"BF16": {"rtol": 1.6e-2, "atol": 1e-2}}
+    torch.cuda.synchronize()
+
+    class Generated(torch.nn.Module):
+        def __init__(self, shape):
+            super().__init__()
+
+        def forward(self, x):
+            return g
+
+    class Reference(Generated):
+        def forward(self, x):
+            return r
+
+    kw = dict(language="hip", correctness_shape={}, generated_model_class=Generated, reference_model_class=Reference,
+              generate_inputs_fn=lambda shape: torch.zeros(1), backend=None, device=dev, input_seed=1024,
+              param_seed=10_001_024, tolerance_policy=tol, correctness_policy=None)
+    for _ in range(args.warmup):
+        trial._run_correctness_trial_once(**kw)
+    times = []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ok, details, metas = trial._run_correctness_trial_once(**kw)
+        times.append(time.perf_counter() - t0)
+    dev_ms = 1e3 * statistics.median(times)
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    log("[bench] reference-style stage: host copies, then the CPU oracle")
+    t0 = time.perf_counter()
+    g_cpu, r_cpu = trial._to_cpu(g), trial._to_cpu(r)
+    d2h_ms = 1e3 * (time.perf_counter() - t0)
+    t0 = time.perf_counter()
+    ref_ok, ref_details, ref_metas = tv.compare_outputs(g_cpu, r_cpu, tolerance_policy=tol)
+    cpu_ms = 1e3 * (time.perf_counter() - t0)
+    same = (ok == ref_ok and details == ref_details
+            and all(m.get(k) == rm.get(k) for m, rm in zip(metas, ref_metas)
+                    for k in ("mismatch_rate", "p99_abs", "p99_rel", "max_abs", "max_rel", "first_mismatch_index")))
+    print(json.dumps({
+        "metric": "correctness trial verdict stage on C1-shaped outputs (ms per trial)",
+        "value": round(dev_ms, 3), "unit": "ms", "higher_is_better": False, "steps": args.steps,
+        "device_trial_ms_median": round(dev_ms, 3),
+        "reference_stage_ms": round(d2h_ms + cpu_ms, 1),
+        "reference_d2h_ms": round(d2h_ms, 1),
+        "reference_cpu_compare_ms": round(cpu_ms, 1),
+        "speedup": round((d2h_ms + cpu_ms) / dev_ms, 1),
+        "same_verdict": bool(same),
+        "cpu_threads": threads,
+        "config": {"workload": "c1 outputs: bf16 pair of 268,435,456 elements, atol=1e-2 rtol=1.6e-2, strict policy"},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -175,6 +248,9 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time a plain 512 MiB device copy instead (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counts to bytes)")
+    ap.add_argument("--trial", action="store_true",
+                    help="time the correctness trial's verdict stage (device) against the reference's host copies "
+                         "plus CPU compare, on C1-shaped outputs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the verdict path has no multi-GPU mode "
@@ -184,6 +260,9 @@ def main():
         raise SystemExit("bench.py needs a ROCm GPU")
     if args.copy_calibration:
         copy_calibration(args.steps)
+        return
+    if args.trial:
+        trial_measurement(args)
         return
     from kernelverse_amd import _lib, synth, verdict
 

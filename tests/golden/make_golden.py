@@ -15,6 +15,13 @@ reference ships, and ``_correctness_criteria`` for each policy kind.
 
 The fixtures pin the branching and reporting logic (key order, rounding,
 policy rules, detail strings) that no library routine or closed form pins.
+
+``--part host`` writes only the fixtures of the code around the verdict:
+``host_logic.json`` (random-mode configuration and summary GCR:250-302; the
+timing payload and per-operator perf seed of ``utils/performance.py``),
+``finalize_cases_*.json`` (case finalisation GCR:999-1040, 1760-1810) and
+``trial_cases.json`` (``_run_correctness_trial_once`` GCR:1281-1322 run on the
+CPU with the operator pairs of ``tests/trial_models.py``).
 """
 
 from __future__ import annotations
@@ -330,5 +337,110 @@ def main(reference_root: str) -> None:
     print(f"wrote {len(out_cases)} verdict cases in {len(chunks)} files, {len(policies)} policy resolutions")
 
 
+# ------------------------------------------------------------- code around the verdict
+def _outcome(fn, *args, **kwargs):
+    """What a reference call returns, or the exception it raises."""
+    try:
+        return {"value": encode_value(fn(*args, **kwargs))}
+    except Exception as exc:  # the reference raising is itself the expected result
+        return {"raises": type(exc).__name__, "message": str(exc)}
+
+
+def host_fixtures(reference_root: str) -> None:
+    sys.dont_write_bytecode = True
+    sys.path.insert(0, reference_root)
+    import copy
+
+    import runner.correctness_policy as cp  # noqa: E402
+    import runner.generated_correctness_runner as gcr  # noqa: E402
+    import utils.performance as perf  # noqa: E402
+
+    sys.path.insert(0, str(HERE.parent))
+    import trial_models  # noqa: E402
+
+    # random-mode configuration and summary
+    specs = [{"op_name": "a", "config": {}}, {"op_name": "b", "config": None}, {"config": {"random_correctness": {}}},
+             {"op_name": "c", "config": {"random_correctness": {"max_failed_case_rate": 0.1}}},
+             {"op_name": "d", "config": {"random_correctness": {"max_failed_case_rate": "0.25"}}},
+             {"op_name": "e", "config": {"random_correctness": {"max_failed_case_rate": "x"}}},
+             {"op_name": "f", "config": {"random_correctness": {"max_failed_case_rate": None}}},
+             {"op_name": "g", "config": {"random_correctness": {"max_failed_case_rate": 1.5}}},
+             {"op_name": "h", "config": {"random_correctness": {"max_failed_case_rate": -0.01}}},
+             {"op_name": "i", "config": {"random_correctness": [0.1]}},
+             {"op_name": "j", "config": {"random_correctness": {"max_failed_case_rate": 0}}},
+             {"op_name": "k", "config": {"random_correctness": {"max_failed_case_rate": 1}}}]
+    resolve = [{"spec": sp, "expected": _outcome(gcr._resolve_random_correctness_config, sp)} for sp in specs]
+    summaries = []
+    for mode in ("random", "single", "fixed"):
+        for total, failed in ((0, 0), (1, 0), (1, 1), (3, 1), (33, 1), (100, 3), (100, 4), (7, 7), (10, 0)):
+            for rate in (0.0, 0.03, 0.5, 1.0):
+                kw = dict(shape_mode=mode, total_cases=total, failed_cases=failed,
+                          random_correctness_config={"max_failed_case_rate": rate})
+                summaries.append({"kwargs": kw, "expected": _outcome(gcr._random_case_summary, **kw)})
+
+    def case(i, ok, details=None, **extra):
+        c = {"case_index": i, "success": ok, "failed_trials": [{"case_index": i, "trial": 0, "details": d}
+                                                               for d in (details or [])]}
+        c.update(extra)
+        return c
+
+    results = [
+        {"language": "cuda", "cases": [case(2, True), case(0, True), case(1, True)]},
+        {"language": "cuda", "cases": [case(1, False, [["output mismatch"]]), case(0, True)]},
+        {"language": "cuda", "cases": []},
+        {"language": "hip", "cases": [case(i, i % 40 != 5, [["x"]] if i % 40 == 5 else None) for i in range(40)]},
+        {"language": "biren", "cases": [case(0, False, error_type="CaseCompileFailed")]},
+        {"language": "BIREN", "cases": [case(0, False, [["fatal error: main.cpp: No such file or directory"]])]},
+        {"language": "biren", "cases": [case(0, False, [["fatal error: something else"]])]},
+        {"language": "biren", "cases": [case(0, True, performance_error_message={"generated": "ninja: build stopped"})]},
+        {"language": "biren", "cases": [case(0, True, performance_error_message="Error building extension 'x'")]},
+        {"language": "cuda", "cases": [case(0, False, error_type="CaseCompileFailed")]},
+        {"language": "cuda", "cases": [{"case_index": 0}, case(1, True)]},
+    ]
+    finals = []
+    for res in results:
+        for mode in ("random", "single"):
+            for total in (None, len(res["cases"]), len(res["cases"]) + 1):
+                r = copy.deepcopy(res)
+                r["correctness"] = {"existing": 1}
+                kw = dict(shape_mode=mode, random_correctness_config={"max_failed_case_rate": 0.03},
+                          total_cases=total)
+                finals.append({"result": copy.deepcopy(r), "kwargs": kw,
+                               "expected": _outcome(gcr.finalize_generated_operator_result, result=r, **kw)})
+    perf_results = [{"times": t, "expected": perf._build_cuda_perf_result(t)}
+                    for t in ([], [1.0], [0.5, 0.25], [1.23456, 1.23449, 2.0004999, 0.0001], list(np.linspace(0.1, 3, 17)))]
+    seeds = [{"op_name": n, "seed": perf.perf_seed_for_op(n)}
+             for n in ("op_benchmark/gelu/case_0/operator_defined", "matmul", "", "ünïcode")]
+    (HERE / "host_logic.json").write_text(json.dumps(
+        {"resolve_random_correctness": resolve, "random_case_summary": summaries,
+         "perf_result": perf_results, "perf_seed": seeds}, separators=(",", ":")))
+    half = (len(finals) + 1) // 2
+    for i, part in enumerate((finals[:half], finals[half:])):
+        (HERE / f"finalize_cases_{i:02d}.json").write_text(json.dumps(part, separators=(",", ":")))
+
+    # trials on the CPU: the reference's own driver, with host outputs
+    trials = []
+    for name, gen, ref, n, spec, tol in trial_models.TRIAL_CASES:
+        pol = cp.resolve_correctness_policy({"category": spec.get("category"), "op_name": spec.get("op_name"),
+                                             "config": spec.get("config") or {}}) if spec else None
+        tol = tol if tol is not None else gcr.TOLERANCE_POLICY
+        out = _outcome(gcr._run_correctness_trial_once, language="cuda", correctness_shape={"n": n},
+                       generated_model_class=trial_models.MODELS[gen], reference_model_class=trial_models.MODELS[ref],
+                       generate_inputs_fn=trial_models.generate_inputs, backend=None, device="cpu",
+                       input_seed=trial_models.INPUT_SEED, param_seed=trial_models.PARAM_SEED,
+                       tolerance_policy=tol, correctness_policy=pol)
+        trials.append({"name": name, "generated": gen, "reference": ref, "n": n, "tolerance_policy": tol,
+                       "correctness_policy": pol, "expected": out})
+    (HERE / "trial_cases.json").write_text(json.dumps(trials, indent=0, allow_nan=True))
+    print(f"wrote {len(resolve) + len(summaries) + len(finals) + len(perf_results) + len(seeds)} host-logic "
+          f"fixtures, {len(trials)} trial fixtures")
+
+
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    args = [a for a in sys.argv[1:] if not a.startswith("--part")]
+    part = next((a.split("=", 1)[1] for a in sys.argv[1:] if a.startswith("--part=")), "all")
+    root = args[0] if args else "/root/reference"
+    if part in ("all", "verdict"):
+        main(root)
+    if part in ("all", "host"):
+        host_fixtures(root)

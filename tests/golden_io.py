@@ -111,3 +111,23 @@ def diff_meta(a: Dict[str, Any], b: Dict[str, Any]) -> List[str]:
         if k in b and not same_value(a[k], b[k]):
             out.append(f"{k}: {a[k]!r} != {b[k]!r}")
     return out
+
+
+def load_host_logic() -> Dict[str, Any]:
+    """Random-mode configuration and summary, timing payload and perf-seed fixtures."""
+    return json.loads((GOLDEN / "host_logic.json").read_text())
+
+
+def load_finalize_cases() -> List[Dict[str, Any]]:
+    out: List[Dict[str, Any]] = []
+    for p in sorted(GOLDEN.glob("finalize_cases_*.json")):
+        out += json.loads(p.read_text())
+    return out
+
+
+def load_trial_cases() -> List[Dict[str, Any]]:
+    """Reference trial results (GCR:1281-1322 run on the CPU) for the pairs of ``trial_models``."""
+    cases = json.loads((GOLDEN / "trial_cases.json").read_text())
+    for c in cases:
+        c["expected"] = decode_value(c["expected"], {})
+    return cases
