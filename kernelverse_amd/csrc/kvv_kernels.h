@@ -991,10 +991,9 @@ __device__ __forceinline__ void sample_write(const SegDesc& d, typename Elem<DT>
   srel[d.sample_off + i] = rel;
 }
 
-// A wave's buffer of sample values in LDS: abs and rel of the consecutive
-// sample positions [at0, at0 + fill).  It is written out (coalesced) when full,
-// when the positions stop being consecutive (a new segment) and at the end of
-// the wave's range.  Sample values written to HBM while the scan streams its
+// A wave's buffer of samples in LDS: the consecutive sample positions
+// [at0, at0 + fill).  It is written out (coalesced) when full, at the end of a
+// segment and at the end of the wave's range.  Sample values written to HBM while the scan streams its
 // inputs cost far more read bandwidth than their bytes, so a wave whose samples
 // fit (kSampleBuf) writes them all at the end.
 constexpr int kSampleBuf = 384;
@@ -1003,32 +1002,54 @@ struct SampleBuf {
   uint32_t fill;
 };
 
-__device__ __forceinline__ void sbuf_store(SampleBuf& b, KVV_LDS float* ba, KVV_LDS float* br, float* sabs,
-                                           float* srel) {
+// What the buffer keeps per sample position, in two 32-bit words: the raw codes
+// of the pair for element types of at most 4 bytes (abs_diff, rel_diff and the
+// sampled sums are computed when the buffer is written out, every lane busy),
+// else the finished abs_diff and rel_diff.
+template <int DT>
+struct SampleWords {
+  static constexpr bool codes = sizeof(typename Elem<DT>::T) <= 4;
+};
+
+// Writes the buffered positions out (coalesced), finishing their values first
+// when the buffer holds codes.  d is the segment the positions belong to.
+template <int DT, int MODE>
+__device__ __forceinline__ void sbuf_store(const SegDesc& d, SampleBuf& b, KVV_LDS uint32_t* ba, KVV_LDS uint32_t* br,
+                                           float* sabs, float* srel, Acc& acc) {
+  using T = typename Elem<DT>::T;
   if (b.at0 != kNone) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     for (uint32_t k = (uint32_t)lane_id(); k < b.fill; k += 64) {
-      sabs[b.at0 + k] = ba[k];
-      srel[b.at0 + k] = br[k];
+      float adf, rel;
+      if constexpr (SampleWords<DT>::codes) {
+        sample_value<DT, MODE>(d, (T)ba[k], (T)br[k], acc, adf, rel);
+      } else {
+        adf = __uint_as_float(ba[k]);
+        rel = __uint_as_float(br[k]);
+      }
+      sabs[b.at0 + k] = adf;
+      srel[b.at0 + k] = rel;
     }
   }
   b.at0 = kNone;
   b.fill = 0;
 }
 
-// Adds the values of c consecutive sample positions [at, at + c), held by lanes
-// 0..c-1 (c <= 64).
-__device__ __forceinline__ void sbuf_put(SampleBuf& b, uint64_t at, int c, float va, float vr, KVV_LDS float* ba,
-                                         KVV_LDS float* br, float* sabs, float* srel) {
+// Adds c consecutive sample positions [at, at + c), held by lanes 0..c-1
+// (c <= 64), as the two words w0, w1 of each.
+template <int DT, int MODE>
+__device__ __forceinline__ void sbuf_put(const SegDesc& d, SampleBuf& b, uint64_t at, int c, uint32_t w0,
+                                         uint32_t w1, KVV_LDS uint32_t* ba, KVV_LDS uint32_t* br, float* sabs,
+                                         float* srel, Acc& acc) {
   if (b.at0 != kNone && (at != b.at0 + b.fill || b.fill + (uint32_t)c > (uint32_t)kSampleBuf))
-    sbuf_store(b, ba, br, sabs, srel);
+    sbuf_store<DT, MODE>(d, b, ba, br, sabs, srel, acc);
   if (b.at0 == kNone) b.at0 = at;
   const int lane = lane_id();
   if (lane < c) {
-    ba[b.fill + lane] = va;
-    br[b.fill + lane] = vr;
+    ba[b.fill + lane] = w0;
+    br[b.fill + lane] = w1;
   }
   b.fill = uniform(b.fill + (uint32_t)c);
   b.at0 = uniform(b.at0);
@@ -1042,7 +1063,7 @@ __device__ __forceinline__ void sbuf_put(SampleBuf& b, uint64_t at, int c, float
 template <int DT, int MODE>
 __device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_t L1, StageP stage, Acc& acc,
                                             float* sabs, float* srel, SampleCursor& cur, SampleBuf& sb,
-                                            KVV_LDS float* ba, KVV_LDS float* br) {
+                                            KVV_LDS uint32_t* ba, KVV_LDS uint32_t* br) {
   using IO = VecIO<DT>;
   using T = typename IO::T;
   constexpr int V = IO::V;
@@ -1065,15 +1086,23 @@ __device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_
     // the in-range lanes are a prefix; the cursor moves past the last of them
     const int c = (int)__popcll(__ballot(in));
     if (c == 0) return;
-    float adf = 0.0f, rel = 0.0f;
+    uint32_t w0 = 0, w1 = 0;
     if (in) {
       const uint32_t vi = off >> LV;
       const int u = (int)(vi >> 6), tt = (int)(vi & 63u), e = (int)(off & (V - 1));
       const T gc = stage_elem<T>(stage, (2 * u) * 64 + tt, e);
       const T rc = stage_elem<T>(stage, (2 * u + 1) * 64 + tt, e);
-      sample_value<DT, MODE>(d, gc, rc, acc, adf, rel);
+      if constexpr (SampleWords<DT>::codes) {
+        w0 = (uint32_t)gc;
+        w1 = (uint32_t)rc;
+      } else {
+        float adf, rel;
+        sample_value<DT, MODE>(d, gc, rc, acc, adf, rel);
+        w0 = __float_as_uint(adf);
+        w1 = __float_as_uint(rel);
+      }
     }
-    sbuf_put(sb, d.sample_off + cur.i, c, adf, rel, ba, br, sabs, srel);
+    sbuf_put<DT, MODE>(d, sb, d.sample_off + cur.i, c, w0, w1, ba, br, sabs, srel, acc);
     const uint32_t offl = (uint32_t)__builtin_amdgcn_readlane((int)off, c - 1);
     uint32_t nr = (uint32_t)__builtin_amdgcn_readlane((int)rem, c - 1) + smod;
     uint64_t nidx = (uint64_t)L0 + offl + d.s_div;
@@ -1254,14 +1283,14 @@ __device__ inline void fold_block_record(const LdsRecord* rec, const RunCols& ou
 // ------------------------------------------------------------ scan kernel
 // LDS of one scan block: per wave, its item's vectors (SW uint4: kUnroll
 // vectors of each tensor per lane), its queue of stage positions (NQ = 64 lanes
-// x kQSlots), its sample buffer (abs and rel values of kSampleBuf consecutive
+// x kQSlots), its sample buffer (two words for each of kSampleBuf consecutive
 // sample positions) and its counters.  Waves never touch each other's part.
 template <int SW, int NQ>
 struct ScanShared {
   uint32_t done;  // waves of the block that have left their record (single-segment launches)
   uint4 stage[kWaves][SW];
   uint16_t queue[kWaves][NQ];
-  float sbuf[kWaves][2][kSampleBuf];
+  uint32_t sbuf[kWaves][2][kSampleBuf];
   uint32_t wcnt[kWaves][WC_COUNT];
 };
 
@@ -1395,8 +1424,8 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
   SampleBuf sb;
   sb.at0 = kNone;
   sb.fill = 0;
-  KVV_LDS float* ba = (KVV_LDS float*)sm.sbuf[w][0];
-  KVV_LDS float* br = (KVV_LDS float*)sm.sbuf[w][1];
+  KVV_LDS uint32_t* ba = (KVV_LDS uint32_t*)sm.sbuf[w][0];
+  KVV_LDS uint32_t* br = (KVV_LDS uint32_t*)sm.sbuf[w][1];
   SampleCursor cur;
   {
     const SegDesc& d = BATCH ? a.table[s] : a.seg0;
@@ -1407,6 +1436,8 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
       if (it >= a.table[s].item_begin + a.table[s].item_count) {
         const int prev_s = s;
         while (it >= a.table[s].item_begin + a.table[s].item_count) ++s;
+        // the finished segment's buffered samples join its record
+        if constexpr (KIND != K_SCALAR) sbuf_store<DT, MODE>(a.table[prev_s], sb, ba, br, a.sample_abs, a.sample_rel, acc);
         const ColSink out{&a.runs, run_slot(a.table[prev_s], run_start)};
         flush_run(acc, wc, out, (run_start - a.table[prev_s].item_begin) * (int64_t)a.table[prev_s].item_elems);
         run_start = it;
@@ -1458,8 +1489,8 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
     }
     if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, wc, near_prev);
   }
-  if constexpr (KIND != K_SCALAR) sbuf_store(sb, ba, br, a.sample_abs, a.sample_rel);
   const SegDesc& d = BATCH ? a.table[s] : a.seg0;
+  if constexpr (KIND != K_SCALAR) sbuf_store<DT, MODE>(d, sb, ba, br, a.sample_abs, a.sample_rel, acc);
   const int64_t base = (run_start - d.item_begin) * (int64_t)d.item_elems;
   if constexpr (BATCH) {
     const ColSink out{&a.runs, run_slot(d, run_start)};
