@@ -965,17 +965,24 @@ __device__ __forceinline__ void stage_pair(int64_t L0, int64_t idx, StageP stage
   rc = stage_elem<T>(stage, (2 * u + 1) * 64 + t, e);
 }
 
-// abs_diff and rel_diff of one sampled pair; its values join the sampled fp64 sums.
+// abs_diff and rel_diff of one sampled pair.
 template <int DT, int MODE>
-__device__ __forceinline__ void sample_value(const SegDesc& d, typename Elem<DT>::T gc, typename Elem<DT>::T rc,
-                                             Acc& acc, float& adf, float& rel) {
-  using E = Elem<DT>;
+__device__ __forceinline__ void sample_pair(const SegDesc& d, typename Elem<DT>::T gc, typename Elem<DT>::T rc,
+                                            float& adf, float& rel) {
   float rf;
   uint32_t kk;
   bool mm;
   elem_test<DT, MODE>(gc, rc, d, adf, kk, mm, rf);
   // abs_diff == 0 leaves rel_diff == +0 (the denominator is then finite and positive)
   rel = adf == 0.0f ? 0.0f : adf / (fabsf(rf) + 1e-12f);
+}
+
+// abs_diff and rel_diff of one sampled pair; its values join the sampled fp64 sums.
+template <int DT, int MODE>
+__device__ __forceinline__ void sample_value(const SegDesc& d, typename Elem<DT>::T gc, typename Elem<DT>::T rc,
+                                             Acc& acc, float& adf, float& rel) {
+  using E = Elem<DT>;
+  sample_pair<DT, MODE>(d, gc, rc, adf, rel);
   const double g64 = E::f64(gc), r64 = E::f64(rc);
   acc.s[4] = fma(g64, g64, acc.s[4]);
   acc.s[5] = fma(r64, r64, acc.s[5]);
@@ -1053,6 +1060,65 @@ __device__ __forceinline__ void sbuf_put(const SegDesc& d, SampleBuf& b, uint64_
   }
   b.fill = uniform(b.fill + (uint32_t)c);
   b.at0 = uniform(b.at0);
+}
+
+// Code of element e of a 16-byte vector.
+template <int DT>
+__device__ __forceinline__ typename Elem<DT>::T vec_code(const uint4& q, int e) {
+  using T = typename Elem<DT>::T;
+  constexpr int W = Elem<DT>::width;
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  if constexpr (W == 64) {
+    return (T)(((uint64_t)w[2 * e + 1] << 32) | w[2 * e]);
+  } else {
+    return (T)(w[(e * W) >> 5] >> ((e * W) & 31));
+  }
+}
+
+// Samples of a segment whose every element is a sample (n <= max_samples, so
+// sample index == logical index): each lane finishes the values of its own
+// vectors from the stage and stores them with vector stores, no walk.  The
+// sampled sums are then the full sums; the fold takes those.
+template <int DT, int MODE>
+__device__ __forceinline__ void dense_samples(const SegDesc& d, int64_t L0, int64_t L1, StageP stage, float* sabs,
+                                              float* srel) {
+  constexpr int V = VecIO<DT>::V;
+  constexpr int S = V >= 4 ? 4 : V;  // floats per store
+  typedef float fvec __attribute__((ext_vector_type(S)));
+  const int lane = lane_id();
+#pragma unroll 1
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t v0 = L0 + (int64_t)(u * 64 + lane) * V;
+    if (v0 >= L1) break;  // this lane's later vectors lie further out
+    const uint4 gq = stage_vec(stage, (2 * u) * 64 + lane);
+    const uint4 rq = stage_vec(stage, (2 * u + 1) * 64 + lane);
+    float* pa = sabs + d.sample_off + v0;
+    float* pr = srel + d.sample_off + v0;
+    // S values at a time, so few registers are live beside the prefetched item
+#pragma unroll
+    for (int k = 0; k < V; k += S) {
+      fvec xa, xr;
+#pragma unroll
+      for (int j = 0; j < S; ++j) {
+        float fa, fr;
+        sample_pair<DT, MODE>(d, vec_code<DT>(gq, k + j), vec_code<DT>(rq, k + j), fa, fr);
+        xa[j] = fa;
+        xr[j] = fr;
+      }
+      if (v0 + k + S <= L1) {
+        *reinterpret_cast<fvec*>(pa + k) = xa;
+        *reinterpret_cast<fvec*>(pr + k) = xr;
+      } else {
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+          if (v0 + k + j < L1) {
+            pa[k + j] = xa[j];
+            pr[k + j] = xr[j];
+          }
+        }
+      }
+    }
+  }
 }
 
 // Samples of a vector item (GCR:346-347): the wave walks its cursor 64 samples
@@ -1377,7 +1443,7 @@ __device__ inline void block_record_part(const ScanArgs& a, SM& sm, Acc& acc, ui
 }
 
 template <int DT, int MODE, int KIND, bool BATCH>
-__global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
+__global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a) {
   __shared__ typename ScanLds<DT, KIND>::type sm;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   uint32_t* wc = sm.wcnt[w];
@@ -1416,87 +1482,78 @@ __global__ __launch_bounds__(kBlock) void scan_kernel(ScanArgs a) {
     }
     s = lo;
   }
-  int64_t run_start = i0;
-  uint32_t near_prev = 0;
-  uint4 gv[kUnroll], rv[kUnroll];
-  uint32_t full = 0, careful = 0;
-  bool loaded = false;
+  uint32_t careful = 0;
   SampleBuf sb;
   sb.at0 = kNone;
   sb.fill = 0;
   KVV_LDS uint32_t* ba = (KVV_LDS uint32_t*)sm.sbuf[w][0];
   KVV_LDS uint32_t* br = (KVV_LDS uint32_t*)sm.sbuf[w][1];
-  SampleCursor cur;
-  {
+  // one pass per run of items of one segment (a single-segment launch has one);
+  // the prefetched registers are dead between runs, where the record is written
+  for (int64_t it = i0;;) {
     const SegDesc& d = BATCH ? a.table[s] : a.seg0;
-    cur = cursor_at(d, (i0 - d.item_begin) * (int64_t)d.item_elems);
-  }
-  for (int64_t it = i0; it < i1; ++it) {
-    if constexpr (BATCH) {
-      if (it >= a.table[s].item_begin + a.table[s].item_count) {
-        const int prev_s = s;
-        while (it >= a.table[s].item_begin + a.table[s].item_count) ++s;
-        // the finished segment's buffered samples join its record
-        if constexpr (KIND != K_SCALAR) sbuf_store<DT, MODE>(a.table[prev_s], sb, ba, br, a.sample_abs, a.sample_rel, acc);
-        const ColSink out{&a.runs, run_slot(a.table[prev_s], run_start)};
-        flush_run(acc, wc, out, (run_start - a.table[prev_s].item_begin) * (int64_t)a.table[prev_s].item_elems);
-        run_start = it;
-        near_prev = 0;
-        loaded = false;
-        cur = cursor_at(a.table[s], 0);
-      }
-    }
-    const SegDesc& d = BATCH ? a.table[s] : a.seg0;
-    const int64_t L0 = (it - d.item_begin) * (int64_t)d.item_elems;
-    const int64_t L1 = L0 + d.item_elems < d.n ? L0 + d.item_elems : d.n;
+    const int64_t run_start = it;
+    const int64_t seg_end = d.item_begin + d.item_count;
+    const int64_t run_end = i1 < seg_end ? i1 : seg_end;
     const int64_t base = (run_start - d.item_begin) * (int64_t)d.item_elems;  // the run's first element
-    const uint32_t R0 = (uint32_t)(L0 - base);
-    if constexpr (KIND == K_SCALAR) {
-      scan_item_scalar<DT, MODE>(d, L0, L1, base, acc, wc);
-      sample_range<DT, MODE>(d, L0, L1, acc, a.sample_abs, a.sample_rel);
-    } else {
-      if (!loaded) full = load_item<DT, KIND>(d, L0, L1, gv, rv);
-      if (full != (1u << kUnroll) - 1) patch_partial<DT, KIND>(d, L0, L1, full, gv, rv);
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        sm.stage[w][(2 * u) * 64 + lane] = gv[u];
-        sm.stage[w][(2 * u + 1) * 64 + lane] = rv[u];
-      }
-      const uint32_t full_now = full;
-      StageP stage = (StageP)sm.stage[w];
-      // next item of the same segment: its loads fly while this one finishes
-      loaded = false;
-      if (it + 1 < i1 && it + 1 < d.item_begin + d.item_count) {
-        const int64_t N0 = L1;
-        const int64_t N1 = N0 + d.item_elems < d.n ? N0 + d.item_elems : d.n;
-        full = load_item<DT, KIND>(d, N0, N1, gv, rv);
-        loaded = true;
-      }
-      sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, sb, ba, br);
-      const uint64_t slow = phase_a_any<DT>(d, L0, R0, stage, full_now, acc, careful);
-      if (__ballot(slow != 0)) {
-        uint32_t nq = queue_all(slow, sm.queue[w]);
-        // more than the queue holds: kQSlots slots of every lane at a time
-        const bool split = nq > 64u * kQSlots;
-#pragma unroll 1
-        for (int p0 = 0;; p0 += kQSlots) {
-          if (split) nq = queue_part((uint32_t)(slow >> p0), p0, sm.queue[w]);
-          if (nq) phase_b<DT, MODE>(d, R0, nq, stage, sm.queue[w], acc, wc);
-          if (!split || p0 + kQSlots >= VecIO<DT>::NE) break;
-        }
-      }
-      if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, R0, full_now, stage, acc, wc);
+    const bool dense = d.m == d.n;
+    uint32_t near_prev = 0;
+    SampleCursor cur = cursor_at(d, base);
+    uint4 gv[kUnroll], rv[kUnroll];
+    uint32_t full = 0;
+    if constexpr (KIND != K_SCALAR) {
+      const int64_t L1 = base + d.item_elems < d.n ? base + d.item_elems : d.n;
+      full = load_item<DT, KIND>(d, base, L1, gv, rv);
     }
-    if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, wc, near_prev);
-  }
-  const SegDesc& d = BATCH ? a.table[s] : a.seg0;
-  if constexpr (KIND != K_SCALAR) sbuf_store<DT, MODE>(d, sb, ba, br, a.sample_abs, a.sample_rel, acc);
-  const int64_t base = (run_start - d.item_begin) * (int64_t)d.item_elems;
-  if constexpr (BATCH) {
-    const ColSink out{&a.runs, run_slot(d, run_start)};
-    flush_run(acc, wc, out, base);
-  } else {
-    block_record_part(a, sm, acc, wc, w, base);
+    for (; it < run_end; ++it) {
+      const int64_t L0 = (it - d.item_begin) * (int64_t)d.item_elems;
+      const int64_t L1 = L0 + d.item_elems < d.n ? L0 + d.item_elems : d.n;
+      const uint32_t R0 = (uint32_t)(L0 - base);
+      if constexpr (KIND == K_SCALAR) {
+        scan_item_scalar<DT, MODE>(d, L0, L1, base, acc, wc);
+        sample_range<DT, MODE>(d, L0, L1, acc, a.sample_abs, a.sample_rel);
+      } else {
+        if (full != (1u << kUnroll) - 1) patch_partial<DT, KIND>(d, L0, L1, full, gv, rv);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          sm.stage[w][(2 * u) * 64 + lane] = gv[u];
+          sm.stage[w][(2 * u + 1) * 64 + lane] = rv[u];
+        }
+        const uint32_t full_now = full;
+        StageP stage = (StageP)sm.stage[w];
+        // the next item of the run: its loads fly while this one finishes
+        if (it + 1 < run_end) {
+          const int64_t N1 = L1 + d.item_elems < d.n ? L1 + d.item_elems : d.n;
+          full = load_item<DT, KIND>(d, L1, N1, gv, rv);
+        }
+        if (!dense) sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, sb, ba, br);
+        const uint64_t slow = phase_a_any<DT>(d, L0, R0, stage, full_now, acc, careful);
+        if (__ballot(slow != 0)) {
+          uint32_t nq = queue_all(slow, sm.queue[w]);
+          // more than the queue holds: kQSlots slots of every lane at a time
+          const bool split = nq > 64u * kQSlots;
+#pragma unroll 1
+          for (int p0 = 0;; p0 += kQSlots) {
+            if (split) nq = queue_part((uint32_t)(slow >> p0), p0, sm.queue[w]);
+            if (nq) phase_b<DT, MODE>(d, R0, nq, stage, sm.queue[w], acc, wc);
+            if (!split || p0 + kQSlots >= VecIO<DT>::NE) break;
+          }
+        }
+        if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, R0, full_now, stage, acc, wc);
+        if (dense) dense_samples<DT, MODE>(d, L0, L1, stage, a.sample_abs, a.sample_rel);
+      }
+      if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, wc, near_prev);
+    }
+    // the run's buffered samples join its record
+    if constexpr (KIND != K_SCALAR) sbuf_store<DT, MODE>(d, sb, ba, br, a.sample_abs, a.sample_rel, acc);
+    if constexpr (BATCH) {
+      flush_run(acc, wc, ColSink{&a.runs, run_slot(d, run_start)}, base);
+      if (it >= i1) break;
+      while (it >= a.table[s].item_begin + a.table[s].item_count) ++s;
+    } else {
+      block_record_part(a, sm, acc, wc, w, base);
+      break;
+    }
   }
 }
 

@@ -299,11 +299,13 @@ __device__ inline void reduce_sums(const TailArgs& a, const SegDesc& d, int64_t 
   auto sum = [&](int i) { return L.td[i]; };
   kvv_result& o = a.res[d.out_index];
   if (tid == 0) {
-    o.sample_sum_gg = sum(4);
-    o.sample_sum_rr = sum(5);
-    o.sample_sum_gr = sum(6);
-    o.sample_cosine = cosine_of(sum(6), sum(4), sum(5));
-    const double gn = sqrt(sum(4)), rn = sqrt(sum(5));
+    // every element a sample: the sampled sums are the full sums
+    const int k = d.m == d.n ? 0 : 4;
+    o.sample_sum_gg = sum(k);
+    o.sample_sum_rr = sum(k + 1);
+    o.sample_sum_gr = sum(k + 2);
+    o.sample_cosine = cosine_of(sum(k + 2), sum(k), sum(k + 1));
+    const double gn = sqrt(sum(k)), rn = sqrt(sum(k + 1));
     o.sample_norm_ratio = (gn == 0.0 && rn == 0.0) ? 1.0 : (gn == 0.0 ? 0.0 : (rn == 0.0 ? __builtin_inf() : gn / rn));
   } else if (tid == 1) {
     o.sum_gg = sum(0);
