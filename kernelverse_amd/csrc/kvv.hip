@@ -113,6 +113,15 @@ NearFn near_fn(int dt, int mode) {
 }
 
 // Coalesces the joint (size, gen stride, ref stride) dims and picks the layout.
+// Select blocks per array of a group of m samples: one for a small group, one
+// per `rounds` x kSelChunk samples otherwise.
+int64_t select_chunks(int64_t m, int rounds) {
+  if (m == 0) return 0;
+  if (m <= kSmall) return 1;
+  const int64_t per = (int64_t)rounds * kSelChunk;
+  return (m + per - 1) / per;
+}
+
 int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, SegDesc& d) {
   if (!g || !r || !p) return fail(KVV_E_INVALID, "null tensor or policy");
   if (g->dtype != r->dtype) return fail(KVV_E_INVALID, "generated and reference dtypes differ");
@@ -201,8 +210,8 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
     d.vec = 0;
   }
   d.item_count = (n + d.item_elems - 1) / d.item_elems;
-  // select blocks per array: one for a small group, one per kSelChunk samples otherwise
-  d.chunk_count = d.m == 0 ? 0 : (d.m <= kSmall ? 1 : (d.m + kSelChunk - 1) / kSelChunk);
+  d.sel_rounds = 1;
+  d.chunk_count = select_chunks(d.m, 1);
   d.lslot = -1;
   d.s_div = 1;  // n <= max_samples: every element is a sample (stride 1)
   d.s_mod = 0;
@@ -449,6 +458,17 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     segs[i].out_index = i;
     kinds[i] = scan_kind(segs[i]);
     order[i] = i;
+  }
+  // many samples in one launch: fewer, fuller select blocks (each block's fixed
+  // work -- its group's state, its histogram's clear and flush -- is paid once
+  // per kMaxSelRounds rounds)
+  int64_t chunks1 = 0;
+  for (const SegDesc& d : segs) chunks1 += d.chunk_count;
+  const int rounds = chunks1 >= 4 * 8192 ? 4 : (chunks1 >= 2 * 8192 ? 2 : 1);
+  static_assert(kMaxSelRounds >= 4, "select rounds");
+  for (SegDesc& d : segs) {
+    d.sel_rounds = rounds;
+    d.chunk_count = select_chunks(d.m, rounds);
   }
   auto key = [&](int i) { return (segs[i].dtype * 2 + segs[i].mode) * 3 + kinds[i]; };
   std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return key(a) < key(b); });

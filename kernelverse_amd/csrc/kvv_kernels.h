@@ -28,7 +28,8 @@
 namespace kvv {
 
 constexpr int kUnroll = 4;            // 16-byte vectors per thread per item
-constexpr int kSelChunk = 8192;       // sample values per select block of a large group
+constexpr int kSelChunk = 8192;       // sample values per select round of a large group
+constexpr int kMaxSelRounds = 4;      // rounds per select block (many samples in a launch: fewer, fuller blocks)
 constexpr int kSmall = 8192;          // groups of at most this many samples are selected by one block
 constexpr int kArrays = 3;            // abs, rel, near-zero abs
 // Per (large segment, array) slot: level-0 histogram (256), level-1 and level-2
@@ -79,7 +80,7 @@ struct SegDesc {
   int32_t item_elems;
   int32_t out_index;      // position of this pair's kvv_result in the caller's array
   int32_t lslot;          // large-group select slot (m > kSmall), else -1
-  int32_t pad2;
+  int32_t sel_rounds;     // kSelChunk sub-chunks per select block of a large group (1..kMaxSelRounds)
   int64_t run_slot0;      // first run slot of this segment (a multiple of 4)
   int64_t row_len;        // L_ROWS: contiguous inner length
   Dims dims;              // L_ROWS: outer dims; L_GENERIC: all dims

@@ -49,7 +49,8 @@ struct ReduceLds {
 };
 
 // Block histograms hold two 16-bit bin counts per word: a block counts at most
-// max(kSelChunk, kSmall) values, so a count never carries into its neighbour.
+// max(kSelChunk * kMaxSelRounds, kSmall) values, so a count never carries into
+// its neighbour.
 // Sample counts stay below 2^24 (the host caps max_samples), so ranks and
 // histogram sums fit 32 bits.
 struct SelectLds {
@@ -58,7 +59,7 @@ struct SelectLds {
   uint32_t sh[16];
   uint32_t misc[4];
 };
-static_assert(kSelChunk <= 65535 && kSmall <= 65535, "16-bit block bin counts");
+static_assert(kSelChunk * kMaxSelRounds <= 65535 && kSmall <= 65535, "16-bit block bin counts");
 
 union TailLds {
   ReduceLds r;
@@ -619,25 +620,22 @@ __device__ inline void group_state(const uint32_t* slot, const uint64_t rank64[2
 }
 
 // One chunk of a large group at digit level LEVEL: 0 = bits 31..24, 1 = 23..12,
-// 2 = 11..0.
+// 2 = 11..0.  The chunk is d.sel_rounds consecutive rounds of kSelChunk
+// samples, each read with 16-byte loads (thread t takes 4 consecutive values of
+// every 4 * kBlock), histogrammed into one block histogram that is added to the
+// group's once.
 template <int LEVEL>
 __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr, int64_t count, int64_t c,
                                     SelectLds& L) {
-  constexpr int PER = kSelChunk / kBlock;
+  constexpr int PER = kSelChunk / kBlock;  // values per thread and round
+  constexpr int NV = PER / 4;
   constexpr int HS = LEVEL == 2 ? 12 : 24;                     // prefix = key >> HS
   constexpr int DS = LEVEL == 0 ? 24 : (LEVEL == 1 ? 12 : 0);  // digit = (key >> DS) & DM
   constexpr uint32_t DM = LEVEL == 0 ? 255u : 4095u;
   const int tid = threadIdx.x;
-  const int64_t c0 = c * (int64_t)kSelChunk;
-  const int64_t c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
+  const int rounds = d.sel_rounds;
   uint32_t* slot = a.slots + ((size_t)d.lslot * kArrays + arr) * kSlotWords;
   const float* v = a.arr[arr] + d.sample_off;
-  float x[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int64_t idx = c0 + (int64_t)i * kBlock + tid;
-    x[i] = idx < c1 ? v[idx] : 0.0f;
-  }
   uint64_t rank64[2];
   float wgt;
   q99_ranks(count, rank64, wgt);
@@ -649,20 +647,41 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
   __syncthreads();
   uint32_t nans = 0;
   BinRun run0;
+#pragma unroll 1
+  for (int r = 0; r < rounds; ++r) {
+    const int64_t c0 = (c * rounds + r) * (int64_t)kSelChunk;
+    if (c0 >= count) break;
+    const int64_t c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
+    float x[PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int64_t idx = c0 + (int64_t)i * kBlock + tid;
-    const bool isn = __builtin_isnan(x[i]);
-    const bool ok = idx < c1 && !isn;
-    if (LEVEL == 0) nans += (idx < c1 && isn) ? 1u : 0u;
-    const uint32_t key = fkey(x[i]);
-    const uint32_t dig = (key >> DS) & DM;
-    if (LEVEL == 0) {
-      run0.add(L.h[0], dig, ok);
-    } else {
-      const uint32_t top = key >> HS;
-      lds_hist_add(L.h[0], dig, ok && top == pfx[0]);
-      if (!same) lds_hist_add(L.h[1], dig, ok && top == pfx[1]);
+    for (int k = 0; k < NV; ++k) {
+      const int64_t i0 = c0 + (int64_t)k * (4 * kBlock) + 4 * tid;
+      if (i0 + 3 < c1) {
+        const float4 q = *reinterpret_cast<const float4*>(v + i0);
+        x[4 * k] = q.x;
+        x[4 * k + 1] = q.y;
+        x[4 * k + 2] = q.z;
+        x[4 * k + 3] = q.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[4 * k + j] = i0 + j < c1 ? v[i0 + j] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int64_t idx = c0 + (int64_t)(i >> 2) * (4 * kBlock) + 4 * tid + (i & 3);
+      const bool isn = __builtin_isnan(x[i]);
+      const bool ok = idx < c1 && !isn;
+      if (LEVEL == 0) nans += (idx < c1 && isn) ? 1u : 0u;
+      const uint32_t key = fkey(x[i]);
+      const uint32_t dig = (key >> DS) & DM;
+      if (LEVEL == 0) {
+        run0.add(L.h[0], dig, ok);
+      } else {
+        const uint32_t top = key >> HS;
+        lds_hist_add(L.h[0], dig, ok && top == pfx[0]);
+        if (!same) lds_hist_add(L.h[1], dig, ok && top == pfx[1]);
+      }
     }
   }
   if (LEVEL == 0) {
@@ -722,7 +741,7 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
     if (c == 0) select_final(a, d, arr, count, lds.s);
     return;
   }
-  if (c * (int64_t)kSelChunk >= count) return;
+  if (c * d.sel_rounds * (int64_t)kSelChunk >= count) return;
   select_chunk<LEVEL>(a, d, arr, count, c, lds.s);
 }
 #endif  // KVV_COMMON_KERNELS
