@@ -317,7 +317,7 @@ __device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem
   uint64_t pend = __ballot(hv);
   while (pend) {
     const int l0 = __ffsll((long long)pend) - 1;
-    const int kb = __shfl(bk, l0);
+    const int kb = __builtin_amdgcn_readlane(bk, l0);  // l0 is wave-uniform: a register read, no LDS trip
     const uint64_t same = __ballot(hv && bk == kb);
     if (lane_id() == l0) atomicAdd(&wc[LC_HIST0 + kb], (uint32_t)__popcll(same));
     pend &= ~same;
