@@ -773,6 +773,7 @@ struct DotForm {
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float dot2_sq_f16(uint32_t h, float a) {
@@ -837,17 +838,29 @@ __device__ __forceinline__ PhaseA phase_a_dot(const SegDesc& d, StageP stage, ui
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int dd = u * 4 + j;
-      const uint32_t f = CAREFUL ? dword_flags<DT>(gw[j], rw[j]) : ident_flags<DT>(gw[j], rw[j]);
-      if constexpr (W == 8) {
-        if (dd < 8) m0 |= f << dd; else m1 |= f << (dd - 8);
+      if constexpr (W == 16 && !CAREFUL) {
+        // per half: same = sat(1 - (g ^ r)) is 1 for an identical pair, else 0;
+        // g * same keeps the identical codes; m0 collects the identical flags
+        // (inverted into slow flags below)
+        const u16x2 same = __builtin_elementwise_sub_sat(u16x2{1, 1}, __builtin_bit_cast(u16x2, gw[j] ^ rw[j]));
+        const uint32_t z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, gw[j]) * same);
+        m0 |= __builtin_bit_cast(uint32_t, same) << dd;
+        if constexpr (DT == KVV_BF16) orz |= z;
+        dot_sq<DT>(z, a, j);
       } else {
-        m0 |= f << dd;
+        const uint32_t f = CAREFUL ? dword_flags<DT>(gw[j], rw[j]) : ident_flags<DT>(gw[j], rw[j]);
+        if constexpr (W == 8) {
+          if (dd < 8) m0 |= f << dd; else m1 |= f << (dd - 8);
+        } else {
+          m0 |= f << dd;
+        }
+        const uint32_t z = gw[j] & ~flag_mask<W>(f);
+        if constexpr (DT == KVV_BF16) orz |= z;
+        dot_sq<DT>(z, a, j);
       }
-      const uint32_t z = gw[j] & ~flag_mask<W>(f);
-      if constexpr (DT == KVV_BF16) orz |= z;
-      dot_sq<DT>(z, a, j);
     }
   }
+  if constexpr (W == 16 && !CAREFUL) m0 = ~m0;  // identical flags -> slow flags (every vector is full)
   bool redo = false;
   if constexpr (!DF::is_int && DT != KVV_F8E4M3FN) {
     float t = 0.0f;
