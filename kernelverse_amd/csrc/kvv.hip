@@ -383,6 +383,37 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
 }
 
 // ------------------------------------------------------------ one verdict
+// Relative item rates of the three dispatch rounds of a scan grid that holds
+// three blocks per CU (oldest round first).  The grid is dispatched one block
+// per CU at a time and the waves of earlier rounds are served faster: with
+// equal shares on MI355X the bf16 main pass's first-round blocks finished in
+// 143 us, the second round's in 164 us and the third round's in 191 us (the
+// kernel ends with the slowest).  Shares in proportion to the rates, refined
+// once from the per-round end times they gave, let the rounds finish together.
+constexpr double kRoundRate3[3] = {1.18, 1.0, 0.79};
+
+// Splits a single-segment grid's items over its dispatch rounds (a.rounds = 1:
+// one share for every wave).
+void plan_rounds(ScanArgs& a, ScanFn scan, int64_t grid) {
+  a.rounds = 1;
+  const int64_t cus = device_cus();
+  if (cus <= 0 || blocks_target(scan) != 3 * cus || grid <= 2 * cus) return;
+  const int64_t nb[3] = {cus, cus, grid - 2 * cus};
+  double wsum = 0.0;
+  for (int r = 0; r < 3; ++r) wsum += kRoundRate3[r] * (double)nb[r];
+  int64_t first = 0;
+  for (int r = 0; r < 3; ++r) {
+    const int64_t n = r < 2 ? (int64_t)((double)a.items * kRoundRate3[r] * (double)nb[r] / wsum) : a.items - first;
+    const int64_t waves = nb[r] * kWaves;
+    a.round_first[r] = first;
+    a.round_ipw[r] = n > 0 ? (n + waves - 1) / waves : 0;
+    first += n;
+  }
+  a.round_first[3] = a.items;
+  a.rounds = 3;
+  a.round_blocks = (int32_t)cus;
+}
+
 int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st,
                hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr) {
   SegDesc d = d0;
@@ -424,6 +455,10 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     a.zero_n4 = (int64_t)(L.slot_bytes / 16);
     const int64_t per_block = a.items_per_wave * kWaves;
     const int64_t grid = (d.item_count + per_block - 1) / per_block;
+    plan_rounds(a, scan, grid);
+    for (int r = 0; r < a.rounds; ++r)
+      if ((uint64_t)a.round_ipw[r] * kWaves * (uint64_t)d.item_elems >= (1ull << 32))
+        return fail(KVV_E_UNSUPPORTED, "tensor too large for 32-bit per-block counts");
     if (ev_begin) KVV_HIP(hipEventRecord(ev_begin, st));
     hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
     KVV_HIP(hipGetLastError());

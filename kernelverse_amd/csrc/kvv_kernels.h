@@ -30,6 +30,7 @@ namespace kvv {
 constexpr int kUnroll = 4;            // 16-byte vectors per thread per item
 constexpr int kSelChunk = 8192;       // sample values per select round of a large group
 constexpr int kMaxSelRounds = 4;      // rounds per select block (many samples in a launch: fewer, fuller blocks)
+constexpr int kMaxRounds = 4;         // dispatch rounds of a single-segment scan grid (blocks per CU)
 constexpr int kSmall = 8192;          // groups of at most this many samples are selected by one block
 constexpr int kArrays = 3;            // abs, rel, near-zero abs
 // Per (large segment, array) slot: level-0 histogram (256), level-1 and level-2
@@ -106,6 +107,13 @@ struct ScanArgs {
   int64_t item_lo;         // items of this launch: [item_lo, item_lo + items)
   int64_t items;
   int64_t items_per_wave;  // each wave of the grid owns this many consecutive items
+  // single-segment launches filling the device in `rounds` dispatch rounds of
+  // `round_blocks` blocks (rounds > 1): round r's waves own round_ipw[r] items
+  // each, from round_first[r] on (round_first[rounds] == items)
+  int32_t rounds;
+  int32_t round_blocks;
+  int64_t round_first[kMaxRounds + 1];
+  int64_t round_ipw[kMaxRounds];
   RunCols runs;            // one slot per run (see run_slot)
   float* sample_abs;
   float* sample_rel;
@@ -1476,9 +1484,24 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
   }
   // each wave owns a contiguous range of items; the waves of a block never wait
   // for each other
-  const int64_t i0 = a.item_lo + ((int64_t)blockIdx.x * kWaves + w) * a.items_per_wave;
-  int64_t i1 = i0 + a.items_per_wave;
-  if (i1 > a.item_lo + a.items) i1 = a.item_lo + a.items;
+  int64_t i0, i1;
+  if (!BATCH && a.rounds > 1) {
+    // the grid is dispatched one block per CU at a time, and earlier rounds'
+    // waves are served faster: each round's waves get a share of the items in
+    // proportion to its rate
+    int r = (int)(blockIdx.x / (uint32_t)a.round_blocks);
+    r = r < a.rounds - 1 ? r : a.rounds - 1;
+    const int64_t q = ((int64_t)blockIdx.x - (int64_t)r * a.round_blocks) * kWaves + w;
+    i0 = a.item_lo + a.round_first[r] + q * a.round_ipw[r];
+    i1 = i0 + a.round_ipw[r];
+    const int64_t r1 = a.item_lo + a.round_first[r + 1];
+    if (i0 > r1) i0 = r1;
+    if (i1 > r1) i1 = r1;
+  } else {
+    i0 = a.item_lo + ((int64_t)blockIdx.x * kWaves + w) * a.items_per_wave;
+    i1 = i0 + a.items_per_wave;
+    if (i1 > a.item_lo + a.items) i1 = a.item_lo + a.items;
+  }
   Acc acc;
   acc.init();
   if (i0 >= i1) {
