@@ -316,7 +316,7 @@ struct NearLaunch {
 // level; then select levels 1 and 2 and the final read-off of every array.
 int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchunk, int nseg, int64_t total_chunks,
                 int64_t nslots, bool near, const WsLayout& L, void* ws, kvv_result* out, hipStream_t st,
-                const std::vector<NearLaunch>& nears) {
+                const std::vector<NearLaunch>& nears, bool stream_groups = false) {
   TailArgs t{};
   if (seg0) t.seg0 = *seg0;
   t.table = dtable;
@@ -344,12 +344,17 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
     if (level == 0) hipLaunchKernelGGL(tail_kernel<0>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
     else if (level == 1) hipLaunchKernelGGL(tail_kernel<1>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
     else if (level == 2) hipLaunchKernelGGL(tail_kernel<2>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
-    else hipLaunchKernelGGL(tail_kernel<3>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
+    else if (level == 3) hipLaunchKernelGGL(tail_kernel<3>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
+    else hipLaunchKernelGGL(tail_kernel<4>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
     KVV_HIP(hipGetLastError());
     return KVV_OK;
   };
   int rc = launch(nseg * t.reduce_roles, 0, 0, 2);
   if (rc) return rc;
+  if (stream_groups) {
+    rc = launch(0, 4, 0, 2);
+    if (rc) return rc;
+  }
   if (near) {
     for (const auto& nl : nears) {
       if (nl.items == 0) continue;
@@ -369,6 +374,10 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
     }
     rc = launch(0, 0, 2, 1);
     if (rc) return rc;
+    if (stream_groups) {
+      rc = launch(0, 4, 2, 1);
+      if (rc) return rc;
+    }
   }
   if (nslots > 0) {
     const int narr = near ? 3 : 2;
@@ -478,6 +487,7 @@ struct BatchPlan {
     int64_t item_lo, items, ipb;
   };
   std::vector<Group> groups;
+  bool stream_groups = false;  // large groups selected one block each (tail level 4)
   int64_t items = 0, samples = 0, chunks = 0, nslots = 0, run_slots = 0;
   bool near = false;
 };
@@ -497,13 +507,23 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   // many samples in one launch: fewer, fuller select blocks (each block's fixed
   // work -- its group's state, its histogram's clear and flush -- is paid once
   // per kMaxSelRounds rounds)
-  int64_t chunks1 = 0;
-  for (const SegDesc& d : segs) chunks1 += d.chunk_count;
+  int64_t chunks1 = 0, large = 0, max_m = 0;
+  for (const SegDesc& d : segs) {
+    chunks1 += d.chunk_count;
+    if (d.m > kSmall) {
+      ++large;
+      max_m = d.m > max_m ? d.m : max_m;
+    }
+  }
+  // enough large groups to fill the device by themselves: each is selected by
+  // one block in the first tail launch (no global histograms, no level launches)
+  const bool group_mode = large >= (int64_t)device_cus() && max_m <= kGroupStreamMax;
+  bp.stream_groups = group_mode;
   const int rounds = chunks1 >= 4 * 8192 ? 4 : (chunks1 >= 2 * 8192 ? 2 : 1);
   static_assert(kMaxSelRounds >= 4, "select rounds");
   for (SegDesc& d : segs) {
-    d.sel_rounds = rounds;
-    d.chunk_count = select_chunks(d.m, rounds);
+    d.sel_rounds = group_mode ? 1 : rounds;
+    d.chunk_count = group_mode ? (d.m > 0 ? 1 : 0) : select_chunks(d.m, rounds);
   }
   auto key = [&](int i) { return (segs[i].dtype * 2 + segs[i].mode) * 3 + kinds[i]; };
   std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return key(a) < key(b); });
@@ -514,7 +534,7 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     d.item_begin = item;
     d.sample_off = sample;
     d.chunk_begin = chunk;
-    d.lslot = d.m > kSmall ? (int32_t)bp.nslots++ : -1;
+    d.lslot = !group_mode && d.m > kSmall ? (int32_t)bp.nslots++ : -1;
     d.run_slot0 = bp.run_slots;
     bp.run_slots += run_slot_bound(d.item_count);
     const int s = (int)bp.table.size();
@@ -545,6 +565,18 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   bp.items = item;
   bp.samples = sample;
   bp.chunks = chunk;
+  if (bp.stream_groups) {
+    // one select block per group: the largest groups first, so the longest
+    // blocks start early and the small ones fill in behind them
+    std::vector<int> by_size;
+    for (int s = 0; s < (int)bp.table.size(); ++s)
+      if (bp.table[s].chunk_count > 0) by_size.push_back(s);
+    std::stable_sort(by_size.begin(), by_size.end(), [&](int x, int y) { return bp.table[x].m > bp.table[y].m; });
+    for (size_t k = 0; k < by_size.size(); ++k) {
+      bp.table[by_size[k]].chunk_begin = (int64_t)k;
+      bp.chunk_seg[k] = by_size[k];
+    }
+  }
   return KVV_OK;
 }
 
@@ -586,7 +618,8 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
     KVV_HIP(hipGetLastError());
   }
-  return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, bp.near, L, ws, out, st, nears);
+  return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, bp.near, L, ws, out, st, nears,
+                     bp.stream_groups);
 }
 
 }  // namespace

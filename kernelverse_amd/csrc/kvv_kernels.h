@@ -32,6 +32,7 @@ constexpr int kSelChunk = 8192;       // sample values per select round of a lar
 constexpr int kMaxSelRounds = 4;      // rounds per select block (many samples in a launch: fewer, fuller blocks)
 constexpr int kMaxRounds = 4;         // dispatch rounds of a single-segment scan grid (blocks per CU)
 constexpr int kSmall = 8192;          // groups of at most this many samples are selected by one block
+constexpr int64_t kGroupStreamMax = 1 << 22;  // largest group one block streams in a many-group launch
 constexpr int kArrays = 3;            // abs, rel, near-zero abs
 // Per (large segment, array) slot: level-0 histogram (256), level-1 and level-2
 // histograms (2 ranks x 4096 each) and the NaN count.

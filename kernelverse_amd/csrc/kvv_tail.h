@@ -569,6 +569,127 @@ __device__ inline void select_small(const TailArgs& a, const SegDesc& d, int arr
   finalize_group(a, d, arr, count, key, wgt, has_nan, L);
 }
 
+// BinRun with full 32-bit counts (a histogram of one bin per word).
+struct BinRun32 {
+  uint32_t bin = 0, cnt = 0;
+  __device__ __forceinline__ void add(uint32_t* h, uint32_t b, bool act) {
+    const bool change = act && b != bin;
+    if (change && cnt) atomicAdd(&h[bin], cnt);
+    bin = change ? b : bin;
+    cnt = change ? 1u : cnt + (act ? 1u : 0u);
+  }
+  __device__ __forceinline__ void flush(uint32_t* h) {
+    if (cnt) atomicAdd(&h[bin], cnt);
+  }
+};
+
+// One digit pass of select_group_stream over the whole group: digit
+// (key >> SH) & (2^W - 1) of the values whose bits above SH + W equal the
+// rank's prefix (every value at the first pass), counted in 32-bit LDS bins.
+template <int SH, int W, bool FIRST>
+__device__ inline uint32_t group_pass(const float* v, int64_t count, const uint32_t pfx[2], bool same, SelectLds& L) {
+  constexpr int PER = kSelChunk / kBlock;
+  constexpr uint32_t DM = (1u << W) - 1u;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < 2 * 2048; i += kBlock) (&L.h[0][0])[i] = 0;
+  __syncthreads();
+  uint32_t nans = 0;
+  BinRun32 ra, rb;
+  // thread t takes 4 consecutive values of every 4 * kBlock, read with 16-byte loads
+  auto load = [&](float (&x)[PER], int64_t c0) {
+#pragma unroll
+    for (int k = 0; k < PER / 4; ++k) {
+      const int64_t i0 = c0 + (int64_t)k * (4 * kBlock) + 4 * tid;
+      if (i0 + 3 < count) {
+        const float4 q = *reinterpret_cast<const float4*>(v + i0);
+        x[4 * k] = q.x;
+        x[4 * k + 1] = q.y;
+        x[4 * k + 2] = q.z;
+        x[4 * k + 3] = q.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[4 * k + j] = i0 + j < count ? v[i0 + j] : 0.0f;
+      }
+    }
+  };
+  auto count_in = [&](const float (&x)[PER], int64_t c0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int64_t idx = c0 + (int64_t)(i >> 2) * (4 * kBlock) + 4 * tid + (i & 3);
+      const bool isn = __builtin_isnan(x[i]);
+      const bool ok = idx < count && !isn;
+      const uint32_t key = fkey(x[i]);
+      const uint32_t dig = (key >> SH) & DM;
+      if (FIRST) {
+        nans += (idx < count && isn) ? 1u : 0u;
+        ra.add(L.h[0], dig, ok);
+      } else {
+        const uint32_t top = key >> (SH + W);
+        ra.add(L.h[0], dig, ok && top == pfx[0]);
+        if (!same) rb.add(L.h[1], dig, ok && top == pfx[1]);
+      }
+    }
+  };
+  // one buffer: a second one in flight would double the registers (2 blocks per
+  // CU instead of 5), and more resident blocks hide the load latency better
+  float xa[PER];
+#pragma unroll 1
+  for (int64_t c0 = 0; c0 < count; c0 += kSelChunk) {
+    load(xa, c0);
+    count_in(xa, c0);
+  }
+  ra.flush(L.h[0]);
+  if (!FIRST && !same) rb.flush(L.h[1]);
+  __syncthreads();
+  return nans;
+}
+
+// Folds one pass's histograms into the ranks' prefixes and residual ranks.
+template <int W>
+__device__ inline void group_pass_ranks(bool same, uint32_t key[2], uint32_t resid[2], SelectLds& L) {
+  constexpr int PER = (1 << W) / kBlock;
+  const int tid = threadIdx.x;
+  uint32_t cA[PER], cB[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    cA[i] = L.h[0][tid * PER + i];
+    cB[i] = L.h[1][tid * PER + i];
+  }
+  uint32_t bin[2], below[2];
+  block_find2<PER>(cA, cB, same, resid, bin, below, L.sh);
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    key[rr] = (key[rr] << W) | bin[rr];
+    resid[rr] -= below[rr];
+  }
+  __syncthreads();
+}
+
+// A whole large group selected by one block, streaming its samples once per
+// digit (bits 31..21, 20..10, 9..0).  Used when a launch holds enough groups to
+// fill the device by itself: no global histograms, no further launches.
+__device__ inline void select_group_stream(const TailArgs& a, const SegDesc& d, int arr, int64_t count,
+                                           SelectLds& L) {
+  const float* v = a.arr[arr] + d.sample_off;
+  uint64_t rank64[2];
+  float wgt;
+  q99_ranks(count, rank64, wgt);
+  uint32_t key[2] = {0u, 0u}, resid[2] = {(uint32_t)rank64[0], (uint32_t)rank64[1]};
+  const uint32_t none[2] = {0u, 0u};
+  const uint32_t nans = group_pass<21, 11, true>(v, count, none, true, L);
+  const bool has_nan = block_sum_nan(nans, L) != 0;
+  if (!has_nan) {
+    group_pass_ranks<11>(true, key, resid, L);
+    bool same = key[0] == key[1];
+    group_pass<10, 11, false>(v, count, key, same, L);
+    group_pass_ranks<11>(same, key, resid, L);
+    same = key[0] == key[1];
+    group_pass<0, 10, false>(v, count, key, same, L);
+    group_pass_ranks<10>(same, key, resid, L);
+  }
+  finalize_group(a, d, arr, count, key, wgt, has_nan, L);
+}
+
 // Prefixes and residual ranks of the two order statistics of a large group
 // after the digit levels below LEVEL, from the group's global histograms.  All
 // histogram words the block needs are loaded in one go.
@@ -716,7 +837,8 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
 }
 
 #ifdef KVV_COMMON_KERNELS
-// Level 0 also folds run records (leading blocks) and selects small groups.
+// Level 0 also folds run records (leading blocks) and selects small groups;
+// "level" 4 selects the large groups of a many-group launch (select_group_stream).
 template <int LEVEL>
 __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
   __shared__ TailLds lds;
@@ -733,8 +855,13 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
   const int64_t count = group_count(d, a.res[d.out_index], arr);
   const int64_t c = chunk - d.chunk_begin;
   if (count <= 0) return;
+  if (LEVEL == 4) {
+    // many-group launches: a large group without global histograms, one block
+    if (count > kSmall && d.lslot < 0 && c == 0) select_group_stream(a, d, arr, count, lds.s);
+    return;
+  }
   if (count <= kSmall || d.lslot < 0) {
-    if (LEVEL == 0 && c == 0) select_small(a, d, arr, count, lds.s);
+    if (LEVEL == 0 && c == 0 && count <= kSmall) select_small(a, d, arr, count, lds.s);
     return;
   }
   if (LEVEL == 3) {

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from golden_io import load_cases
+from golden_io import load_cases, same_value
 from parity_util import meta_problems, record_vs_oracle
 from oracle import torch_verdict as tv
 
@@ -235,6 +235,56 @@ def test_batch_matches_single_and_oracle(kv):
     assert got[0] == want[0] and got[1] == want[1]
     for a, b in zip(got[2], want[2]):
         assert not meta_problems(a, b)
+
+
+def test_many_group_batch_selects_each_group_in_one_block(kv):
+    """A batch with more large groups (more than 8192 samples) than the device has
+    CUs takes the one-block-per-group select: p99 of every pair against the
+    oracle, with NaN, negative, tied and tolerant-policy members."""
+    from kernelverse_amd import synth
+    sizes = synth.ragged_sizes(300, seed=21, lo=8_200, hi=40_000)
+    pairs = []
+    for i, n in enumerate(sizes):
+        g, r = synth.fp32_noise_pair(n, seed=100 + i)
+        if i % 7 == 0:
+            g[::97] = float("nan")
+        if i % 11 == 0:
+            g, r = -g.abs(), -r.abs()
+        if i % 13 == 0:
+            g = r.clone()
+            g[: n // 3] += 1e-3  # many identical abs_diff values: ties at the order statistics
+        pairs.append((g, r))
+    bf = [synth.code_flip_pair(30_000 + 17 * i, seed=400 + i) for i in range(12)]
+    pairs += [(g, r) for g, r in bf]
+    tol = {"FP32": {"rtol": 1e-5, "atol": 1e-5}, "BF16": {"rtol": 1.6e-2, "atol": 1e-2}}
+    _say("many-group batch", len(pairs))
+    recs = kv.verdict_records([(g.to(DEV), r.to(DEV)) for g, r in pairs], tolerance_policy=tol)
+    for (g, r), rec in zip(pairs, recs):
+        probs = record_vs_oracle(rec, g, r, tol)
+        abs_d, rel_d, _, _ = tv.mismatch_parts(g, r, tol)  # every element is a sample here
+        for k, vals in (("p99_abs", abs_d), ("p99_rel", rel_d)):
+            want = tv.p99_meta(vals)
+            if not same_value(float(rec[k]), float(want)):
+                probs.append(f"{k}: device {rec[k]!r} != oracle {want!r}")
+        # the full sums serve as the sampled sums here: unrounded they agree to 1e-6, so
+        # after round(., 4) they match or sit one step apart at a rounding boundary
+        want_cos = tv.cosine_similarity_meta(g, r)
+        got_cos = round(rec["sample_cosine"], 4)
+        if want_cos is not None and not same_value(got_cos, want_cos) and not abs(got_cos - want_cos) <= 1e-4 + 1e-12:
+            probs.append(f"sample_cosine: device {rec['sample_cosine']!r} vs oracle {want_cos!r}")
+        assert not probs, (tuple(g.shape), g.dtype, probs)
+    # the tolerant policy adds the near-zero sample array to every group
+    pol = {"name": "tolerant", **__import__("kernelverse_amd.correctness_policy", fromlist=["x"]).resolve_correctness_policy(
+        {"category": "activation", "op_name": "gelu", "config": {"policy": "tolerant"}})}
+    half = [(g.to(torch.bfloat16), r.to(torch.bfloat16)) for g, r in pairs[:280]]
+    got = kv._compare_outputs(tuple(p[0].to(DEV) for p in half), tuple(p[1].to(DEV) for p in half),
+                              tolerance_policy=tol, correctness_policy=pol)
+    want = tv.compare_outputs(tuple(p[0] for p in half), tuple(p[1] for p in half), tolerance_policy=tol,
+                              correctness_policy=pol)
+    assert got[0] == want[0] and got[1] == want[1]
+    for a, b in zip(got[2], want[2]):
+        probs = meta_problems(a, b)
+        assert not probs, probs
 
 
 def test_repeat_is_bit_identical(kv):
