@@ -392,6 +392,24 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
 }
 
 // ------------------------------------------------------------ one verdict
+// A single pair too small to give every wave of the grid two full items takes
+// smaller items (down to one 16-byte vector per lane): more waves then share
+// its work, which for all-slow data is latency, not bandwidth.  The kernels
+// treat the vectors past an item's end as absent.
+int plan_single(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, SegDesc& d) {
+  int rc = plan_segment(g, r, p, d);
+  if (rc) return rc;
+  if (scan_kind(d) == K_CONTIG) {
+    const int64_t min_elems = d.item_elems / kUnroll;
+    const int64_t want = 2 * 12 * (int64_t)device_cus();  // two items per wave of a full grid
+    while (d.item_elems > min_elems && d.item_count < want) {
+      d.item_elems /= 2;
+      d.item_count = (d.n + d.item_elems - 1) / d.item_elems;
+    }
+  }
+  return KVV_OK;
+}
+
 // Relative item rates of the three dispatch rounds of a scan grid that holds
 // three blocks per CU (oldest round first).  The grid is dispatched one block
 // per CU at a time and the waves of earlier rounds are served faster: with
@@ -635,7 +653,7 @@ const char* kvv_last_error(void) { return kvv::g_err.c_str(); }
 int kvv_workspace_size(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy, size_t* bytes) {
   if (!bytes) return kvv::fail(KVV_E_INVALID, "null bytes pointer");
   kvv::SegDesc d;
-  int rc = kvv::plan_segment(gen, ref, policy, d);
+  int rc = kvv::plan_single(gen, ref, policy, d);
   if (rc) return rc;
   *bytes =
       kvv::workspace_layout(kvv::run_slot_bound(d.item_count), d.m, 1, d.m > kvv::kSmall ? 1 : 0, d.chunk_count,
@@ -647,7 +665,7 @@ int kvv_workspace_size(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_p
 int kvv_verdict(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy, kvv_result* out,
                 void* workspace, size_t workspace_bytes, void* stream) {
   kvv::SegDesc d;
-  int rc = kvv::plan_segment(gen, ref, policy, d);
+  int rc = kvv::plan_single(gen, ref, policy, d);
   if (rc) return rc;
   return kvv::run_single(d, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
@@ -655,7 +673,7 @@ int kvv_verdict(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* 
 int kvv_verdict_timed(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy, kvv_result* out,
                       void* workspace, size_t workspace_bytes, void* stream, void* main_begin, void* main_end) {
   kvv::SegDesc d;
-  int rc = kvv::plan_segment(gen, ref, policy, d);
+  int rc = kvv::plan_single(gen, ref, policy, d);
   if (rc) return rc;
   return kvv::run_single(d, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
                          static_cast<hipEvent_t>(main_begin), static_cast<hipEvent_t>(main_end));
