@@ -320,16 +320,21 @@ __device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem
       wave_add(wc, LC_NANPAIR, act && nan_pair);
     }
   }
-  // ULP histogram: one ds_add per distinct bucket present in the wave
+  // ULP histogram: one aggregated add when the wave's elements share a bucket
+  // (e.g. 1-ULP steps), else every lane adds its own in one LDS atomic
+  // instruction (a loop over the distinct buckets would serialise the wave)
   const bool hv = act && !nan_pair;
   const int bk = pair_bucket<DT>(gc, rc);
-  uint64_t pend = __ballot(hv);
-  while (pend) {
-    const int l0 = __ffsll((long long)pend) - 1;
+  const uint64_t hb = __ballot(hv);
+  if (hb) {
+    const int l0 = __ffsll((long long)hb) - 1;
     const int kb = __builtin_amdgcn_readlane(bk, l0);  // l0 is wave-uniform: a register read, no LDS trip
     const uint64_t same = __ballot(hv && bk == kb);
-    if (lane_id() == l0) atomicAdd(&wc[LC_HIST0 + kb], (uint32_t)__popcll(same));
-    pend &= ~same;
+    if (same == hb) {
+      if (lane_id() == l0) atomicAdd(&wc[LC_HIST0 + kb], (uint32_t)__popcll(same));
+    } else if (hv) {
+      atomicAdd(&wc[LC_HIST0 + bk], 1u);
+    }
   }
   if (act) {
     const double g64 = E::f64(gc), r64 = E::f64(rc);
