@@ -979,20 +979,6 @@ __device__ __forceinline__ SampleCursor cursor_at(const SegDesc& d, int64_t L0) 
   return c;
 }
 
-// The pair at logical index idx (L0 <= idx < L1) of a vector item, from the
-// stage (load_item filled a partial last vector element by element).
-template <int DT>
-__device__ __forceinline__ void stage_pair(int64_t L0, int64_t idx, StageP stage, typename Elem<DT>::T& gc,
-                                           typename Elem<DT>::T& rc) {
-  using T = typename Elem<DT>::T;
-  constexpr int V = VecIO<DT>::V;
-  const int q = (int)(idx - L0);
-  const int vec = q / V;
-  const int u = vec >> 6, t = vec & 63, e = q % V;
-  gc = stage_elem<T>(stage, (2 * u) * 64 + t, e);
-  rc = stage_elem<T>(stage, (2 * u + 1) * 64 + t, e);
-}
-
 // abs_diff and rel_diff of one sampled pair.
 template <int DT, int MODE>
 __device__ __forceinline__ void sample_pair(const SegDesc& d, typename Elem<DT>::T gc, typename Elem<DT>::T rc,
@@ -1015,15 +1001,6 @@ __device__ __forceinline__ void sample_value(const SegDesc& d, typename Elem<DT>
   acc.s[4] = fma(g64, g64, acc.s[4]);
   acc.s[5] = fma(r64, r64, acc.s[5]);
   acc.s[6] = fma(g64, r64, acc.s[6]);
-}
-
-template <int DT, int MODE>
-__device__ __forceinline__ void sample_write(const SegDesc& d, typename Elem<DT>::T gc, typename Elem<DT>::T rc,
-                                             uint64_t i, Acc& acc, float* sabs, float* srel) {
-  float adf, rel;
-  sample_value<DT, MODE>(d, gc, rc, acc, adf, rel);
-  sabs[d.sample_off + i] = adf;
-  srel[d.sample_off + i] = rel;
 }
 
 // A wave's buffer of samples in LDS: the consecutive sample positions

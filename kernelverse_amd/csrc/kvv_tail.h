@@ -17,6 +17,11 @@
 // level's blocks locate the ranks in it.  A fourth launch (one block per large
 // group) reads the full keys off the three histograms, interpolates like
 // torch.quantile and writes the result.  The main pass cleared the histograms.
+//
+// A launch with at least as many large groups as the device has CUs (a big
+// batch) selects each of them with one block instead ("level" 4,
+// select_group_stream): the block streams its group once per digit, so no
+// global histograms or level launches are needed.
 
 struct TailArgs {
   SegDesc seg0;               // the segment when table == nullptr
