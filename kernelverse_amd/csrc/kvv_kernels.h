@@ -637,7 +637,13 @@ __device__ __forceinline__ uint32_t dword_flags(uint32_t g, uint32_t r) {
 // Zero mask of a dword from its flags: all ones over each flagged element.
 template <int W>
 __device__ __forceinline__ uint32_t flag_mask(uint32_t f) {
-  if constexpr (W == 8) return (f << 8) - f;
+  // 8-bit: 0x80 | 0x7F per flagged byte, from full-rate ops ((f << 8) - f would
+  // become a quarter-rate 32-bit multiply by 255)
+  if constexpr (W == 8) {
+    uint32_t h = f << 7;
+    asm("" : "+v"(h));  // keeps the compiler from folding h | (h - f) back into f * 255
+    return h | (h - f);
+  }
   else if constexpr (W == 16) return __umul24(f, 0xFFFFu);
   else return 0u - f;
 }
