@@ -102,6 +102,16 @@ ScanFn scan_fn(int dt, int mode, int kind, bool batch) {
   }
 }
 
+IselFn isel_fn(int dt, bool gather) {
+  switch (dt) {
+#define KVV_CASE(X) case X: return KVV_ISEL_FN(X)(gather);
+    KVV_CASE(0) KVV_CASE(1) KVV_CASE(2) KVV_CASE(3) KVV_CASE(4) KVV_CASE(5)
+    KVV_CASE(6) KVV_CASE(7) KVV_CASE(8) KVV_CASE(9) KVV_CASE(10) KVV_CASE(11)
+#undef KVV_CASE
+    default: return nullptr;
+  }
+}
+
 NearFn near_fn(int dt, int mode) {
   switch (dt) {
 #define KVV_CASE(X) case X: return KVV_NEAR_FN(X)(mode);
@@ -151,7 +161,7 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
   d.max_samples = p->max_samples;
   d.m = n < p->max_samples ? n : p->max_samples;
   d.mode = p->mode;
-  d.flags = p->flags;
+  d.flags = p->flags & KVV_FLAG_NEAR_ZERO;
   d.rtol = (float)p->rtol;
   d.atol = (float)p->atol;
   d.zero_tol = (p->rtol == 0.0 && p->atol == 0.0) ? 1 : 0;
@@ -213,6 +223,7 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
   d.sel_rounds = 1;
   d.chunk_count = select_chunks(d.m, 1);
   d.lslot = -1;
+  d.isel_slot = -1;
   d.s_div = 1;  // n <= max_samples: every element is a sample (stride 1)
   d.s_mod = 0;
   d.s_magic = 0;
@@ -242,7 +253,7 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
 struct WsLayout {
   int64_t run_stride;
   size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample, table,
-      chunk_seg, total;
+      chunk_seg, isel_state, isel_seg, isel_chunk, isel_sums, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -256,7 +267,7 @@ int64_t run_slot_bound(int64_t item_count) {
 }
 
 WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int64_t nslots, int64_t chunks,
-                          int64_t items, bool near, bool batch) {
+                          int64_t items, bool near, bool batch, int64_t nisel = 0, int64_t isel_chunks = 0) {
   WsLayout L{};
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -269,8 +280,11 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
   L.runs_u64 = take((size_t)run_slots * kColU64 * 8);
   L.sample_abs = take((size_t)samples * 4);
   L.sample_rel = take((size_t)samples * 4);
-  L.slot_bytes = (size_t)nslots * kArrays * kSlotWords * 4;
+  // the select slots and the input-select states: one region, cleared by the first main-pass launch
+  const size_t slot_part = (size_t)nslots * kArrays * kSlotWords * 4;
+  L.slot_bytes = slot_part + (size_t)nisel * kIselStateWords * 4;
   L.slots = take(L.slot_bytes);
+  L.isel_state = L.slots + slot_part;
   if (near) {
     L.item_near = take((size_t)items * 4);
     L.item_near_off = take((size_t)items * 8);
@@ -280,6 +294,9 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
   if (batch) {
     L.table = take((size_t)nseg * sizeof(SegDesc));
     L.chunk_seg = take((size_t)chunks * 8);
+    L.isel_seg = take((size_t)nisel * 4);
+    L.isel_chunk = take((size_t)isel_chunks * 8);
+    L.isel_sums = take((size_t)isel_chunks * 3 * 8);
   }
   L.total = off + 256;
   return L;
@@ -333,6 +350,7 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   t.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
   t.item_near_off = near ? at<uint64_t>(ws, L.item_near_off) : nullptr;
   t.item_near_sum = near ? at<double>(ws, L.item_near_sum) : nullptr;
+  t.isel_sums = at<double>(ws, L.isel_sums);
   auto launch = [&](int reduce_blocks, int level, int arr_lo, int narr) -> int {
     TailArgs x = t;
     x.reduce_blocks = reduce_blocks;
@@ -503,7 +521,10 @@ struct BatchPlan {
     int dt, mode, kind;
     int seg_lo, seg_hi;
     int64_t item_lo, items, ipb;
+    int64_t ick_lo, ick_n;  // this group's input-select chunks in isel_chunk
   };
+  std::vector<int32_t> isel_seg;      // input-select segments
+  std::vector<int32_t> isel_chunk;    // (segment, chunk of the segment) pairs, grouped like the scans
   std::vector<Group> groups;
   bool stream_groups = false;  // large groups selected one block each (tail level 4)
   int64_t items = 0, samples = 0, chunks = 0, nslots = 0, run_slots = 0;
@@ -539,9 +560,13 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   bp.stream_groups = group_mode;
   const int rounds = chunks1 >= 4 * 8192 ? 4 : (chunks1 >= 2 * 8192 ? 2 : 1);
   static_assert(kMaxSelRounds >= 4, "select rounds");
-  for (SegDesc& d : segs) {
+  for (int i = 0; i < count; ++i) {
+    SegDesc& d = segs[i];
     d.sel_rounds = group_mode ? 1 : rounds;
     d.chunk_count = group_mode ? (d.m > 0 ? 1 : 0) : select_chunks(d.m, rounds);
+    // a large contiguous group: the p99 of abs/rel is selected from the inputs,
+    // and the main pass neither walks nor writes its samples
+    if (group_mode && d.m > kSmall && kinds[i] == K_CONTIG) d.flags |= kFlagInputSelect;
   }
   auto key = [&](int i) { return (segs[i].dtype * 2 + segs[i].mode) * 3 + kinds[i]; };
   std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return key(a) < key(b); });
@@ -561,9 +586,13 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     sample += (d.m + 63) & ~int64_t(63);  // each segment's samples start on a 256-byte line
     chunk += d.chunk_count;
     bp.near = bp.near || (d.flags & KVV_FLAG_NEAR_ZERO);
+    if (d.flags & kFlagInputSelect) {
+      d.isel_slot = (int32_t)bp.isel_seg.size();
+      bp.isel_seg.push_back(s);
+    }
     if (bp.groups.empty() || bp.groups.back().dt != d.dtype || bp.groups.back().mode != d.mode ||
         bp.groups.back().kind != kinds[i]) {
-      bp.groups.push_back({d.dtype, d.mode, kinds[i], s, s + 1, d.item_begin, d.item_count, 1});
+      bp.groups.push_back({d.dtype, d.mode, kinds[i], s, s + 1, d.item_begin, d.item_count, 1, 0, 0});
     } else {
       bp.groups.back().seg_hi = s + 1;
       bp.groups.back().items += d.item_count;
@@ -583,6 +612,19 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   bp.items = item;
   bp.samples = sample;
   bp.chunks = chunk;
+  // the input-select chunk launches follow the scan groups (one kernel per dtype)
+  for (auto& gr : bp.groups) {
+    gr.ick_lo = (int64_t)bp.isel_chunk.size() / 2;
+    for (int s = gr.seg_lo; s < gr.seg_hi; ++s) {
+      if (!(bp.table[s].flags & kFlagInputSelect)) continue;
+      bp.table[s].isel_chunk0 = (int32_t)(bp.isel_chunk.size() / 2);
+      for (int64_t c = 0; c * kIselChunk < bp.table[s].m; ++c) {
+        bp.isel_chunk.push_back(s);
+        bp.isel_chunk.push_back((int32_t)c);
+      }
+    }
+    gr.ick_n = (int64_t)bp.isel_chunk.size() / 2 - gr.ick_lo;
+  }
   if (bp.stream_groups) {
     // one select block per group: the largest groups first, so the longest
     // blocks start early and the small ones fill in behind them
@@ -601,14 +643,21 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
 int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st) {
   const int nseg = (int)bp.table.size();
   if (nseg == 0) return KVV_OK;
-  const WsLayout L =
-      workspace_layout(bp.run_slots, bp.samples, nseg, bp.nslots, bp.chunks, bp.items, bp.near, true);
+  const int64_t nisel = (int64_t)bp.isel_seg.size(), isel_chunks = (int64_t)bp.isel_chunk.size() / 2;
+  const WsLayout L = workspace_layout(bp.run_slots, bp.samples, nseg, bp.nslots, bp.chunks, bp.items, bp.near, true,
+                                      nisel, isel_chunks);
   int rc = check_ws(L, ws, ws_bytes, out);
   if (rc) return rc;
   SegDesc* dtable = at<SegDesc>(ws, L.table);
   int64_t* dchunk = at<int64_t>(ws, L.chunk_seg);
   KVV_HIP(hipMemcpyAsync(dtable, bp.table.data(), nseg * sizeof(SegDesc), hipMemcpyHostToDevice, st));
   if (bp.chunks) KVV_HIP(hipMemcpyAsync(dchunk, bp.chunk_seg.data(), bp.chunks * 8, hipMemcpyHostToDevice, st));
+  int32_t* disel = at<int32_t>(ws, L.isel_seg);
+  int2* dichunk = at<int2>(ws, L.isel_chunk);
+  if (nisel) {
+    KVV_HIP(hipMemcpyAsync(disel, bp.isel_seg.data(), nisel * 4, hipMemcpyHostToDevice, st));
+    KVV_HIP(hipMemcpyAsync(dichunk, bp.isel_chunk.data(), isel_chunks * 8, hipMemcpyHostToDevice, st));
+  }
   std::vector<NearLaunch> nears;
   bool zeroed = false;
   for (const auto& gr : bp.groups) {
@@ -635,6 +684,32 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     const int64_t grid = (gr.items + gr.ipb * kWaves - 1) / (gr.ipb * kWaves);
     hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
     KVV_HIP(hipGetLastError());
+  }
+  if (nisel) {
+    // p99 of the input-select segments: histograms, target bins, gather, final select
+    IselArgs ia{};
+    ia.table = dtable;
+    ia.segs = disel;
+    ia.state = at<uint32_t>(ws, L.isel_state);
+    ia.sums = at<double>(ws, L.isel_sums);
+    ia.buf[0] = at<float>(ws, L.sample_abs);
+    ia.buf[1] = at<float>(ws, L.sample_rel);
+    ia.res = out;
+    for (int pass = 0; pass < 2; ++pass) {
+      for (const auto& gr : bp.groups) {
+        if (gr.ick_n == 0) continue;
+        IselFn fn = isel_fn(gr.dt, pass == 1);
+        if (!fn) return fail(KVV_E_INVALID, "no input-select kernel for dtype");
+        IselArgs x = ia;
+        x.chunks = dichunk + gr.ick_lo;
+        x.chunk_lo = gr.ick_lo;
+        hipLaunchKernelGGL(fn, dim3((unsigned)gr.ick_n), dim3(kBlock), 0, st, x);
+        KVV_HIP(hipGetLastError());
+      }
+      if (pass == 0) hipLaunchKernelGGL(isel_find_kernel, dim3((unsigned)nisel), dim3(kBlock), 0, st, ia);
+      else hipLaunchKernelGGL(isel_final_kernel, dim3((unsigned)nisel), dim3(kBlock), 0, st, ia);
+      KVV_HIP(hipGetLastError());
+    }
   }
   return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, bp.near, L, ws, out, st, nears,
                      bp.stream_groups);
@@ -686,7 +761,7 @@ int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_te
   int rc = kvv::plan_batch(count, gens, refs, policies, bp);
   if (rc) return rc;
   *bytes = kvv::workspace_layout(bp.run_slots, bp.samples, (int64_t)bp.table.size(), bp.nslots, bp.chunks, bp.items,
-                                 bp.near, true)
+                                 bp.near, true, (int64_t)bp.isel_seg.size(), (int64_t)bp.isel_chunk.size() / 2)
                .total;
   return KVV_OK;
 }

@@ -34,6 +34,8 @@ constexpr int kMaxRounds = 4;         // dispatch rounds of a single-segment sca
 constexpr int kSmall = 8192;          // groups of at most this many samples are selected by one block
 constexpr int64_t kGroupStreamMax = 1 << 22;  // largest group one block streams in a many-group launch
 constexpr int kArrays = 3;            // abs, rel, near-zero abs
+constexpr uint32_t kFlagInputSelect = 0x80000000u;  // SegDesc.flags: abs/rel p99 selected from the inputs
+constexpr int64_t kIselChunk = 1 << 17;  // samples per block of the input-select chunk launches
 // Per (large segment, array) slot: level-0 histogram (256), level-1 and level-2
 // histograms (2 ranks x 4096 each) and the NaN count.
 constexpr int kH0 = 0, kH1 = 256, kH2 = 256 + 8192, kMisc = 256 + 16384;
@@ -83,6 +85,8 @@ struct SegDesc {
   int32_t out_index;      // position of this pair's kvv_result in the caller's array
   int32_t lslot;          // large-group select slot (m > kSmall), else -1
   int32_t sel_rounds;     // kSelChunk sub-chunks per select block of a large group (1..kMaxSelRounds)
+  int32_t isel_slot;      // input-select state of the segment (kFlagInputSelect), else -1
+  int32_t isel_chunk0;    // its first input-select chunk (batch-wide numbering)
   int64_t run_slot0;      // first run slot of this segment (a multiple of 4)
   int64_t row_len;        // L_ROWS: contiguous inner length
   Dims dims;              // L_ROWS: outer dims; L_GENERIC: all dims
@@ -1552,7 +1556,9 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
           const int64_t N1 = L1 + d.item_elems < d.n ? L1 + d.item_elems : d.n;
           full = load_item<DT, KIND>(d, L1, N1, gv, rv);
         }
-        if (!dense) sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, sb, ba, br);
+        // (an input-select segment's samples and sampled sums come from the input-select kernels)
+        if (!dense && !(d.flags & kFlagInputSelect))
+          sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, sb, ba, br);
         const uint64_t slow = phase_a_any<DT>(d, L0, R0, stage, full_now, acc, careful);
         if (__ballot(slow != 0)) {
           uint32_t nq = queue_all(slow, sm.queue[w]);
@@ -1566,7 +1572,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
           }
         }
         if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, R0, full_now, stage, acc, wc);
-        if (dense) dense_samples<DT, MODE>(d, L0, L1, stage, a.sample_abs, a.sample_rel);
+        if (dense && !(d.flags & kFlagInputSelect)) dense_samples<DT, MODE>(d, L0, L1, stage, a.sample_abs, a.sample_rel);
       }
       if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, wc, near_prev);
     }
@@ -1701,5 +1707,6 @@ __global__ __launch_bounds__(kBlock) void near_kernel(NearArgs a) {
 }
 
 #include "kvv_tail.h"
+#include "kvv_isel.h"
 
 }  // namespace kvv

@@ -7,15 +7,18 @@ namespace kvv {
 
 using ScanFn = void (*)(ScanArgs);
 using NearFn = void (*)(NearArgs);
+using IselFn = void (*)(IselArgs);
 
 #define KVV_CAT_(a, b) a##b
 #define KVV_CAT(a, b) KVV_CAT_(a, b)
 #define KVV_SCAN_FN(dt) KVV_CAT(kvv_scan_fn_, dt)
 #define KVV_NEAR_FN(dt) KVV_CAT(kvv_near_fn_, dt)
+#define KVV_ISEL_FN(dt) KVV_CAT(kvv_isel_fn_, dt)
 
 #define KVV_DECLARE(dt)                          \
   ScanFn KVV_SCAN_FN(dt)(int mode, int kind, bool batch); \
-  NearFn KVV_NEAR_FN(dt)(int mode);
+  NearFn KVV_NEAR_FN(dt)(int mode);                      \
+  IselFn KVV_ISEL_FN(dt)(bool gather);
 
 KVV_DECLARE(0)
 KVV_DECLARE(1)

@@ -1,7 +1,7 @@
-// Instantiates the scan and near-zero kernels of one element type.  The build
+// Instantiates the scan, near-zero and input-select kernels of one element type.  The build
 // compiles this file once per dtype code (-DKVV_DT=<kvv_dtype>) so the twelve
 // dtypes compile in parallel; kvv.hip reaches the kernels through the
-// kvv_scan_fn_<n> / kvv_near_fn_<n> accessors defined here.
+// kvv_scan_fn_<n> / kvv_near_fn_<n> / kvv_isel_fn_<n> accessors defined here.
 #include <hip/hip_runtime.h>
 
 #include "kvv.h"
@@ -40,6 +40,11 @@ ScanFn KVV_SCAN_FN(KVV_DT)(int mode, int kind, bool batch) {
 NearFn KVV_NEAR_FN(KVV_DT)(int mode) {
   return mode == KVV_MODE_ISCLOSE ? (NearFn)near_kernel<kDt, KVV_MODE_ISCLOSE>
                                   : (NearFn)near_kernel<kDt, KVV_MODE_MAX_ABS_DIFF>;
+}
+
+// Input-select chunk kernels: contiguous segments only, so the dtype's natural test.
+IselFn KVV_ISEL_FN(KVV_DT)(bool gather) {
+  return gather ? (IselFn)isel_gather_kernel<kDt, kNative> : (IselFn)isel_hist_kernel<kDt, kNative>;
 }
 
 }  // namespace kvv

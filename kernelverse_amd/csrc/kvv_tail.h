@@ -42,6 +42,7 @@ struct TailArgs {
   const uint32_t* item_near;
   uint64_t* item_near_off;
   const double* item_near_sum;
+  const double* isel_sums;    // input-select segments with m < n: sampled sums per chunk (3 each)
 };
 
 struct ReduceLds {
@@ -63,6 +64,7 @@ struct SelectLds {
   double part[kBlock];
   uint32_t sh[16];
   uint32_t misc[4];
+  uint32_t fill[2];  // input select: compacted values per array
 };
 static_assert(kSelChunk * kMaxSelRounds <= 65535 && kSmall <= 65535, "16-bit block bin counts");
 
@@ -305,13 +307,25 @@ __device__ inline void reduce_sums(const TailArgs& a, const SegDesc& d, int64_t 
   auto sum = [&](int i) { return L.td[i]; };
   kvv_result& o = a.res[d.out_index];
   if (tid == 0) {
-    // every element a sample: the sampled sums are the full sums
+    // every element a sample: the sampled sums are the full sums; an
+    // input-select segment's sampled sums are its chunks', in chunk order
     const int k = d.m == d.n ? 0 : 4;
-    o.sample_sum_gg = sum(k);
-    o.sample_sum_rr = sum(k + 1);
-    o.sample_sum_gr = sum(k + 2);
-    o.sample_cosine = cosine_of(sum(k + 2), sum(k), sum(k + 1));
-    const double gn = sqrt(sum(k)), rn = sqrt(sum(k + 1));
+    double sg = sum(k), sr = sum(k + 1), sx = sum(k + 2);
+    if (d.m != d.n && (d.flags & kFlagInputSelect)) {
+      sg = sr = sx = 0.0;
+      const int64_t nck = (d.m + kIselChunk - 1) / kIselChunk;
+      for (int64_t c = 0; c < nck; ++c) {
+        const double* p = a.isel_sums + (size_t)(d.isel_chunk0 + c) * 3;
+        sg += p[0];
+        sr += p[1];
+        sx += p[2];
+      }
+    }
+    o.sample_sum_gg = sg;
+    o.sample_sum_rr = sr;
+    o.sample_sum_gr = sx;
+    o.sample_cosine = cosine_of(sx, sg, sr);
+    const double gn = sqrt(sg), rn = sqrt(sr);
     o.sample_norm_ratio = (gn == 0.0 && rn == 0.0) ? 1.0 : (gn == 0.0 ? 0.0 : (rn == 0.0 ? __builtin_inf() : gn / rn));
   } else if (tid == 1) {
     o.sum_gg = sum(0);
@@ -471,23 +485,25 @@ __device__ inline void block_find2(const uint32_t* cA, const uint32_t* cB, bool 
 // torch's quantile interpolation between the order statistics (NaN when the
 // sample holds a NaN); the near-zero array also gets its sample mean.  Called
 // by all threads of the block.
+__device__ __forceinline__ void store_p99(kvv_result& res, int arr, const uint32_t key[2], float wgt, bool has_nan) {
+  double out = __builtin_nan("");
+  if (!has_nan) {
+    const float va = fkey_value(key[0]), vb = fkey_value(key[1]);
+    // small weights from the lower end, large ones from the upper end, one rounding each
+    const float diff = vb - va;
+    const float q = fabsf(wgt) < 0.5f ? fmaf(wgt, diff, va) : fmaf(wgt - 1.0f, diff, vb);
+    out = (double)q;
+  }
+  if (arr == 0) res.p99_abs = out;
+  else if (arr == 1) res.p99_rel = out;
+  else res.near_zero_p99_abs = out;
+}
+
 __device__ inline void finalize_group(const TailArgs& a, const SegDesc& d, int arr, int64_t count,
                                       const uint32_t key[2], float wgt, bool has_nan, SelectLds& L) {
   kvv_result& res = a.res[d.out_index];
   const int tid = threadIdx.x;
-  if (tid == 0) {
-    double out = __builtin_nan("");
-    if (!has_nan) {
-      const float va = fkey_value(key[0]), vb = fkey_value(key[1]);
-      // small weights from the lower end, large ones from the upper end, one rounding each
-      const float diff = vb - va;
-      const float q = fabsf(wgt) < 0.5f ? fmaf(wgt, diff, va) : fmaf(wgt - 1.0f, diff, vb);
-      out = (double)q;
-    }
-    if (arr == 0) res.p99_abs = out;
-    else if (arr == 1) res.p99_rel = out;
-    else res.near_zero_p99_abs = out;
-  }
+  if (tid == 0) store_p99(res, arr, key, wgt, has_nan);
   if (arr == 2) {
     // near-zero sample mean: fixed-order sum of the per-item sampled sums
     const int64_t per = (d.item_count + kBlock - 1) / kBlock;
@@ -517,12 +533,14 @@ __device__ __forceinline__ uint32_t block_sum_nan(uint32_t v, SelectLds& L) {
   return t;
 }
 
-// A group of at most kSmall samples: keys in registers, four 8-bit digit
-// passes over block histograms in LDS.
-__device__ inline void select_small(const TailArgs& a, const SegDesc& d, int arr, int64_t count, SelectLds& L) {
+// The keys of the order statistics of ranks rank[0] <= rank[1] among at most
+// kSmall values: keys in registers, four 8-bit digit passes over block
+// histograms in LDS.  Returns whether a value is NaN (the keys are then not
+// searched).  Called by all threads of the block.
+__device__ inline bool small_keys(const float* v, int64_t count, const uint32_t rank[2], uint32_t key[2],
+                                  SelectLds& L) {
   constexpr int PER = kSmall / kBlock;
   const int tid = threadIdx.x;
-  const float* v = a.arr[arr] + d.sample_off;
   float x[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -539,13 +557,10 @@ __device__ inline void select_small(const TailArgs& a, const SegDesc& d, int arr
     valid |= (idx < count && !isn ? 1u : 0u) << i;
     k[i] = fkey(x[i]);
   }
-  uint64_t rank64[2];
-  float wgt;
-  q99_ranks(count, rank64, wgt);
-  uint32_t key[2] = {0u, 0u};
+  key[0] = key[1] = 0u;
   const bool has_nan = block_sum_nan(nans, L) != 0;
   if (!has_nan) {
-    uint32_t resid[2] = {(uint32_t)rank64[0], (uint32_t)rank64[1]};
+    uint32_t resid[2] = {rank[0], rank[1]};
 #pragma unroll 1
     for (int pass = 0; pass < 4; ++pass) {
       const int shift = 24 - 8 * pass;
@@ -571,6 +586,17 @@ __device__ inline void select_small(const TailArgs& a, const SegDesc& d, int arr
       }
     }
   }
+  return has_nan;
+}
+
+// A group of at most kSmall samples, selected by one block.
+__device__ inline void select_small(const TailArgs& a, const SegDesc& d, int arr, int64_t count, SelectLds& L) {
+  uint64_t rank64[2];
+  float wgt;
+  q99_ranks(count, rank64, wgt);
+  const uint32_t rank[2] = {(uint32_t)rank64[0], (uint32_t)rank64[1]};
+  uint32_t key[2];
+  const bool has_nan = small_keys(a.arr[arr] + d.sample_off, count, rank, key, L);
   finalize_group(a, d, arr, count, key, wgt, has_nan, L);
 }
 
@@ -670,16 +696,14 @@ __device__ inline void group_pass_ranks(bool same, uint32_t key[2], uint32_t res
   __syncthreads();
 }
 
-// A whole large group selected by one block, streaming its samples once per
-// digit (bits 31..21, 20..10, 9..0).  Used when a launch holds enough groups to
-// fill the device by itself: no global histograms, no further launches.
-__device__ inline void select_group_stream(const TailArgs& a, const SegDesc& d, int arr, int64_t count,
-                                           SelectLds& L) {
-  const float* v = a.arr[arr] + d.sample_off;
-  uint64_t rank64[2];
-  float wgt;
-  q99_ranks(count, rank64, wgt);
-  uint32_t key[2] = {0u, 0u}, resid[2] = {(uint32_t)rank64[0], (uint32_t)rank64[1]};
+// The keys of the order statistics of ranks rank[0] <= rank[1] among `count`
+// values, found by one block streaming them once per digit (bits 31..21,
+// 20..10, 9..0).  Returns whether a value is NaN (the keys are then not
+// searched).  Called by all threads of the block.
+__device__ inline bool stream_keys(const float* v, int64_t count, const uint32_t rank[2], uint32_t key[2],
+                                   SelectLds& L) {
+  key[0] = key[1] = 0u;
+  uint32_t resid[2] = {rank[0], rank[1]};
   const uint32_t none[2] = {0u, 0u};
   const uint32_t nans = group_pass<21, 11, true>(v, count, none, true, L);
   const bool has_nan = block_sum_nan(nans, L) != 0;
@@ -692,6 +716,20 @@ __device__ inline void select_group_stream(const TailArgs& a, const SegDesc& d, 
     group_pass<0, 10, false>(v, count, key, same, L);
     group_pass_ranks<10>(same, key, resid, L);
   }
+  return has_nan;
+}
+
+// A whole large group selected by one block (stream_keys).  Used when a launch
+// holds enough groups to fill the device by itself: no global histograms, no
+// further launches.
+__device__ inline void select_group_stream(const TailArgs& a, const SegDesc& d, int arr, int64_t count,
+                                           SelectLds& L) {
+  uint64_t rank64[2];
+  float wgt;
+  q99_ranks(count, rank64, wgt);
+  const uint32_t rank[2] = {(uint32_t)rank64[0], (uint32_t)rank64[1]};
+  uint32_t key[2];
+  const bool has_nan = stream_keys(a.arr[arr] + d.sample_off, count, rank, key, L);
   finalize_group(a, d, arr, count, key, wgt, has_nan, L);
 }
 
@@ -862,6 +900,8 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
   if (count <= 0) return;
   if (LEVEL == 4) {
     // many-group launches: a large group without global histograms, one block
+    // (abs/rel of an input-select segment are selected by input_select_kernel)
+    if (arr < 2 && (d.flags & kFlagInputSelect)) return;
     if (count > kSmall && d.lslot < 0 && c == 0) select_group_stream(a, d, arr, count, lds.s);
     return;
   }
