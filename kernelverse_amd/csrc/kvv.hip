@@ -612,15 +612,19 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   bp.items = item;
   bp.samples = sample;
   bp.chunks = chunk;
-  // the input-select chunk launches follow the scan groups (one kernel per dtype)
+  // the input-select chunk launches follow the scan groups (one kernel per
+  // dtype); strided-sample chunks (element loads, slower) are dispatched first
   for (auto& gr : bp.groups) {
     gr.ick_lo = (int64_t)bp.isel_chunk.size() / 2;
-    for (int s = gr.seg_lo; s < gr.seg_hi; ++s) {
-      if (!(bp.table[s].flags & kFlagInputSelect)) continue;
-      bp.table[s].isel_chunk0 = (int32_t)(bp.isel_chunk.size() / 2);
-      for (int64_t c = 0; c * kIselChunk < bp.table[s].m; ++c) {
-        bp.isel_chunk.push_back(s);
-        bp.isel_chunk.push_back((int32_t)c);
+    for (int pass = 0; pass < 2; ++pass) {
+      for (int s = gr.seg_lo; s < gr.seg_hi; ++s) {
+        const SegDesc& d = bp.table[s];
+        if (!(d.flags & kFlagInputSelect) || (d.m == d.n) != (pass == 1)) continue;
+        bp.table[s].isel_chunk0 = (int32_t)(bp.isel_chunk.size() / 2);
+        for (int64_t c = 0; c * isel_chunk_len(d) < d.m; ++c) {
+          bp.isel_chunk.push_back(s);
+          bp.isel_chunk.push_back((int32_t)c);
+        }
       }
     }
     gr.ick_n = (int64_t)bp.isel_chunk.size() / 2 - gr.ick_lo;

@@ -10,7 +10,7 @@
 // arrays three times, spread over chunks instead of one block per group.
 // Four launches after the main pass:
 //
-//   isel_hist_kernel    one block per chunk of kIselChunk samples: 11-bit
+//   isel_hist_kernel    one block per chunk of samples: 11-bit
 //                       histograms of the top key digit (bits 31..21) of
 //                       abs_diff and rel_diff, added into the segment's global
 //                       histograms (nonzero bins only); exact zeros (identical
@@ -143,6 +143,8 @@ __device__ __forceinline__ int64_t sample_index(const SegDesc& d, int64_t i, dou
 
 // Calls f(abs_diff, den, act, g, r) for samples [i0, i1) of segment d (m < n,
 // contiguous): kIselSampleUnroll samples per thread and round, element loads.
+// A thread's samples are kBlock apart; its index steps from one to the next
+// with the quotient and remainder of kBlock * s_mod / (m - 1).
 constexpr int kIselSampleUnroll = 8;
 template <int DT, int MODE, typename F>
 __device__ __forceinline__ void sample_pass(const SegDesc& d, int64_t i0, int64_t i1, F&& f) {
@@ -150,8 +152,14 @@ __device__ __forceinline__ void sample_pass(const SegDesc& d, int64_t i0, int64_
   typedef const __attribute__((address_space(1))) T* GT;
   const GT g = (GT)d.g;
   const GT r = (GT)d.r;
-  const double inv_den = 1.0 / (double)(d.m - 1);
   const int tid = threadIdx.x;
+  const uint32_t den = (uint32_t)(d.m - 1);  // m <= 2^24
+  const uint64_t step_t = (uint64_t)kBlock * d.s_mod;
+  const uint32_t step_q = (uint32_t)(step_t / den), step_r = (uint32_t)(step_t % den);
+  const int64_t step_idx = (int64_t)kBlock * (int64_t)d.s_div + step_q;
+  // the thread's first sample: index and remainder of i * s_mod / (m - 1)
+  int64_t idx = sample_index(d, i0 + tid, 1.0 / (double)den);
+  uint32_t rem = (uint32_t)(((uint64_t)(i0 + tid) * d.s_mod) % den);
 #pragma unroll 1
   for (int64_t b = i0; b < i1; b += kIselSampleUnroll * kBlock) {
     T gc[kIselSampleUnroll], rc[kIselSampleUnroll];
@@ -160,10 +168,13 @@ __device__ __forceinline__ void sample_pass(const SegDesc& d, int64_t i0, int64_
       const int64_t i = b + u * kBlock + tid;
       gc[u] = rc[u] = (T)0;
       if (i < i1) {
-        const int64_t idx = sample_index(d, i, inv_den);
         gc[u] = g[idx];
         rc[u] = r[idx];
       }
+      rem += step_r;
+      const bool carry = rem >= den;
+      rem -= carry ? den : 0u;
+      idx += step_idx + (carry ? 1 : 0);
     }
 #pragma unroll
     for (int u = 0; u < kIselSampleUnroll; ++u) {
@@ -185,8 +196,9 @@ __device__ __forceinline__ void unit_pass(const SegDesc& d, int64_t e0, int64_t 
 __device__ __forceinline__ void chunk_range(const IselArgs& a, const SegDesc*& d, int64_t& e0, int64_t& e1) {
   const int2 ck = a.chunks[blockIdx.x];
   d = &a.table[ck.x];
-  e0 = (int64_t)ck.y * kIselChunk;
-  e1 = e0 + kIselChunk < d->m ? e0 + kIselChunk : d->m;
+  const int64_t len = isel_chunk_len(*d);
+  e0 = (int64_t)ck.y * len;
+  e1 = e0 + len < d->m ? e0 + len : d->m;
 }
 
 template <int DT, int MODE>

@@ -35,7 +35,8 @@ constexpr int kSmall = 8192;          // groups of at most this many samples are
 constexpr int64_t kGroupStreamMax = 1 << 22;  // largest group one block streams in a many-group launch
 constexpr int kArrays = 3;            // abs, rel, near-zero abs
 constexpr uint32_t kFlagInputSelect = 0x80000000u;  // SegDesc.flags: abs/rel p99 selected from the inputs
-constexpr int64_t kIselChunk = 1 << 17;  // samples per block of the input-select chunk launches
+constexpr int64_t kIselChunk = 1 << 17;        // elements per input-select chunk (every element a sample)
+constexpr int64_t kIselChunkSampled = 1 << 15;  // samples per chunk at strided positions (element loads)
 // Per (large segment, array) slot: level-0 histogram (256), level-1 and level-2
 // histograms (2 ranks x 4096 each) and the NaN count.
 constexpr int kH0 = 0, kH1 = 256, kH2 = 256 + 8192, kMisc = 256 + 16384;
@@ -91,6 +92,11 @@ struct SegDesc {
   int64_t row_len;        // L_ROWS: contiguous inner length
   Dims dims;              // L_ROWS: outer dims; L_GENERIC: all dims
 };
+
+// Samples per input-select chunk of segment d.
+__host__ __device__ inline int64_t isel_chunk_len(const SegDesc& d) {
+  return d.m == d.n ? kIselChunk : kIselChunkSampled;
+}
 
 // Partial verdict of a contiguous run of items handled by one block, stored
 // field-major ("columns") at a dense run slot: column c of slot k is at

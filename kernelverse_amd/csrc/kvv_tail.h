@@ -313,7 +313,7 @@ __device__ inline void reduce_sums(const TailArgs& a, const SegDesc& d, int64_t 
     double sg = sum(k), sr = sum(k + 1), sx = sum(k + 2);
     if (d.m != d.n && (d.flags & kFlagInputSelect)) {
       sg = sr = sx = 0.0;
-      const int64_t nck = (d.m + kIselChunk - 1) / kIselChunk;
+      const int64_t nck = (d.m + kIselChunkSampled - 1) / kIselChunkSampled;
       for (int64_t c = 0; c < nck; ++c) {
         const double* p = a.isel_sums + (size_t)(d.isel_chunk0 + c) * 3;
         sg += p[0];
