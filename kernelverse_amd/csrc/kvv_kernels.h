@@ -1466,7 +1466,10 @@ __device__ inline void block_record_part(const ScanArgs& a, SM& sm, Acc& acc, ui
 template <int DT, int MODE, int KIND, bool BATCH>
 __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a) {
   __shared__ typename ScanLds<DT, KIND>::type sm;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  // the wave index, and all that derives from it (item range, segment, run), is
+  // wave-uniform: segment fields are then read with scalar loads, which the
+  // item loop's waits on the prefetched vector loads do not cover
+  const int tid = threadIdx.x, w = (int)uniform((uint32_t)(tid >> 6)), lane = tid & 63;
   uint32_t* wc = sm.wcnt[w];
   if (lane < WC_COUNT) wc[lane] = 0;
   if constexpr (!BATCH) {
@@ -1516,8 +1519,12 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
       const int mid = (lo + hi + 1) >> 1;
       if (a.table[mid].item_begin <= i0) lo = mid; else hi = mid - 1;
     }
-    s = lo;
+    s = (int)uniform((uint32_t)lo);
   }
+  // the segment table through the constant address space: with a uniform index
+  // its fields are scalar loads
+  typedef const __attribute__((address_space(4))) SegDesc CSegDesc;
+  const CSegDesc* ctable = (const CSegDesc*)a.table;
   uint32_t careful = 0;
   SampleBuf sb;
   sb.at0 = kNone;
@@ -1527,7 +1534,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
   // one pass per run of items of one segment (a single-segment launch has one);
   // the prefetched registers are dead between runs, where the record is written
   for (int64_t it = i0;;) {
-    const SegDesc& d = BATCH ? a.table[s] : a.seg0;
+    const SegDesc& d = BATCH ? *(const SegDesc*)&ctable[s] : a.seg0;
     const int64_t run_start = it;
     const int64_t seg_end = d.item_begin + d.item_count;
     const int64_t run_end = i1 < seg_end ? i1 : seg_end;
@@ -1587,7 +1594,8 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
     if constexpr (BATCH) {
       flush_run(acc, wc, ColSink{&a.runs, run_slot(d, run_start)}, base);
       if (it >= i1) break;
-      while (it >= a.table[s].item_begin + a.table[s].item_count) ++s;
+      while (it >= ctable[s].item_begin + ctable[s].item_count) ++s;
+      s = (int)uniform((uint32_t)s);
     } else {
       block_record_part(a, sm, acc, wc, w, base);
       break;
