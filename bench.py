@@ -140,7 +140,7 @@ def cpu_baseline(pairs, budget_s: float = 20.0):
 # dispatch) scaled by what the same counters read for a plain 512 MiB device copy (factors below); the runs and
 # commands are in profiles/scan_bf16_c1_traffic.md.  Keyed by config.
 PMC_TRAFFIC = {
-    "c1": {"fetch_kib": 524486.4, "write_kib": 9090.2, "fetch_factor": 524288.0 / 262157.4, "write_factor": 1.0},
+    "c1": {"fetch_kib": 524479.7, "write_kib": 9091.1, "fetch_factor": 524288.0 / 262157.4, "write_factor": 1.0},
 }
 
 
