@@ -446,20 +446,43 @@ __device__ __forceinline__ uint32_t load_item(const SegDesc& d, int64_t L0, int6
   using T = typename IO::T;
   constexpr int V = IO::V;
   uint32_t full = 0;
+  // rows: one division per lane and item; a lane's later vectors step the
+  // (row, column) pair, rows being at least one step (64 vectors) long
+  int64_t row = 0, col = 0;
+  const bool step_rows = KIND != K_CONTIG && d.row_len >= 64 * V;
+  if constexpr (KIND != K_CONTIG) {
+    if (step_rows) {
+      const int64_t v0 = L0 + (int64_t)lane_id() * V;
+      row = ((v0 | d.row_len) >> 32) == 0 ? (int64_t)((uint32_t)v0 / (uint32_t)d.row_len) : v0 / d.row_len;
+      col = v0 - row * d.row_len;
+    }
+  }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t v = L0 + (int64_t)(u * 64 + lane_id()) * V;
+    if constexpr (KIND != K_CONTIG) {
+      if (u > 0 && step_rows) {
+        col += 64 * V;
+        if (col >= d.row_len) {
+          col -= d.row_len;
+          ++row;
+        }
+      }
+    }
     if (v + V <= L1) {
       full |= 1u << u;
       int64_t og, orr;
       if constexpr (KIND == K_CONTIG) {
         og = orr = v;
       } else {
-        const int64_t row = v / d.row_len;
-        const int64_t col = v - row * d.row_len;
-        outer_offsets(d.dims, row, og, orr);
-        og += col;
-        orr += col;
+        int64_t r = row, c = col;
+        if (!step_rows) {
+          r = v / d.row_len;
+          c = v - r * d.row_len;
+        }
+        outer_offsets(d.dims, r, og, orr);
+        og += c;
+        orr += c;
       }
       // streamed once: non-temporal loads keep them from displacing reusable lines
       gv[u] = nt_load16(reinterpret_cast<const T*>(d.g) + og);

@@ -4,7 +4,7 @@ A batch with at least as many groups of more than 8192 samples as the device
 has CUs selects the p99 of each contiguous pair straight from its two inputs
 (two passes over the samples, the target bins' values compacted, zeros only
 counted).  Every p99 here must equal the oracle's torch.quantile over the
-sampled abs_diff / rel_diff, across element types and the cases the compaction
+sampled abs_diff / rel_diff, across twelve element types and the cases the compaction
 distinguishes: the order statistics inside the zeros, straddling the last zero
 and the first non-zero value, in two adjacent bins, with more than 8192 values
 in the target bin (streamed, not in LDS), negative int32 abs_diff (|INT_MIN|
@@ -26,7 +26,7 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
 TOL = {"FP32": {"rtol": 1e-5, "atol": 1e-5}, "BF16": {"rtol": 1.6e-2, "atol": 1e-2},
-       "FP16": {"rtol": 1e-3, "atol": 1e-3}, "INT32": {"max_abs_diff": 1}}
+       "FP16": {"rtol": 1e-3, "atol": 1e-3}, "INT32": {"max_abs_diff": 1}, "INT64": {"max_abs_diff": 2}}
 
 
 def _say(*a):
@@ -114,12 +114,29 @@ def _pair(i, rng):
         d[hi:] = 0.2                      # ranks >= hi fall in a higher bin
         g = r + d[torch.from_numpy(rng.permutation(n))]
         return g, r
-    if kind == 10:      # fp8 e4m3 code flips
-        r = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(torch.float8_e4m3fn)
+    if kind == 10:      # fp8 code flips (e4m3fn, or e5m2 every other time)
+        dt = torch.float8_e5m2 if i % 24 == 10 else torch.float8_e4m3fn
+        r = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(dt)
         g = r.clone()
         codes = g.view(torch.int8)
         idx = torch.from_numpy(rng.choice(n, size=n // 30, replace=False))
         codes[idx] ^= 1
+        return g, r
+    if kind == 11 and i % 36 == 11:  # int64 beyond int32 (the int32 casts wrap)
+        r = torch.from_numpy(rng.integers(-2**40, 2**40, size=n))
+        g = r.clone()
+        idx = torch.from_numpy(rng.choice(n, size=n // 25, replace=False))
+        g[idx] += torch.from_numpy(rng.integers(-5, 6, size=idx.numel()))
+        return g, r
+    if kind == 11 and i % 36 == 23:  # int16 and bool
+        r = torch.from_numpy(rng.integers(-300, 300, size=n).astype(np.int16))
+        g = r.clone()
+        g[:: 7] += 1
+        return g, r
+    if kind == 11 and i % 36 == 35:
+        r = torch.from_numpy(rng.integers(0, 2, size=n).astype(np.bool_))
+        g = r.clone()
+        g[:: 13] = ~g[:: 13]
         return g, r
     return _fp32_noise(n, rng)
 
