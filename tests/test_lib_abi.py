@@ -102,3 +102,22 @@ def test_workspace_grows_with_samples_and_near_zero():
     lib.kvv_workspace_size(t, t, _policy(), ctypes.byref(b))
     lib.kvv_workspace_size(t, t, _policy(flags=_lib.FLAG_NEAR_ZERO), ctypes.byref(c))
     assert a.value < b.value < c.value
+
+
+def test_many_group_batch_reserves_input_select_state():
+    """A batch with more large contiguous pairs than the device has CUs selects
+    their p99 from the inputs: its workspace holds 16,640 bytes of state per
+    such pair (plus the chunk list and the per-chunk sampled sums), which the
+    same batch with transposed pairs (selected from sample arrays) does not."""
+    lib = _lib.load()
+    count = 300  # above any device's CU count (no device here: the planner assumes 256)
+    GA, PA = _lib.KvvTensor * count, _lib.KvvPolicy * count
+    pols = PA(*[_policy() for _ in range(count)])
+    contig = GA(*[_tensor((100, 100), (100, 1), ptr=4096 * (1 + i)) for i in range(count)])
+    transposed = GA(*[_tensor((100, 100), (1, 100), ptr=4096 * (1 + i)) for i in range(count)])
+    a, b = ctypes.c_size_t(), ctypes.c_size_t()
+    assert lib.kvv_batch_workspace_size(count, contig, contig, pols, ctypes.byref(a)) == 0
+    assert lib.kvv_batch_workspace_size(count, transposed, transposed, pols, ctypes.byref(b)) == 0
+    state = count * 16_640
+    lists = 256 * (-(-count * 4 // 256) + -(-count * 8 // 256) + -(-count * 24 // 256))  # one chunk per pair
+    assert a.value - b.value == state + lists
