@@ -103,16 +103,16 @@ __device__ __forceinline__ int64_t segment_runs(const SegDesc& d) {
   return 1 + (b_end > b_first ? b_end - b_first : 0);
 }
 
-// Folds a u32 column part [j0, j1) (sum or max), 4 slots per load, 16 loads in flight.
+// Folds a u32 column part [j0, j1) (sum or max), 4 slots per load, 8 loads in flight.
 template <bool MAX>
 __device__ __forceinline__ uint64_t fold_u32(const uint32_t* col, int64_t j0, int64_t j1) {
   uint64_t t = 0;
-  for (int64_t j = j0; j < j1; j += 64) {
-    uint4 q[16];
+  for (int64_t j = j0; j < j1; j += 32) {
+    uint4 q[8];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) q[i] = j + 4 * i < j1 ? *reinterpret_cast<const uint4*>(col + j + 4 * i) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < 8; ++i) q[i] = j + 4 * i < j1 ? *reinterpret_cast<const uint4*>(col + j + 4 * i) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < 8; ++i) {
       const uint32_t v[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -284,12 +284,12 @@ __device__ inline void reduce_sums(const TailArgs& a, const SegDesc& d, int64_t 
   const int tid = threadIdx.x;
   const uint64_t* col = a.runs.u64 + (size_t)(CL_S0 + (f < F ? f : 0)) * a.runs.stride + d.run_slot0;
   double t = 0.0;
-  for (int64_t j = j0; j < j1; j += 32) {
-    uint4 q[16];
+  for (int64_t j = j0; j < j1; j += 16) {
+    uint4 q[8];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) q[i] = j + 2 * i < j1 ? *reinterpret_cast<const uint4*>(col + j + 2 * i) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < 8; ++i) q[i] = j + 2 * i < j1 ? *reinterpret_cast<const uint4*>(col + j + 2 * i) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
+    for (int e = 0; e < 16; ++e) {
       if (j + e >= j1) continue;
       const uint4 w = q[e >> 1];
       const uint64_t bits = (e & 1) ? (((uint64_t)w.w << 32) | w.z) : (((uint64_t)w.y << 32) | w.x);
