@@ -91,13 +91,14 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(pairs, budget_s: float = 20.0):
+def cpu_baseline(pairs, budget_s: float = 12.0):
     """Torch-CPU oracle verdicts (the port, oracle/torch_verdict.py) on a bounded leading sample of the workload:
-    the first 16 Mi elements of a single pair, or the leading pairs of a batch up to 16 Mi elements."""
+    the first 64 Mi elements of a single pair, or the leading pairs of a batch up to 64 Mi elements, repeated
+    for about budget_s seconds of CPU work (at least 3 runs)."""
     from oracle import torch_verdict as tv
     threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
-    cap = 1 << 24
+    cap = 1 << 26
     host, taken = [], 0
     t0 = time.perf_counter()
     for g_dev, r_dev, tol in pairs:
@@ -119,7 +120,7 @@ def cpu_baseline(pairs, budget_s: float = 20.0):
     run_all()  # warm-up
     times = []
     t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 200):
         t1 = time.perf_counter()
         run_all()
         times.append(time.perf_counter() - t1)
