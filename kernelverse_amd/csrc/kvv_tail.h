@@ -19,9 +19,10 @@
 // torch.quantile and writes the result.  The main pass cleared the histograms.
 //
 // A launch with at least as many large groups as the device has CUs (a big
-// batch) selects each of them with one block instead ("level" 4,
-// select_group_stream): the block streams its group once per digit, so no
-// global histograms or level launches are needed.
+// batch) needs no global histograms or level launches: a contiguous pair's
+// abs/rel are selected from its inputs (kvv_isel.h), any other large group by
+// one block ("level" 4, select_group_stream) that streams the group once per
+// digit.
 
 struct TailArgs {
   SegDesc seg0;               // the segment when table == nullptr
@@ -900,7 +901,7 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
   if (count <= 0) return;
   if (LEVEL == 4) {
     // many-group launches: a large group without global histograms, one block
-    // (abs/rel of an input-select segment are selected by input_select_kernel)
+    // (abs/rel of an input-select segment are selected by the isel_* kernels)
     if (arr < 2 && (d.flags & kFlagInputSelect)) return;
     if (count > kSmall && d.lslot < 0 && c == 0) select_group_stream(a, d, arr, count, lds.s);
     return;
