@@ -205,3 +205,28 @@ def test_input_select_strided_samples(kv):
             if not close(got, want, SUM_RTOL):
                 probs.append(f"{k}: device {got!r} vs {want!r}")
         assert not probs, (i, i % 12, tuple(g.shape), g.dtype, probs)
+
+
+def test_input_select_long_strided_pair(kv):
+    """One pair of 50 M elements (10^6 strided samples, stride ~50) among 260
+    smaller ones: the chunks step far-apart sample indices, and the sampled
+    sums of 31 chunks are folded in order."""
+    rng = np.random.default_rng(13)
+    big = _fp32_noise(50_000_000, rng)
+    big[0][:: 77_777] += 0.25
+    pairs = [big] + [_fp32_noise(int(rng.integers(9_000, 20_000)), rng) for _ in range(260)]
+    recs = kv.verdict_records([(g.to(DEV), r.to(DEV)) for g, r in pairs], tolerance_policy=TOL)
+    g, r = big
+    rec = recs[0]
+    abs_d, rel_d, _, _ = tv.mismatch_parts(g, r, TOL)
+    for k, vals in (("p99_abs", abs_d), ("p99_rel", rel_d)):
+        want = tv.p99_meta(vals)
+        assert same_value(float(rec[k]), float(want)), (k, rec[k], want)
+    gs = tv.sample_flat_values(g.double(), 1_000_000)
+    rs = tv.sample_flat_values(r.double(), 1_000_000)
+    for k, want in (("sample_sum_gg", float((gs * gs).sum())), ("sample_sum_rr", float((rs * rs).sum())),
+                    ("sample_sum_gr", float((gs * rs).sum()))):
+        assert close(float(rec[k]), want, SUM_RTOL), (k, rec[k], want)
+    for (g2, r2), rec2 in zip(pairs[1:40], recs[1:40]):
+        a2, _, _, _ = tv.mismatch_parts(g2, r2, TOL)
+        assert same_value(float(rec2["p99_abs"]), float(tv.p99_meta(a2)))
