@@ -55,7 +55,10 @@ enum kvv_dtype {
   KVV_I16 = 8,       /* int16 */
   KVV_I32 = 9,       /* int32 */
   KVV_I64 = 10,      /* int64 */
-  KVV_BOOL = 11      /* bool (one byte, 0 or 1) */
+  KVV_BOOL = 11,     /* bool (one byte, 0 or 1) */
+  KVV_U16 = 12,      /* uint16 */
+  KVV_U32 = 13,      /* uint32 */
+  KVV_U64 = 14       /* uint64 */
 };
 
 /* Error codes. */

@@ -18,7 +18,7 @@ MAX_DIMS = 8
 HIST_BUCKETS = 16
 
 # enum kvv_dtype
-F32, F16, BF16, F64, F8E4M3FN, F8E5M2, I8, U8, I16, I32, I64, BOOL = range(12)
+F32, F16, BF16, F64, F8E4M3FN, F8E5M2, I8, U8, I16, I32, I64, BOOL, U16, U32, U64 = range(15)
 # enum kvv_mode
 MODE_ISCLOSE, MODE_MAX_ABS_DIFF = 0, 1
 FLAG_NEAR_ZERO = 0x1

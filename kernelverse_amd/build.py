@@ -3,7 +3,7 @@
     python -m kernelverse_amd.build
 
 The scan kernels are instantiated once per element type from
-csrc/kvv_scan_inst.hip (-DKVV_DT=<code>), so the twelve dtypes compile in
+csrc/kvv_scan_inst.hip (-DKVV_DT=<code>), so the fifteen dtypes compile in
 parallel next to csrc/kvv.hip (API, reduce, select, finalize); the objects are
 linked into kernelverse_amd/libkvv.so, which travels with the repository.
 """
@@ -22,7 +22,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libkvv.so"
-N_DTYPES = 12
+N_DTYPES = 15
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

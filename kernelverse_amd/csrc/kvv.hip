@@ -35,9 +35,9 @@ constexpr int64_t kMaxSamplesCap = int64_t(1) << 24;
 
 int elem_size(int dt) {
   switch (dt) {
-    case KVV_F32: case KVV_I32: return 4;
-    case KVV_F16: case KVV_BF16: case KVV_I16: return 2;
-    case KVV_F64: case KVV_I64: return 8;
+    case KVV_F32: case KVV_I32: case KVV_U32: return 4;
+    case KVV_F16: case KVV_BF16: case KVV_I16: case KVV_U16: return 2;
+    case KVV_F64: case KVV_I64: case KVV_U64: return 8;
     case KVV_F8E4M3FN: case KVV_F8E5M2: case KVV_I8: case KVV_U8: case KVV_BOOL: return 1;
     default: return 0;
   }
@@ -97,6 +97,7 @@ ScanFn scan_fn(int dt, int mode, int kind, bool batch) {
 #define KVV_CASE(X) case X: return KVV_SCAN_FN(X)(mode, kind, batch);
     KVV_CASE(0) KVV_CASE(1) KVV_CASE(2) KVV_CASE(3) KVV_CASE(4) KVV_CASE(5)
     KVV_CASE(6) KVV_CASE(7) KVV_CASE(8) KVV_CASE(9) KVV_CASE(10) KVV_CASE(11)
+    KVV_CASE(12) KVV_CASE(13) KVV_CASE(14)
 #undef KVV_CASE
     default: return nullptr;
   }
@@ -107,6 +108,7 @@ IselFn isel_fn(int dt, bool gather) {
 #define KVV_CASE(X) case X: return KVV_ISEL_FN(X)(gather);
     KVV_CASE(0) KVV_CASE(1) KVV_CASE(2) KVV_CASE(3) KVV_CASE(4) KVV_CASE(5)
     KVV_CASE(6) KVV_CASE(7) KVV_CASE(8) KVV_CASE(9) KVV_CASE(10) KVV_CASE(11)
+    KVV_CASE(12) KVV_CASE(13) KVV_CASE(14)
 #undef KVV_CASE
     default: return nullptr;
   }
@@ -117,6 +119,7 @@ NearFn near_fn(int dt, int mode) {
 #define KVV_CASE(X) case X: return KVV_NEAR_FN(X)(mode);
     KVV_CASE(0) KVV_CASE(1) KVV_CASE(2) KVV_CASE(3) KVV_CASE(4) KVV_CASE(5)
     KVV_CASE(6) KVV_CASE(7) KVV_CASE(8) KVV_CASE(9) KVV_CASE(10) KVV_CASE(11)
+    KVV_CASE(12) KVV_CASE(13) KVV_CASE(14)
 #undef KVV_CASE
     default: return nullptr;
   }
@@ -513,6 +516,12 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   return launch_tail(&d, nullptr, nullptr, 1, d.chunk_count, nslots, near, L, ws, out, st, nears);
 }
 
+size_t single_workspace_bytes(const SegDesc& d) {
+  return workspace_layout(run_slot_bound(d.item_count), d.m, 1, d.m > kSmall ? 1 : 0, d.chunk_count, d.item_count,
+                          (d.flags & KVV_FLAG_NEAR_ZERO) != 0, false)
+      .total;
+}
+
 // ------------------------------------------------------------ batch
 struct BatchPlan {
   std::vector<SegDesc> table;   // sorted by (dtype, mode, kind) group, then input order
@@ -734,10 +743,7 @@ int kvv_workspace_size(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_p
   kvv::SegDesc d;
   int rc = kvv::plan_single(gen, ref, policy, d);
   if (rc) return rc;
-  *bytes =
-      kvv::workspace_layout(kvv::run_slot_bound(d.item_count), d.m, 1, d.m > kvv::kSmall ? 1 : 0, d.chunk_count,
-                            d.item_count, (d.flags & KVV_FLAG_NEAR_ZERO) != 0, false)
-          .total;
+  *bytes = kvv::single_workspace_bytes(d);
   return KVV_OK;
 }
 

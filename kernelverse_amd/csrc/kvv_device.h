@@ -168,6 +168,15 @@ template <> struct Elem<KVV_U8> : IntElem<uint8_t, uint8_t> {};
 template <> struct Elem<KVV_I16> : IntElem<uint16_t, int16_t> {};
 template <> struct Elem<KVV_I32> : IntElem<uint32_t, int32_t> {};
 template <> struct Elem<KVV_I64> : IntElem<uint64_t, int64_t> {};
+template <> struct Elem<KVV_U16> : IntElem<uint16_t, uint16_t> {};
+template <> struct Elem<KVV_U32> : IntElem<uint32_t, uint32_t> {};
+// uint64: the float conversions take the unsigned value (torch's uint64 ->
+// float32/float64); v(), which only the integer ULP distance reads, is the
+// int64 reinterpretation of the code.
+template <> struct Elem<KVV_U64> : IntElem<uint64_t, int64_t> {
+  __device__ static float f32(T c) { return (float)c; }
+  __device__ static double f64(T c) { return (double)c; }
+};
 template <> struct Elem<KVV_BOOL> : IntElemBase {
   using T = uint8_t;
   static constexpr int width = 8;

@@ -14,10 +14,10 @@
 //                       histograms of the top key digit (bits 31..21) of
 //                       abs_diff and rel_diff, added into the segment's global
 //                       histograms (nonzero bins only); exact zeros (identical
-//                       pairs) are only counted.  With m < n the block also
-//                       sums g^2, r^2 and g*r over its samples (the sampled
-//                       cosine and norm ratio, GCR:351-393), which the run
-//                       fold adds up in chunk order;
+//                       pairs) are only counted.  The block also sums g^2,
+//                       r^2 and g*r over its samples (the sampled cosine and
+//                       norm ratio, GCR:351-393), which the run fold adds up
+//                       in chunk order;
 //   isel_find_kernel    one block per segment: the bins of the two order
 //                       statistics of each array and the count below them;
 //   isel_gather_kernel  one block per chunk: the values that fall in those bins
@@ -51,7 +51,7 @@ struct IselArgs {
   const SegDesc* table;
   const int2* chunks;      // chunk launches: (segment, chunk of the segment) per block
   int64_t chunk_lo;        // chunk launches: batch-wide number of the launch's first chunk
-  double* sums;            // sampled sums per chunk (3 each; segments with m < n)
+  double* sums;            // sampled sums per chunk (3 each)
   const int32_t* segs;     // segment launches: segment per block
   uint32_t* state;         // kIselStateWords per input-select segment (SegDesc::isel_slot)
   float* buf[2];           // the sample arrays: space for the appended abs_diff, rel_diff
@@ -216,7 +216,6 @@ __global__ __launch_bounds__(kBlock) void isel_hist_kernel(IselArgs a) {
   using E = Elem<DT>;
   uint32_t zeros = 0;
   double sg = 0.0, sr = 0.0, sx = 0.0;
-  const bool sampled = d->m != d->n;
   unit_pass<DT, MODE>(*d, e0, e1, [&](float adf, float den, bool act, typename E::T gc, typename E::T rc) {
     const bool z = adf == 0.0f;
     zeros += act && z ? 1u : 0u;
@@ -225,29 +224,25 @@ __global__ __launch_bounds__(kBlock) void isel_hist_kernel(IselArgs a) {
     const uint32_t br = cnt ? fkey(adf / den) >> 21 : 2048u + lane;
     atomicAdd(&h[0][ba], 1u);
     atomicAdd(&h[1][br], 1u);
-    if (sampled) {
-      // inactive lanes hold zero codes, which add 0
-      const double g64 = E::f64(gc), r64 = E::f64(rc);
-      sg = fma(g64, g64, sg);
-      sr = fma(r64, r64, sr);
-      sx = fma(g64, r64, sx);
-    }
+    // inactive lanes hold zero codes, which add 0
+    const double g64 = E::f64(gc), r64 = E::f64(rc);
+    sg = fma(g64, g64, sg);
+    sr = fma(r64, r64, sr);
+    sx = fma(g64, r64, sx);
   });
   zeros = wave_sum(zeros);
   if (lane == 0) zs[tid >> 6] = zeros;
-  if (sampled) {
-    // the chunk's sampled sums, in a fixed order (bit-reproducible)
-    sg = wave_sum(sg);
-    sr = wave_sum(sr);
-    sx = wave_sum(sx);
-    if (lane == 0) {
-      ss[tid >> 6][0] = sg;
-      ss[tid >> 6][1] = sr;
-      ss[tid >> 6][2] = sx;
-    }
+  // the chunk's sampled sums, in a fixed order (bit-reproducible)
+  sg = wave_sum(sg);
+  sr = wave_sum(sr);
+  sx = wave_sum(sx);
+  if (lane == 0) {
+    ss[tid >> 6][0] = sg;
+    ss[tid >> 6][1] = sr;
+    ss[tid >> 6][2] = sx;
   }
   __syncthreads();
-  if (sampled && tid < 3) {
+  if (tid < 3) {
     double t = 0.0;
     for (int w = 0; w < kWaves; ++w) t += ss[w][tid];
     a.sums[(size_t)(a.chunk_lo + blockIdx.x) * 3 + tid] = t;

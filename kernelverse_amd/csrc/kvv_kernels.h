@@ -1122,10 +1122,12 @@ __device__ __forceinline__ typename Elem<DT>::T vec_code(const uint4& q, int e) 
 // Samples of a segment whose every element is a sample (n <= max_samples, so
 // sample index == logical index): each lane finishes the values of its own
 // vectors from the stage and stores them with vector stores, no walk.  The
-// sampled sums are then the full sums; the fold takes those.
+// sampled sums take every element's fp64 products here (the full sums may
+// take phase A's packed dot form, which is only accurate to 7.2e-7).
 template <int DT, int MODE>
-__device__ __forceinline__ void dense_samples(const SegDesc& d, int64_t L0, int64_t L1, StageP stage, float* sabs,
-                                              float* srel) {
+__device__ __forceinline__ void dense_samples(const SegDesc& d, int64_t L0, int64_t L1, StageP stage, Acc& acc,
+                                              float* sabs, float* srel) {
+  using E = Elem<DT>;
   constexpr int V = VecIO<DT>::V;
   constexpr int S = V >= 4 ? 4 : V;  // floats per store
   typedef float fvec __attribute__((ext_vector_type(S)));
@@ -1145,9 +1147,16 @@ __device__ __forceinline__ void dense_samples(const SegDesc& d, int64_t L0, int6
 #pragma unroll
       for (int j = 0; j < S; ++j) {
         float fa, fr;
-        sample_pair<DT, MODE>(d, vec_code<DT>(gq, k + j), vec_code<DT>(rq, k + j), fa, fr);
+        const auto gc = vec_code<DT>(gq, k + j), rc = vec_code<DT>(rq, k + j);
+        sample_pair<DT, MODE>(d, gc, rc, fa, fr);
         xa[j] = fa;
         xr[j] = fr;
+        if (v0 + k + j < L1) {
+          const double g64 = E::f64(gc), r64 = E::f64(rc);
+          acc.s[4] = fma(g64, g64, acc.s[4]);
+          acc.s[5] = fma(r64, r64, acc.s[5]);
+          acc.s[6] = fma(g64, r64, acc.s[6]);
+        }
       }
       if (v0 + k + S <= L1) {
         *reinterpret_cast<fvec*>(pa + k) = xa;
@@ -1608,7 +1617,8 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
           }
         }
         if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, R0, full_now, stage, acc, wc);
-        if (dense && !(d.flags & kFlagInputSelect)) dense_samples<DT, MODE>(d, L0, L1, stage, a.sample_abs, a.sample_rel);
+        if (dense && !(d.flags & kFlagInputSelect))
+          dense_samples<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel);
       }
       if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, wc, near_prev);
     }

@@ -32,5 +32,8 @@ KVV_DECLARE(8)
 KVV_DECLARE(9)
 KVV_DECLARE(10)
 KVV_DECLARE(11)
+KVV_DECLARE(12)
+KVV_DECLARE(13)
+KVV_DECLARE(14)
 
 }  // namespace kvv

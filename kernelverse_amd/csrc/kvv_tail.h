@@ -43,7 +43,7 @@ struct TailArgs {
   const uint32_t* item_near;
   uint64_t* item_near_off;
   const double* item_near_sum;
-  const double* isel_sums;    // input-select segments with m < n: sampled sums per chunk (3 each)
+  const double* isel_sums;    // input-select segments: sampled sums per chunk (3 each)
 };
 
 struct ReduceLds {
@@ -308,13 +308,11 @@ __device__ inline void reduce_sums(const TailArgs& a, const SegDesc& d, int64_t 
   auto sum = [&](int i) { return L.td[i]; };
   kvv_result& o = a.res[d.out_index];
   if (tid == 0) {
-    // every element a sample: the sampled sums are the full sums; an
-    // input-select segment's sampled sums are its chunks', in chunk order
-    const int k = d.m == d.n ? 0 : 4;
-    double sg = sum(k), sr = sum(k + 1), sx = sum(k + 2);
-    if (d.m != d.n && (d.flags & kFlagInputSelect)) {
+    // the sampled sums; an input-select segment's are its chunks', in chunk order
+    double sg = sum(4), sr = sum(5), sx = sum(6);
+    if (d.flags & kFlagInputSelect) {
       sg = sr = sx = 0.0;
-      const int64_t nck = (d.m + kIselChunkSampled - 1) / kIselChunkSampled;
+      const int64_t nck = (d.m + isel_chunk_len(d) - 1) / isel_chunk_len(d);
       for (int64_t c = 0; c < nck; ++c) {
         const double* p = a.isel_sums + (size_t)(d.isel_chunk0 + c) * 3;
         sg += p[0];

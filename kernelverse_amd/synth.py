@@ -216,20 +216,42 @@ def c1_pair(device):
     return code_flip_pair_device(268_435_456, seed=1, device=device, dtype=torch.bfloat16, std=2.0, p1=0.05, p3=1e-4)
 
 
+# The 17 finite-pattern breaks of C2, by kind: (reference class, candidate value).
+C2_BREAKS = (("nan", 1.0), ("nan", 1.0), ("nan", 1.0), ("nan", 1.0),
+             ("inf", 1.0), ("inf", 1.0), ("inf", 1.0),
+             ("inf", "negated"), ("inf", "negated"), ("inf", "negated"), ("inf", "negated"),
+             ("finite", float("nan")), ("finite", float("nan")), ("finite", float("nan")),
+             ("nan", float("inf")), ("nan", float("inf")), ("nan", float("-inf")))
+
+
 def c2_pair(device, rows: int = 4096, cols: int = 32768, stride: int = 32896, seed: int = 2):
-    """C2: fp16 (rows, cols) views with row stride `stride`; ref ~ U(-60000, 60000) with 0.05% NaN and 0.05% Inf;
-    the candidate copies the reference except at 17 seeded non-finite reference positions, where it is 1.0."""
+    """C2: fp16 (rows, cols) views with row stride `stride`; ref ~ U(-60000, 60000) with 0.05% NaN and 0.05% +-Inf
+    (either sign); the candidate copies the reference except at 17 seeded positions whose class it breaks
+    (``C2_BREAKS``): NaN or +-Inf replaced by 1.0, +-Inf negated, a finite value replaced by NaN, NaN replaced by
+    +-Inf.  Every break is one finite-pattern violation."""
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     base_r = (torch.rand(rows, stride, generator=gen, device=device) * 120000.0 - 60000.0).to(torch.float16)
     u = torch.rand(rows, stride, generator=gen, device=device)
+    sign = torch.rand(rows, stride, generator=gen, device=device) < 0.5
     base_r[u < 5e-4] = float("nan")
-    base_r[(u >= 5e-4) & (u < 1e-3)] = float("inf")
-    del u
+    inf = (u >= 5e-4) & (u < 1e-3)
+    base_r[inf & sign] = float("inf")
+    base_r[inf & ~sign] = float("-inf")
+    del u, sign, inf
     base_g = base_r.clone()
-    nonfin = torch.nonzero(~torch.isfinite(base_r[:, :cols]).reshape(-1)).reshape(-1)
-    pick = nonfin[torch.randperm(nonfin.numel(), generator=gen, device=device)[:17]]
-    base_g[pick // cols, pick % cols] = 1.0
+    flat = base_r[:, :cols].reshape(-1)
+    pools = {"nan": torch.nonzero(torch.isnan(flat)).reshape(-1), "inf": torch.nonzero(torch.isinf(flat)).reshape(-1)}
+    cand = torch.randint(0, rows * cols, (4096,), generator=gen, device=device)
+    pools["finite"] = cand[torch.isfinite(flat[cand])].unique()
+    for kind in pools:
+        pools[kind] = pools[kind][torch.randperm(pools[kind].numel(), generator=gen, device=device)]
+    taken = {k: 0 for k in pools}
+    for kind, value in C2_BREAKS:
+        p = pools[kind][taken[kind]]
+        taken[kind] += 1
+        row, col = p // cols, p % cols
+        base_g[row, col] = -base_r[row, col] if value == "negated" else value
     return base_g[:, :cols], base_r[:, :cols]
 
 

@@ -49,12 +49,33 @@ TOLERANCE_POLICY = {
 
 MAX_SAMPLES = 1_000_000
 
-# torch-CPU has no isfinite for float8 tensors, so the reference verdict raises
-# NotImplementedError on float8 outputs (GCR:420).  True keeps that behaviour;
-# False evaluates the finite-pattern rule on the decoded values instead.
+# The reference's finite-pattern check (GCR:420) calls torch.isfinite, which
+# torch-CPU implements for float8_e5m2 but not for float8_e4m3fn or the fnuz
+# formats: the reference verdict raises NotImplementedError for those.  True
+# keeps that behaviour; False evaluates the finite-pattern rule on the decoded
+# values instead (the kernels decode e4m3fn and e5m2).
 FP8_REFERENCE_ERRORS = True
 
-_FP8_NAMES = {torch.float8_e4m3fn: "Float8_e4m3fn", torch.float8_e5m2: "Float8_e5m2"}
+
+def _isfinite_errors() -> Dict[Any, str]:
+    """The float8 dtypes whose torch-CPU isfinite raises, with torch's own message (probed once)."""
+    out = {}
+    for name in ("float8_e4m3fn", "float8_e5m2", "float8_e4m3fnuz", "float8_e5m2fnuz"):
+        dt = getattr(torch, name, None)
+        if dt is None:
+            continue
+        try:
+            torch.isfinite(torch.zeros(1, dtype=dt))
+        except NotImplementedError as exc:
+            out[dt] = str(exc)
+    return out
+
+
+_ISFINITE_ERRORS = _isfinite_errors()
+
+# complex inputs take the integer branch (not floating point) and torch's casts
+# to int32 and float32 keep only the real part: the kernels read that part
+_COMPLEX_REAL = {torch.complex64: torch.float32, torch.complex128: torch.float64}
 
 _DTYPE_CODES = {
     torch.float32: _lib.F32,
@@ -69,6 +90,9 @@ _DTYPE_CODES = {
     torch.int32: _lib.I32,
     torch.int64: _lib.I64,
     torch.bool: _lib.BOOL,
+    torch.uint16: _lib.U16,
+    torch.uint32: _lib.U32,
+    torch.uint64: _lib.U64,
 }
 
 
@@ -242,9 +266,9 @@ class _Job:
                 kp.flags |= _lib.FLAG_NEAR_ZERO
                 kp.near_zero_abs = float(th["near_zero_abs"])
                 kp.near_zero_bad_abs = float(th["max_near_zero_bad_abs"])
-        if ref.dtype in _FP8_NAMES and (FP8_REFERENCE_ERRORS if fp8_errors is None else fp8_errors):
-            raise NotImplementedError(f'"isfinite" not implemented for \'{_FP8_NAMES[ref.dtype]}\'')
-        if ref.dtype not in _DTYPE_CODES:
+        if ref.dtype in _ISFINITE_ERRORS and (FP8_REFERENCE_ERRORS if fp8_errors is None else fp8_errors):
+            raise NotImplementedError(_ISFINITE_ERRORS[ref.dtype])
+        if _COMPLEX_REAL.get(ref.dtype, ref.dtype) not in _DTYPE_CODES:
             raise TypeError(f"verdict does not support dtype {ref.dtype}")
         self.kpolicy = kp
         self.record = None
@@ -259,17 +283,54 @@ def _device_for(*tensors) -> torch.device:
     return torch.device("cuda", torch.cuda.current_device())
 
 
-def _kvv_tensor(t: torch.Tensor) -> _lib.KvvTensor:
+def _kvv_tensor(t: torch.Tensor, sizes=None, strides=None) -> _lib.KvvTensor:
+    """The C-ABI view of ``t`` (its own shape and strides unless given)."""
+    sizes = list(t.shape) if sizes is None else sizes
+    strides = list(t.stride()) if strides is None else strides
+    if len(sizes) > _lib.MAX_DIMS:
+        raise _lib.KvvLibraryError(f"tensors of more than {_lib.MAX_DIMS} dims must be coalesced first")
     kt = _lib.KvvTensor()
     kt.data = t.data_ptr() if t.numel() else 0
     kt.dtype = _DTYPE_CODES[t.dtype]
-    if t.dim() > _lib.MAX_DIMS:
-        raise _lib.KvvLibraryError(f"tensors of more than {_lib.MAX_DIMS} dims are not supported")
-    kt.ndim = t.dim()
-    for i, (s, st) in enumerate(zip(t.shape, t.stride())):
+    kt.ndim = len(sizes)
+    for i, (s, st) in enumerate(zip(sizes, strides)):
         kt.sizes[i] = s
         kt.strides[i] = st
     return kt
+
+
+def _device_views(g: torch.Tensor, r: torch.Tensor):
+    """C-ABI views of a same-shape pair on the device.
+
+    Complex tensors are read through their real part (see ``_COMPLEX_REAL``).
+    A pair of more than eight dims is coalesced jointly: size-1 dims dropped,
+    a dim merged into its outer neighbour where both tensors' strides chain.
+    The row-major logical order, and so every reported index, is unchanged.
+    Only when that still leaves more than eight dims are both tensors copied
+    to contiguous memory on the device.  Returns (gen view, ref view, tensors
+    to keep alive until the call has been issued).
+    """
+    if g.dtype in _COMPLEX_REAL:
+        g, r = torch.view_as_real(g.resolve_conj())[..., 0], torch.view_as_real(r.resolve_conj())[..., 0]
+    if g.dim() <= _lib.MAX_DIMS:
+        return _kvv_tensor(g), _kvv_tensor(r), (g, r)
+    sz, gs, rs = [], [], []
+    for s, a, b in zip(g.shape, g.stride(), r.stride()):
+        if s == 1:
+            continue
+        if sz and gs[-1] == a * s and rs[-1] == b * s:
+            sz[-1] *= s
+            gs[-1], rs[-1] = a, b
+        else:
+            sz.append(s)
+            gs.append(a)
+            rs.append(b)
+    if g.numel() == 0:
+        sz, gs, rs = [0], [1], [1]
+    if len(sz) > _lib.MAX_DIMS:
+        g, r = g.contiguous(), r.contiguous()
+        sz, gs, rs = [g.numel()], [1], [1]
+    return _kvv_tensor(g, sz, gs), _kvv_tensor(r, sz, rs), (g, r)
 
 
 def _run_jobs(jobs: List[_Job]) -> None:
@@ -283,9 +344,10 @@ def _run_jobs(jobs: List[_Job]) -> None:
     for j in jobs:
         g = j.gen if j.gen.device == dev else j.gen.to(dev)
         r = j.ref if j.ref.device == dev else j.ref.to(dev)
-        keep += [g, r]
-        gts.append(_kvv_tensor(g))
-        rts.append(_kvv_tensor(r))
+        gt, rt, held = _device_views(g, r)
+        keep += [g, r, *held]
+        gts.append(gt)
+        rts.append(rt)
     n = len(jobs)
     rec_size = ctypes.sizeof(_lib.KvvResult)
     with torch.cuda.device(dev):

@@ -12,8 +12,9 @@ verdict of KernelVerse ``runner/generated_correctness_runner.py`` (GCR):
 * ``dtype_policy``            GCR:305-328 (+ ``TOLERANCE_POLICY`` GCR:39-44)
 * ``format_number``           GCR:331-335
 * ``sample_flat_values``      GCR:338-348
-* ``cosine_similarity_meta``  GCR:351-372
-* ``norm_ratio_meta``         GCR:375-393
+* ``cosine_similarity_meta``  GCR:351-372 (``cosine_similarity_value``: the same
+  before its final rounding)
+* ``norm_ratio_meta``         GCR:375-393 (``norm_ratio_value`` likewise)
 * ``p99_meta``                GCR:396-402
 * ``mean_meta``               GCR:405-411
 * ``finite_pattern_pass``     GCR:414-437
@@ -145,8 +146,9 @@ def sample_flat_values(values: torch.Tensor, max_samples: int = MAX_SAMPLES) -> 
     return values[idx]
 
 
-def cosine_similarity_meta(generated, reference, max_samples: int = MAX_SAMPLES) -> Optional[float]:
-    """GCR:351-372."""
+def cosine_similarity_value(generated, reference, max_samples: int = MAX_SAMPLES) -> Optional[float]:
+    """GCR:351-371 before the final ``round(., 4)``: the clamped fp64 cosine of the
+    strided samples, or the exact 1.0 / 0.0 of the zero-norm conventions."""
     if generated.numel() == 0 or not torch.is_floating_point(reference):
         return None
     g = sample_flat_values(generated, max_samples).to(torch.float64)
@@ -160,11 +162,18 @@ def cosine_similarity_meta(generated, reference, max_samples: int = MAX_SAMPLES)
     if g_zero or r_zero:
         return 0.0
     cos = torch.clamp(torch.dot(g, r) / (gn * rn), -1.0, 1.0)
-    return round(float(cos.item()), 4)
+    return float(cos.item())
 
 
-def norm_ratio_meta(generated, reference, max_samples: int = MAX_SAMPLES) -> Optional[float]:
-    """GCR:375-393."""
+def cosine_similarity_meta(generated, reference, max_samples: int = MAX_SAMPLES) -> Optional[float]:
+    """GCR:351-372 (the conventions' exact 1.0 / 0.0 are unchanged by the rounding)."""
+    v = cosine_similarity_value(generated, reference, max_samples)
+    return None if v is None else round(v, 4)
+
+
+def norm_ratio_value(generated, reference, max_samples: int = MAX_SAMPLES) -> Optional[float]:
+    """GCR:375-392 before the final ``round(., 4)``: ||g|| / ||r|| of the strided
+    samples in fp64, or the exact 1.0 / 0.0 / inf of the zero-norm conventions."""
     if generated.numel() == 0 or not torch.is_floating_point(reference):
         return None
     g = sample_flat_values(generated, max_samples).to(torch.float64)
@@ -179,7 +188,13 @@ def norm_ratio_meta(generated, reference, max_samples: int = MAX_SAMPLES) -> Opt
         return 0.0
     if r_zero:
         return float("inf")
-    return round(float((gn / rn).item()), 4)
+    return float((gn / rn).item())
+
+
+def norm_ratio_meta(generated, reference, max_samples: int = MAX_SAMPLES) -> Optional[float]:
+    """GCR:375-393."""
+    v = norm_ratio_value(generated, reference, max_samples)
+    return None if v is None else round(v, 4)
 
 
 def p99_meta(values, max_samples: int = MAX_SAMPLES) -> Optional[float]:

@@ -172,6 +172,57 @@ def tensor_cases():
     cases.append(("fp32_matching_nans", both_nan, both_nan.clone(), None, {"category": "gemm", "op_name": "x"}))
     f8g, f8r = synth.fp8_pair(1024, seed=19, p=0.05)
     cases.append(("fp8_e4m3fn_reference_raises", f8g, f8r, None, None))
+    # float8_e5m2 has a torch-CPU isfinite, so the reference returns a verdict for it
+    e5g, e5r = synth.code_flip_pair(2048, seed=41, dtype=torch.float8_e5m2, std=4.0, p1=0.05, p3=0.01)
+    cases.append(("fp8_e5m2_flips_default", e5g, e5r, None, None))
+    cases.append(("fp8_e5m2_flips_cosine", e5g, e5r, None, {"category": "attention", "op_name": "x"}))
+    cases.append(("fp8_e5m2_flips_tolerant", e5g, e5r, {"FLOAT8_E5M2": {"rtol": 0.25, "atol": 0.1}},
+                  {"category": "gemm", "op_name": "x"}))
+    e5codes = torch.arange(256, dtype=torch.int16).to(torch.uint8)
+    e5gc = e5codes.clone()
+    e5gc[0x7C] = 0xFC      # +inf -> -inf
+    e5gc[0x7E] = 0x3C      # NaN -> 1.0
+    e5gc[0x3C] = 0x7D      # 1.0 -> NaN
+    e5gc[0xFC] = 0xFE      # -inf -> NaN
+    e5gc[0x10:0x18] += 1   # finite one-code steps
+    cases.append(("fp8_e5m2_nonfinite_codes", e5gc.view(torch.float8_e5m2), e5codes.view(torch.float8_e5m2),
+                  None, {"category": "gemm", "op_name": "x"}))
+    fz = torch.tensor([0.5, 1.0, -2.0, 3.0])
+    cases.append(("fp8_e4m3fnuz_reference_raises", fz.to(torch.float8_e4m3fnuz), (fz * 1.5).to(torch.float8_e4m3fnuz),
+                  None, None))
+    cases.append(("fp8_e5m2fnuz_reference_raises", fz.to(torch.float8_e5m2fnuz), (fz * 1.5).to(torch.float8_e5m2fnuz),
+                  None, None))
+    # unsigned and complex integer-branch inputs: int32 casts wrap, rel_diff divides by the float32 value
+    # (unsigned tensors built in numpy: torch-CPU has no arithmetic kernels for them)
+    u16 = (np.arange(0, 1024, dtype=np.int64) * 64 + 3).astype(np.uint16)
+    u16g = u16.copy()
+    u16g[::29] += 2
+    cases.append(("uint16_default", torch.from_numpy(u16g), torch.from_numpy(u16), None, None))
+    cases.append(("uint16_max_abs_diff", torch.from_numpy(u16g), torch.from_numpy(u16), {"UINT16": {"max_abs_diff": 1}},
+                  None))
+    u32 = (np.arange(0, 1024, dtype=np.int64) * 4194301 + 17).astype(np.uint32)
+    u32g = u32.copy()
+    u32g[::31] += 5
+    u32g[7] = 0
+    u32[7] = 2**31 + 9
+    cases.append(("uint32_wrap", torch.from_numpy(u32g), torch.from_numpy(u32), None, None))
+    u64 = np.arange(0, 512, dtype=np.uint64) * np.uint64(2**54 + 77)
+    u64g = u64.copy()
+    u64g[3::50] += np.uint64(2**32)
+    u64g[11] += np.uint64(9)
+    cases.append(("uint64_low32_compare", torch.from_numpy(u64g), torch.from_numpy(u64), {"UINT64": {"max_abs_diff": 2}},
+                  None))
+    cre = torch.from_numpy(np.linspace(-300.0, 300.0, 600).astype(np.float32))
+    cplx_r = torch.complex(cre, cre * 0.5)
+    cplx_g = torch.complex(cre + (torch.arange(600) % 7 == 0).float() * 2.5, cre * -0.25)
+    cases.append(("complex64_real_part", cplx_g, cplx_r, None, None))
+    # more than eight dimensions: one contiguous, one permuted view
+    hg, hr = synth.fp32_noise_pair(2048, seed=42, noise=1e-4, frac=0.05)
+    cases.append(("fp32_nine_dims", hg[:512].reshape((2,) * 9), hr[:512].reshape((2,) * 9),
+                  {"FP32": {"rtol": 1e-5, "atol": 1e-5}}, {"category": "gemm", "op_name": "x"}))
+    perm = (9, 0, 8, 1, 7, 2, 6, 3, 5, 4)
+    cases.append(("fp32_ten_dims_permuted", hg[:1024].reshape((2,) * 10).permute(perm),
+                  hr[:1024].reshape((2,) * 10).permute(perm), {"FP32": {"rtol": 1e-5, "atol": 1e-5}}, None))
     return cases
 
 
@@ -197,6 +248,16 @@ def recipe_cases():
         ("bf16_sampled_near_zero_3m", {"fn": "code_flip_pair", "kwargs": {"n": 3_000_000, "seed": 32, "std": 0.5,
                                                                           "p1": 0.05, "p3": 0.01}},
          {"BF16": {"rtol": 1e-3, "atol": 1e-4}}, {"category": "gemm", "op_name": "x"}),
+        # the C0 benchmark configuration at its own size, under each policy kind
+        ("c0_fp32_1m_strict", {"fn": "fp32_noise_pair", "kwargs": {"n": 1_048_576, "seed": 0}},
+         {"FP32": {"rtol": 1e-5, "atol": 1e-5}}, None),
+        ("c0_fp32_1m_tolerant", {"fn": "fp32_noise_pair", "kwargs": {"n": 1_048_576, "seed": 0}},
+         {"FP32": {"rtol": 1e-5, "atol": 1e-5}}, {"category": "gemm", "op_name": "x"}),
+        ("c0_fp32_1m_cosine", {"fn": "fp32_noise_pair", "kwargs": {"n": 1_048_576, "seed": 0}},
+         {"FP32": {"rtol": 1e-5, "atol": 1e-5}}, {"category": "attention", "op_name": "x"}),
+        # a C1-like bf16 pair under the tolerant policy (near-zero diagnostics over a sampled compaction)
+        ("bf16_c1_model_tolerant_4m", {"fn": "code_flip_pair", "kwargs": {"n": 4_194_304, "seed": 33}},
+         {"BF16": {"rtol": 1.6e-2, "atol": 1e-2}}, {"category": "gemm", "op_name": "x"}),
     ]
 
 
@@ -303,11 +364,12 @@ def main(reference_root: str) -> None:
                              "random_correctness": {"max_failed_case_rate": 0.03},
                              "criteria": gcr._correctness_criteria(gcr.TOLERANCE_POLICY, pol, mode,
                                                                    {"max_failed_case_rate": 0.03}, shape_mode)})
-    # intern the (large, highly repeated) resolved threshold tables and trim configs to the keys the verdict reads
+    # intern the (large, highly repeated) resolved threshold tables and trim configs to the keys the verdict reads;
+    # a table's key is its JSON text in the reference's own key order, so the order survives the round trip
     tables = {}
 
     def intern(pol):
-        key = json.dumps(pol["thresholds"], sort_keys=True)
+        key = json.dumps(pol["thresholds"])
         tables.setdefault(key, len(tables))
         out = dict(pol)
         out["thresholds"] = {"__table__": tables[key]}
@@ -327,7 +389,7 @@ def main(reference_root: str) -> None:
         entry["criteria"]["metric_fallback"] = dict(entry["criteria"]["metric_fallback"])
         if "thresholds" in entry["criteria"]["metric_fallback"]:
             th = entry["criteria"]["metric_fallback"]["thresholds"]
-            key = json.dumps(th, sort_keys=True)
+            key = json.dumps(th)
             tables.setdefault(key, len(tables))
             entry["criteria"]["metric_fallback"]["thresholds"] = {"__table__": tables[key]}
     table_list = [json.loads(k) for k, _ in sorted(tables.items(), key=lambda kv: kv[1])]

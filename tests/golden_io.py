@@ -15,7 +15,8 @@ GOLDEN = Path(__file__).resolve().parent / "golden"
 
 _DTYPES = {str(d).replace("torch.", ""): d for d in (
     torch.float32, torch.float16, torch.bfloat16, torch.float64, torch.int8, torch.uint8, torch.int16,
-    torch.int32, torch.int64, torch.bool, torch.float8_e4m3fn, torch.float8_e5m2)}
+    torch.int32, torch.int64, torch.bool, torch.float8_e4m3fn, torch.float8_e5m2, torch.float8_e4m3fnuz,
+    torch.float8_e5m2fnuz, torch.uint16, torch.uint32, torch.uint64, torch.complex64)}
 
 
 def _storages() -> Dict[str, bytes]:

@@ -69,7 +69,7 @@ def test_cpu_inputs_are_copied_to_the_device(kv):
     ok, details, meta = kv._compare_tensors(g, r, "output")
     ok2, details2, meta2 = tv.compare_tensors(g, r, "output")
     assert (ok, details) == (ok2, details2)
-    assert not meta_problems(meta, meta2)
+    assert not meta_problems(meta, meta2, g, r)
 
 
 # ---------------------------------------------------------------- extension record
@@ -202,13 +202,13 @@ def test_extension_record_matches_oracle(kv, pair):
 def test_meta_matches_oracle(kv, pair, policy, max_samples):
     from kernelverse_amd.correctness_policy import resolve_correctness_policy
     name, g, r, tol = pair
-    if g.dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
-        pytest.skip("the reference raises on float8 (covered by the fixture test)")
+    if g.dtype == torch.float8_e4m3fn:
+        pytest.skip("the reference raises on float8_e4m3fn (torch-CPU has no isfinite for it; fixture test)")
     pol = resolve_correctness_policy({"category": policy["category"], "op_name": "x"}) if policy else None
     _say("meta", name, policy, max_samples)
     want = tv.compare_tensors(g, r, "output", tol, pol, max_samples=max_samples)
     got = kv._compare_tensors(g.to(DEV), r.to(DEV), "output", tol, pol, max_samples=max_samples)
-    probs = meta_problems(got[2], want[2])
+    probs = meta_problems(got[2], want[2], g, r, max_samples)
     assert not probs, probs
     assert got[0] == want[0]
     assert got[1] == want[1]
@@ -233,8 +233,8 @@ def test_batch_matches_single_and_oracle(kv):
     got = kv._compare_outputs(gen, ref)
     want = tv.compare_outputs(tuple(p[0] for p in pairs[:10]), tuple(p[1] for p in pairs[:10]))
     assert got[0] == want[0] and got[1] == want[1]
-    for a, b in zip(got[2], want[2]):
-        assert not meta_problems(a, b)
+    for p, a, b in zip(pairs[:10], got[2], want[2]):
+        assert not meta_problems(a, b, p[0], p[1])
 
 
 def test_many_group_batch_selects_each_group_in_one_block(kv):
@@ -266,12 +266,6 @@ def test_many_group_batch_selects_each_group_in_one_block(kv):
             want = tv.p99_meta(vals)
             if not same_value(float(rec[k]), float(want)):
                 probs.append(f"{k}: device {rec[k]!r} != oracle {want!r}")
-        # the full sums serve as the sampled sums here: unrounded they agree to 1e-6, so
-        # after round(., 4) they match or sit one step apart at a rounding boundary
-        want_cos = tv.cosine_similarity_meta(g, r)
-        got_cos = round(rec["sample_cosine"], 4)
-        if want_cos is not None and not same_value(got_cos, want_cos) and not abs(got_cos - want_cos) <= 1e-4 + 1e-12:
-            probs.append(f"sample_cosine: device {rec['sample_cosine']!r} vs oracle {want_cos!r}")
         assert not probs, (tuple(g.shape), g.dtype, probs)
     # the tolerant policy adds the near-zero sample array to every group
     pol = {"name": "tolerant", **__import__("kernelverse_amd.correctness_policy", fromlist=["x"]).resolve_correctness_policy(
@@ -282,8 +276,8 @@ def test_many_group_batch_selects_each_group_in_one_block(kv):
     want = tv.compare_outputs(tuple(p[0] for p in half), tuple(p[1] for p in half), tolerance_policy=tol,
                               correctness_policy=pol)
     assert got[0] == want[0] and got[1] == want[1]
-    for a, b in zip(got[2], want[2]):
-        probs = meta_problems(a, b)
+    for p, a, b in zip(half, got[2], want[2]):
+        probs = meta_problems(a, b, p[0], p[1])
         assert not probs, probs
 
 

@@ -71,7 +71,7 @@ def _check_batch(kv, cases, tol, max_samples, tag):
     _say("batch", tag, len(cases), "pairs", "max_samples", max_samples, "tol", tol)
     recs = kv.verdict_records(dev, tolerance_policy=tol, max_samples=max_samples)
     for i, ((g, r), rec) in enumerate(zip(cpu, recs)):
-        probs = record_vs_oracle(rec, g, r, tol)
+        probs = record_vs_oracle(rec, g, r, tol, max_samples)
         if g.numel():
             abs_d, rel_d, _, _ = tv.mismatch_parts(g, r, tol)
             for k, vals in (("p99_abs", abs_d), ("p99_rel", rel_d)):
@@ -88,8 +88,8 @@ def _check_batch(kv, cases, tol, max_samples, tag):
                               correctness_policy=pol, max_samples=max_samples)
     assert got[0] == want[0] and got[1] == want[1], tag
     assert len(got[2]) == len(want[2])
-    for a, b in zip(got[2], want[2]):
-        probs = meta_problems(a, b)
+    for i, a, b in zip(keep, got[2], want[2]):
+        probs = meta_problems(a, b, cpu[i][0], cpu[i][1], max_samples)
         assert not probs, (tag, probs)
 
 

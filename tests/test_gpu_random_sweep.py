@@ -153,14 +153,14 @@ def test_random_case_matches_oracle(kv, seed):
     _say("sweep", seed, dtype, tuple(gd.shape), tuple(gd.stride()), gd.storage_offset(), tol, max_samples)
     if g.numel() > 0:
         rec = kv.verdict_record(gd, rd, tolerance_policy=tol, max_samples=max_samples)
-        probs = record_vs_oracle(rec, g, r, tol)
+        probs = record_vs_oracle(rec, g, r, tol, max_samples)
         assert not probs, probs
     if dtype in FP8:
         return  # the reference raises on float8 metas (pinned by the fixtures)
     pol = resolve_correctness_policy({"category": ["gemm", "attention", "activation"][seed % 3], "op_name": "x"})
     want = tv.compare_tensors(g, r, "output", tol, pol, max_samples=max_samples)
     got = kv._compare_tensors(gd, rd, "output", tol, pol, max_samples=max_samples)
-    probs = meta_problems(got[2], want[2])
+    probs = meta_problems(got[2], want[2], g, r, max_samples)
     assert not probs, probs
     assert got[0] == want[0]
     assert got[1] == want[1]
