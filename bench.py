@@ -91,7 +91,7 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(pairs, budget_s: float = 12.0):
+def cpu_baseline(pairs, policy=None, budget_s: float = 12.0):
     """Torch-CPU oracle verdicts (the port, oracle/torch_verdict.py) on a bounded leading sample of the workload:
     the first 64 Mi elements of a single pair, or the leading pairs of a batch up to 64 Mi elements, repeated
     for about budget_s seconds of CPU work (at least 3 runs)."""
@@ -114,8 +114,9 @@ def cpu_baseline(pairs, budget_s: float = 12.0):
 
     def run_all():
         for g, r, tol in host:
-            # fp8: the reference raises (no isfinite for float8); the port's decode path is what the GPU computes
-            tv.compare_tensors(g, r, "output", tol, fp8_decode=g.dtype in (torch.float8_e4m3fn, torch.float8_e5m2))
+            # float8_e4m3fn: the reference raises (torch-CPU has no isfinite for it); the port's decode path is
+            # what the GPU computes
+            tv.compare_tensors(g, r, "output", tol, policy, fp8_decode=g.dtype == torch.float8_e4m3fn)
 
     run_all()  # warm-up
     times = []
@@ -245,6 +246,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c1")
+    ap.add_argument("--policy", default="strict", choices=("strict", "tolerant", "cosine"),
+                    help="correctness policy of the verdict (the category default of gemm for tolerant, attention "
+                         "for cosine; CP:14-88): tolerant adds the near-zero diagnostics of fp16/bf16 pairs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time a plain 512 MiB device copy instead (the reference kernel for scaling "
@@ -280,7 +284,10 @@ def main():
         g, r, tol, desc, dlabel = make_workload(args.config, dev)
         pairs = [(g, r, tol)]
     torch.cuda.synchronize()
-    jobs = [verdict._Job(g, r, "output", tol, None, verdict.MAX_SAMPLES, fp8_errors=False) for g, r, tol in pairs]
+    from kernelverse_amd.correctness_policy import resolve_correctness_policy
+    category = {"strict": "activation", "tolerant": "gemm", "cosine": "attention"}[args.policy]
+    policy = resolve_correctness_policy({"category": category, "op_name": "bench"})
+    jobs = [verdict._Job(g, r, "output", tol, policy, verdict.MAX_SAMPLES, fp8_errors=False) for g, r, tol in pairs]
     n_pairs = len(jobs)
     gts = [verdict._kvv_tensor(g) for g, _, _ in pairs]
     rts = [verdict._kvv_tensor(r) for _, r, _ in pairs]
@@ -391,7 +398,7 @@ def main():
         "dtype": dlabel,
         "data": "synthetic (seeded, generated on the device)",
         "config": {"workload": desc, "config_id": args.config, "pairs": n_pairs, "numel": n, "bytes_read": bytes_read,
-                   "correctness_policy": "strict"},
+                   "correctness_policy": args.policy},
         "roofline": {
             "bound": "hbm",
             "kernel": ("kvv::scan_kernel (main pass)" if n_pairs == 1 else "whole kvv_verdict_batch call"),
@@ -410,7 +417,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(pairs)
+        result["cpu_baseline"] = cpu_baseline(pairs, policy)
     print(json.dumps(result), flush=True)
 
 

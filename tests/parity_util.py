@@ -56,10 +56,13 @@ def record_vs_oracle(rec: dict, gen_cpu, ref_cpu, tolerance_policy=None, max_sam
 # about 1e-15; the check is 1e-12 relative (with a 1e-15 floor for cosines near
 # zero), far inside the declared 1e-6.  After round(., 4) the metas must then be
 # identical, except where the oracle's unrounded value lies within 1e-9 of a
-# rounding boundary (x.xxxx5), where either neighbour is accepted.
+# rounding boundary (x.xxxx5), where either neighbour is accepted, and where the
+# magnitude is so large (>= 1e11, fp64 spacing above 1e-5) that round(., 4)
+# keeps every digit, so the meta shows the unrounded value (1e-12 relative).
 UNROUNDED_RTOL = 1e-12
 UNROUNDED_FLOOR = 1e-15
 BOUNDARY_EPS = 1e-9
+ROUNDING_IDENTITY = 1e11
 SAMPLED_SUM_KEYS = ("cosine_similarity", "norm_ratio")
 
 
@@ -92,7 +95,11 @@ def rounded_sampled_ok(got, want, unrounded) -> bool:
     """A device meta value against the reference's: equal, or one step apart at a rounding boundary."""
     if same_value(got, want):
         return True
-    if unrounded is None or not isinstance(got, float) or not isinstance(want, float):
+    if not isinstance(got, float) or not isinstance(want, float):
+        return False
+    if math.isfinite(want) and abs(want) >= ROUNDING_IDENTITY and unrounded_close(got, want):
+        return True
+    if unrounded is None:
         return False
     return near_rounding_boundary(unrounded) and abs(got - want) <= 1e-4 + 1e-12
 
