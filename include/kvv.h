@@ -164,6 +164,19 @@ KVV_API int kvv_verdict_timed(const kvv_tensor* gen, const kvv_tensor* ref, cons
                               kvv_result* out, void* workspace, size_t workspace_bytes, void* stream,
                               void* main_begin, void* main_end);
 
+/* kvv_verdict without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The workspace is a 32 MiB array in the
+ * library's code object, one per GPU, held until the process ends; a verdict
+ * whose workspace (kvv_workspace_size) exceeds it fails with
+ * KVV_E_WORKSPACE and leaves the stream untouched.  Calls on one GPU share
+ * that array: calls that overlap on one GPU (other streams, other threads)
+ * race, so the caller orders them.  The kernels clear what must start at
+ * zero; the array keeps the last call's contents. */
+KVV_API int kvv_verdict_noalloc(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy,
+                                kvv_result* out, void* stream);
+
 /* Workspace bytes kvv_verdict_batch needs. */
 KVV_API int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs,
                              const kvv_policy* policies, size_t* bytes);

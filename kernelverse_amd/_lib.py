@@ -108,7 +108,10 @@ class KvvResult(ctypes.Structure):
 
 
 EXPORTED = ("kvv_abi_version", "kvv_last_error", "kvv_workspace_size", "kvv_verdict", "kvv_verdict_timed",
-            "kvv_batch_workspace_size", "kvv_verdict_batch")
+            "kvv_verdict_noalloc", "kvv_batch_workspace_size", "kvv_verdict_batch")
+
+# the fixed workspace of kvv_verdict_noalloc (bytes)
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _lib = None
 
@@ -137,6 +140,9 @@ def load() -> ctypes.CDLL:
     lib.kvv_verdict_timed.restype = c_int32
     lib.kvv_verdict_timed.argtypes = [POINTER(KvvTensor), POINTER(KvvTensor), POINTER(KvvPolicy), c_void_p, c_void_p,
                                       c_size_t, c_void_p, c_void_p, c_void_p]
+    lib.kvv_verdict_noalloc.restype = c_int32
+    lib.kvv_verdict_noalloc.argtypes = [POINTER(KvvTensor), POINTER(KvvTensor), POINTER(KvvPolicy), c_void_p,
+                                        c_void_p]
     lib.kvv_batch_workspace_size.restype = c_int32
     lib.kvv_batch_workspace_size.argtypes = [c_int32, POINTER(KvvTensor), POINTER(KvvTensor), POINTER(KvvPolicy),
                                              POINTER(c_size_t)]

@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -522,6 +523,35 @@ size_t single_workspace_bytes(const SegDesc& d) {
       .total;
 }
 
+// ------------------------------------------------------------ no-alloc entry
+// kvv_verdict_noalloc's workspace: a fixed device array in the code object, so
+// the call needs no allocation.  Each GPU holds its own copy from the library's
+// first use until the process ends.  In host code `scratch` only names the
+// symbol: its device address, per device, comes from hipGetSymbolAddress.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxScratchDevices] = {};
+
+// The current device's scratch address, looked up once per device.
+int scratch_address(void** p) {
+  int dev = 0;
+  KVV_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(KVV_E_UNSUPPORTED, "device ordinal " + std::to_string(dev) + " beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* q = nullptr;
+    KVV_HIP(hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)));
+    if (!q) return fail(KVV_E_HIP, "hipGetSymbolAddress(scratch) gave a null address");
+    g_scratch[dev] = q;
+  }
+  *p = g_scratch[dev];
+  return KVV_OK;
+}
+
 // ------------------------------------------------------------ batch
 struct BatchPlan {
   std::vector<SegDesc> table;   // sorted by (dtype, mode, kind) group, then input order
@@ -762,6 +792,23 @@ int kvv_verdict_timed(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_po
   if (rc) return rc;
   return kvv::run_single(d, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
                          static_cast<hipEvent_t>(main_begin), static_cast<hipEvent_t>(main_end));
+}
+
+int kvv_verdict_noalloc(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy, kvv_result* out,
+                        void* stream) {
+  kvv::SegDesc d;
+  int rc = kvv::plan_single(gen, ref, policy, d);
+  if (rc) return rc;
+  const size_t need = kvv::single_workspace_bytes(d);
+  if (need > kvv::kScratchBytes)
+    return kvv::fail(KVV_E_WORKSPACE, "this verdict needs " + std::to_string(need) +
+                                          " bytes of workspace; the no-alloc entry point holds " +
+                                          std::to_string(kvv::kScratchBytes) +
+                                          " (lower max_samples, or call kvv_verdict with a workspace)");
+  void* ws = nullptr;
+  rc = kvv::scratch_address(&ws);
+  if (rc) return rc;
+  return kvv::run_single(d, out, ws, kvv::kScratchBytes, static_cast<hipStream_t>(stream));
 }
 
 int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs,

@@ -121,3 +121,17 @@ def test_many_group_batch_reserves_input_select_state():
     state = count * 16_640
     lists = 256 * (-(-count * 4 // 256) + -(-count * 8 // 256) + -(-count * 24 // 256))  # one chunk per pair
     assert a.value - b.value == state + lists
+
+
+def test_noalloc_rejects_beyond_its_scratch_without_a_device():
+    """kvv_verdict_noalloc plans first and refuses a verdict whose workspace exceeds its fixed
+    scratch array before touching the device (no device here: nothing may be launched)."""
+    lib = _lib.load()
+    n = 1 << 23  # 8 Mi bf16 samples of abs and rel: 64 MiB of sample arrays
+    t = _tensor((n,), (1,), _lib.BF16)
+    size = ctypes.c_size_t()
+    assert lib.kvv_workspace_size(t, t, _policy(max_samples=n), ctypes.byref(size)) == 0
+    assert size.value > _lib.NOALLOC_SCRATCH_BYTES
+    out = ctypes.create_string_buffer(ctypes.sizeof(_lib.KvvResult))
+    assert lib.kvv_verdict_noalloc(t, t, _policy(max_samples=n), out, None) == -2
+    assert f"holds {_lib.NOALLOC_SCRATCH_BYTES}".encode() in lib.kvv_last_error()
