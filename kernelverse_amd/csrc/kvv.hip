@@ -256,8 +256,8 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
 // ------------------------------------------------------------ workspace
 struct WsLayout {
   int64_t run_stride;
-  size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample, table,
-      chunk_seg, isel_state, isel_seg, isel_chunk, isel_sums, total;
+  size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample,
+      near_cm, table, chunk_seg, isel_state, isel_seg, isel_chunk, isel_sums, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -294,6 +294,7 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
     L.item_near_off = take((size_t)items * 8);
     L.item_near_sum = take((size_t)items * 8);
     L.near_sample = take((size_t)samples * 4);
+    L.near_cm = take((size_t)nseg * 16);
   }
   if (batch) {
     L.table = take((size_t)nseg * sizeof(SegDesc));
@@ -355,6 +356,8 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   t.item_near_off = near ? at<uint64_t>(ws, L.item_near_off) : nullptr;
   t.item_near_sum = near ? at<double>(ws, L.item_near_sum) : nullptr;
   t.isel_sums = at<double>(ws, L.isel_sums);
+  t.near_cm = near ? at<uint64_t>(ws, L.near_cm) : nullptr;
+  const bool batch = dtable != nullptr;
   auto launch = [&](int reduce_blocks, int level, int arr_lo, int narr) -> int {
     TailArgs x = t;
     x.reduce_blocks = reduce_blocks;
@@ -363,11 +366,15 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
     x.narr = narr;
     const int64_t grid = reduce_blocks + (total_chunks > 0 ? (int64_t)narr * total_chunks : 0);
     if (grid == 0) return KVV_OK;
-    if (level == 0) hipLaunchKernelGGL(tail_kernel<0>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
-    else if (level == 1) hipLaunchKernelGGL(tail_kernel<1>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
-    else if (level == 2) hipLaunchKernelGGL(tail_kernel<2>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
-    else if (level == 3) hipLaunchKernelGGL(tail_kernel<3>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
-    else hipLaunchKernelGGL(tail_kernel<4>, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
+    void (*fn)(TailArgs) = nullptr;
+    switch (level) {
+      case 0: fn = batch ? tail_kernel<0, true> : tail_kernel<0, false>; break;
+      case 1: fn = batch ? tail_kernel<1, true> : tail_kernel<1, false>; break;
+      case 2: fn = batch ? tail_kernel<2, true> : tail_kernel<2, false>; break;
+      case 3: fn = batch ? tail_kernel<3, true> : tail_kernel<3, false>; break;
+      default: fn = tail_kernel<4, true>; break;  // many-group launches are batches
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
     KVV_HIP(hipGetLastError());
     return KVV_OK;
   };
@@ -384,6 +391,8 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
       if (seg0) na.seg0 = *seg0;
       na.table = dtable ? dtable + nl.seg_lo : nullptr;
       na.nseg = nl.nseg;
+      na.seg_lo = nl.seg_lo;
+      na.near_cm = at<uint64_t>(ws, L.near_cm);
       na.item_lo = nl.item_lo;
       na.items = nl.items;
       na.res = out;

@@ -29,6 +29,7 @@ namespace kvv {
 
 constexpr int kUnroll = 4;            // 16-byte vectors per thread per item
 constexpr int kSelChunk = 8192;       // sample values per select round of a large group
+constexpr int kStreamChunk = 8192;    // values per round when one block streams a whole group
 constexpr int kMaxSelRounds = 4;      // rounds per select block (many samples in a launch: fewer, fuller blocks)
 constexpr int kMaxRounds = 4;         // dispatch rounds of a single-segment scan grid (blocks per CU)
 constexpr int kSmall = 8192;          // groups of at most this many samples are selected by one block
@@ -1659,7 +1660,8 @@ struct NearArgs {
   SegDesc seg0;
   const SegDesc* table;
   int32_t nseg;
-  int32_t pad;
+  int32_t seg_lo;          // absolute index of table[0] (near_cm is indexed by absolute segment)
+  const uint64_t* near_cm; // near-zero count and sample count per segment, from the fold
   int64_t item_lo, items;
   const kvv_result* res;
   const uint64_t* item_near_off;
@@ -1690,8 +1692,8 @@ __global__ __launch_bounds__(kBlock) void near_kernel(NearArgs a) {
     if (tid == 0) a.item_near_sum[item] = 0.0;
     return;
   }
-  const uint64_t c = (uint64_t)a.res[d.out_index].near_zero_count;
-  const uint64_t mm = (uint64_t)a.res[d.out_index].near_zero_sample_count;
+  const uint64_t c = a.near_cm[2 * (a.seg_lo + s)];
+  const uint64_t mm = a.near_cm[2 * (a.seg_lo + s) + 1];
   const uint64_t off = a.item_near_off[item];
   const int64_t L0 = (item - d.item_begin) * (int64_t)d.item_elems;
   const int64_t L1 = L0 + d.item_elems < d.n ? L0 + d.item_elems : d.n;

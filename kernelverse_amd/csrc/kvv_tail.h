@@ -44,6 +44,7 @@ struct TailArgs {
   uint64_t* item_near_off;
   const double* item_near_sum;
   const double* isel_sums;    // input-select segments: sampled sums per chunk (3 each)
+  uint64_t* near_cm;          // near-zero count and sample count per segment (device copies of the fold's)
 };
 
 struct ReduceLds {
@@ -129,7 +130,7 @@ __device__ __forceinline__ uint64_t fold_u32(const uint32_t* col, int64_t j0, in
 // Count columns [F0, F0 + F) of the segment, folded by one block; the outputs
 // of those counts are written by the same block.
 template <int F0, int F>
-__device__ inline void reduce_counts(const TailArgs& a, const SegDesc& d, int64_t nruns, ReduceLds& L) {
+__device__ inline void reduce_counts(const TailArgs& a, const SegDesc& d, int seg, int64_t nruns, ReduceLds& L) {
   constexpr int P = kBlock / F;
   int f, p;
   int64_t j0, j1;
@@ -175,6 +176,11 @@ __device__ inline void reduce_counts(const TailArgs& a, const SegDesc& d, int64_
         o.near_zero_bad_count = (int64_t)cnt(LC_NEARBAD);
         const int64_t nm = c < d.max_samples ? c : d.max_samples;
         o.near_zero_sample_count = nm;
+        if (a.near_cm) {
+          // the later launches read these from device memory (the record may be host memory)
+          a.near_cm[2 * seg] = (uint64_t)c;
+          a.near_cm[2 * seg + 1] = (uint64_t)nm;
+        }
         // the near-zero selection writes these when it has a sample to work on
         if (!(d.flags & KVV_FLAG_NEAR_ZERO) || nm == 0) o.near_zero_p99_abs = o.near_zero_mean_abs = qnan;
         break;
@@ -362,13 +368,15 @@ __device__ inline void reduce_near_prefix(const TailArgs& a, const SegDesc& d, R
   }
 }
 
+template <bool BATCH>
 __device__ inline void reduce_segment(const TailArgs& a, int seg, int role, ReduceLds& L) {
-  const SegDesc& d = a.table ? a.table[seg] : a.seg0;
+  // a single pair's descriptor is read from the kernel arguments (scalar loads)
+  const SegDesc& d = BATCH ? a.table[seg] : a.seg0;
   const int64_t nruns = segment_runs(d);
   switch (role) {
-    case 0: reduce_counts<0, LC_HIST0>(a, d, nruns, L); break;
-    case 1: reduce_counts<LC_HIST0, kBuckets>(a, d, nruns, L); break;
-    case 2: reduce_counts<CU_MISM, 3>(a, d, nruns, L); break;
+    case 0: reduce_counts<0, LC_HIST0>(a, d, seg, nruns, L); break;
+    case 1: reduce_counts<LC_HIST0, kBuckets>(a, d, seg, nruns, L); break;
+    case 2: reduce_counts<CU_MISM, 3>(a, d, seg, nruns, L); break;
     case 3: reduce_extrema(a, d, nruns, L); break;
     case 4: reduce_sums(a, d, nruns, L); break;
     default: reduce_near_prefix(a, d, L); break;
@@ -376,8 +384,12 @@ __device__ inline void reduce_segment(const TailArgs& a, int seg, int role, Redu
 }
 
 // ------------------------------------------------------------ selection
-__device__ __forceinline__ int64_t group_count(const SegDesc& d, const kvv_result& r, int arr) {
-  return arr < 2 ? d.m : r.near_zero_sample_count;
+// Samples of array arr of segment s (the near-zero sample's size comes from the
+// fold's device copy, written in an earlier launch).
+__device__ __forceinline__ int64_t group_count(const TailArgs& a, const SegDesc& d, int s, int arr) {
+  if (arr < 2) return d.m;
+  // (volatile: kept a load of its own, not merged with d.m's into one generic-pointer load)
+  return (int64_t)*(const volatile uint64_t*)&a.near_cm[2 * s + 1];
 }
 
 // torch.quantile(q=0.99) ranks: rank = f32(0.99) * f32(m-1) rounded to float32;
@@ -618,7 +630,7 @@ struct BinRun32 {
 // rank's prefix (every value at the first pass), counted in 32-bit LDS bins.
 template <int SH, int W, bool FIRST>
 __device__ inline uint32_t group_pass(const float* v, int64_t count, const uint32_t pfx[2], bool same, SelectLds& L) {
-  constexpr int PER = kSelChunk / kBlock;
+  constexpr int PER = kStreamChunk / kBlock;
   constexpr uint32_t DM = (1u << W) - 1u;
   const int tid = threadIdx.x;
   for (int i = tid; i < 2 * 2048; i += kBlock) (&L.h[0][0])[i] = 0;
@@ -664,7 +676,7 @@ __device__ inline uint32_t group_pass(const float* v, int64_t count, const uint3
   // CU instead of 5), and more resident blocks hide the load latency better
   float xa[PER];
 #pragma unroll 1
-  for (int64_t c0 = 0; c0 < count; c0 += kSelChunk) {
+  for (int64_t c0 = 0; c0 < count; c0 += kStreamChunk) {
     load(xa, c0);
     count_in(xa, c0);
   }
@@ -799,23 +811,7 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
   const int rounds = d.sel_rounds;
   uint32_t* slot = a.slots + ((size_t)d.lslot * kArrays + arr) * kSlotWords;
   const float* v = a.arr[arr] + d.sample_off;
-  uint64_t rank64[2];
-  float wgt;
-  q99_ranks(count, rank64, wgt);
-  uint32_t pfx[2], resid[2];
-  group_state<LEVEL>(slot, rank64, pfx, resid, L);
-  const bool same = pfx[0] == pfx[1];
-  const int nwords = LEVEL == 0 ? 128 : (same ? 2048 : 4096);
-  for (int i = tid; i < nwords; i += kBlock) (&L.h[0][0])[i] = 0;
-  __syncthreads();
-  uint32_t nans = 0;
-  BinRun run0;
-#pragma unroll 1
-  for (int r = 0; r < rounds; ++r) {
-    const int64_t c0 = (c * rounds + r) * (int64_t)kSelChunk;
-    if (c0 >= count) break;
-    const int64_t c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
-    float x[PER];
+  auto load_round = [&](float (&x)[PER], int64_t c0, int64_t c1) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int64_t i0 = c0 + (int64_t)k * (4 * kBlock) + 4 * tid;
@@ -829,6 +825,31 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
 #pragma unroll
         for (int j = 0; j < 4; ++j) x[4 * k + j] = i0 + j < c1 ? v[i0 + j] : 0.0f;
       }
+    }
+  };
+  // the first round's values are in flight while the group's state is read
+  int64_t c0 = c * rounds * (int64_t)kSelChunk;
+  int64_t c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
+  float x[PER];
+  load_round(x, c0, c1);
+  uint64_t rank64[2];
+  float wgt;
+  q99_ranks(count, rank64, wgt);
+  uint32_t pfx[2], resid[2];
+  group_state<LEVEL>(slot, rank64, pfx, resid, L);
+  const bool same = pfx[0] == pfx[1];
+  const int nwords = LEVEL == 0 ? 128 : (same ? 2048 : 4096);
+  for (int i = tid; i < nwords; i += kBlock) (&L.h[0][0])[i] = 0;
+  __syncthreads();
+  uint32_t nans = 0;
+  BinRun run0;
+#pragma unroll 1
+  for (int r = 0; r < rounds; ++r) {
+    if (r > 0) {
+      c0 = (c * rounds + r) * (int64_t)kSelChunk;
+      if (c0 >= count) break;
+      c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
+      load_round(x, c0, c1);
     }
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -881,20 +902,22 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
 #ifdef KVV_COMMON_KERNELS
 // Level 0 also folds run records (leading blocks) and selects small groups;
 // "level" 4 selects the large groups of a many-group launch (select_group_stream).
-template <int LEVEL>
+// BATCH: the segments come from the device table; otherwise the single pair's
+// descriptor is a kernel argument, read with scalar loads.
+template <int LEVEL, bool BATCH>
 __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
   __shared__ TailLds lds;
   const int64_t b = blockIdx.x;
   if (LEVEL == 0 && b < a.reduce_blocks) {
-    reduce_segment(a, (int)(b / a.reduce_roles), (int)(b % a.reduce_roles), lds.r);
+    reduce_segment<BATCH>(a, (int)(b / a.reduce_roles), (int)(b % a.reduce_roles), lds.r);
     return;
   }
   const int64_t sb = b - a.reduce_blocks;
   const int arr = a.arr_lo + (int)(sb / a.total_chunks);
   const int64_t chunk = sb - (int64_t)(arr - a.arr_lo) * a.total_chunks;
-  const int s = a.table ? (int)a.chunk_seg[chunk] : 0;
-  const SegDesc& d = a.table ? a.table[s] : a.seg0;
-  const int64_t count = group_count(d, a.res[d.out_index], arr);
+  const int s = BATCH ? (int)a.chunk_seg[chunk] : 0;
+  const SegDesc& d = BATCH ? a.table[s] : a.seg0;
+  const int64_t count = group_count(a, d, s, arr);
   const int64_t c = chunk - d.chunk_begin;
   if (count <= 0) return;
   if (LEVEL == 4) {

@@ -373,6 +373,8 @@ def _run_jobs(jobs: List[_Job]) -> None:
     del keep, ws
     for i, j in enumerate(jobs):
         j.record = _lib.KvvResult.from_buffer_copy(host, i * rec_size)
+        if j.record.status != 0:
+            raise _lib.KvvLibraryError(f"the device verdict of {j.path} reported status {j.record.status}")
 
 
 # ------------------------------------------------------------ meta assembly
