@@ -87,7 +87,16 @@ enum kvv_mode {
 };
 
 /* Policy flags. */
-#define KVV_FLAG_NEAR_ZERO 0x1u   /* tolerant-policy near-zero diagnostics (generated_correctness_runner.py:481-548) */
+#define KVV_FLAG_NEAR_ZERO 0x1u   /* tolerant-policy near-zero diagnostics (generated_correctness_runner.py:481-548);
+                                     honoured for fp16/bf16 pairs, the only dtypes the reference computes them for */
+#define KVV_FLAG_NEAR_EXACT 0x2u  /* with KVV_FLAG_NEAR_ZERO: take the near-zero sample in a second pass over the
+                                     inputs instead of from entries recorded in the main pass (see
+                                     KVV_STATUS_NEAR_RETRY) */
+
+/* kvv_result.status values. */
+#define KVV_STATUS_NEAR_RETRY 1   /* a single fp16/bf16 pair's near-zero elements with a nonzero abs_diff did not fit
+                                     the workspace's entry pool: the near-zero fields are not valid (the others
+                                     are); call again with KVV_FLAG_NEAR_EXACT */
 
 typedef struct kvv_policy {
   int32_t mode;                /* enum kvv_mode */
@@ -130,7 +139,7 @@ typedef struct kvv_result {
   int64_t nan_pairs;                       /* pairs with a NaN on either side (no bucket) */
   double sum_gg, sum_rr, sum_gr, sum_dd;   /* fp64 sums of g*g, r*r, g*r, (g-r)^2 */
   double rel_l2, cosine;                   /* from the sums; cosine clamped to [-1,1] */
-  int32_t status;                          /* 0 */
+  int32_t status;                          /* 0, or KVV_STATUS_NEAR_RETRY */
   int32_t reserved;
 } kvv_result;
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -93,9 +94,9 @@ int scan_kind(const SegDesc& d) {
   return d.layout == L_CONTIG ? K_CONTIG : K_ROWS;
 }
 
-ScanFn scan_fn(int dt, int mode, int kind, bool batch) {
+ScanFn scan_fn(int dt, int mode, int kind, bool batch, bool nz = false) {
   switch (dt) {
-#define KVV_CASE(X) case X: return KVV_SCAN_FN(X)(mode, kind, batch);
+#define KVV_CASE(X) case X: return KVV_SCAN_FN(X)(mode, kind, batch, nz);
     KVV_CASE(0) KVV_CASE(1) KVV_CASE(2) KVV_CASE(3) KVV_CASE(4) KVV_CASE(5)
     KVV_CASE(6) KVV_CASE(7) KVV_CASE(8) KVV_CASE(9) KVV_CASE(10) KVV_CASE(11)
     KVV_CASE(12) KVV_CASE(13) KVV_CASE(14)
@@ -124,6 +125,32 @@ NearFn near_fn(int dt, int mode) {
 #undef KVV_CASE
     default: return nullptr;
   }
+}
+
+// Largest magnitude code of a 16-bit float type whose value is at most t, or -1
+// when even +0 is above t (t negative or NaN): |ref| <= t <=> (code & 0x7FFF) <= it.
+float half_value(int dt, uint32_t mag) {
+  if (dt == KVV_BF16) {
+    const uint32_t b = mag << 16;
+    float f;
+    std::memcpy(&f, &b, 4);
+    return f;
+  }
+  const uint32_t e = (mag >> 10) & 31u, m = mag & 1023u;
+  if (e == 31) return m ? __builtin_nanf("") : __builtin_inff();
+  return e == 0 ? std::ldexp((float)m, -24) : std::ldexp((float)(m | 1024u), (int)e - 25);
+}
+
+int32_t near_code(int dt, float t) {
+  if (dt != KVV_F16 && dt != KVV_BF16) return -1;
+  if (!(half_value(dt, 0) <= t)) return -1;
+  uint32_t lo = 0, hi = dt == KVV_BF16 ? 0x7F80u : 0x7C00u;  // magnitudes up to the infinity code ascend
+  if (half_value(dt, hi) <= t) return (int32_t)hi;
+  while (hi - lo > 1) {  // value(lo) <= t < value(hi)
+    const uint32_t mid = (lo + hi) / 2;
+    if (half_value(dt, mid) <= t) lo = mid; else hi = mid;
+  }
+  return (int32_t)lo;
 }
 
 // Coalesces the joint (size, gen stride, ref stride) dims and picks the layout.
@@ -165,7 +192,8 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
   d.max_samples = p->max_samples;
   d.m = n < p->max_samples ? n : p->max_samples;
   d.mode = p->mode;
-  d.flags = p->flags & KVV_FLAG_NEAR_ZERO;
+  // the reference takes near-zero diagnostics for fp16/bf16 references only (GCR:491-492)
+  d.flags = (r->dtype == KVV_F16 || r->dtype == KVV_BF16) ? (p->flags & KVV_FLAG_NEAR_ZERO) : 0u;
   d.rtol = (float)p->rtol;
   d.atol = (float)p->atol;
   d.zero_tol = (p->rtol == 0.0 && p->atol == 0.0) ? 1 : 0;
@@ -175,7 +203,8 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
   // A bit-identical finite pair is a non-mismatch with abs_diff 0 -- unless the integer
   // threshold is negative (0 > t) or a negative near-zero "bad" threshold counts 0 as bad.
   d.fast = !(p->mode == KVV_MODE_MAX_ABS_DIFF && p->max_abs_diff < 0) &&
-           !((p->flags & KVV_FLAG_NEAR_ZERO) && d.nz_bad < 0.0f);
+           !((d.flags & KVV_FLAG_NEAR_ZERO) && d.nz_bad < 0.0f);
+  d.nz_code = near_code(r->dtype, d.nz_abs);
   d.dtype = r->dtype;
   d.item_elems = item_elems_for(r->dtype);
 
@@ -257,7 +286,21 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
 struct WsLayout {
   int64_t run_stride;
   size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample,
-      near_cm, table, chunk_seg, isel_state, isel_seg, isel_chunk, isel_sums, total;
+      near_cm, ent, near_wave, ent_fill, near_psum, table, chunk_seg, isel_state, isel_seg, isel_chunk, isel_sums, total;
+};
+
+// Near-zero entries of a single fp16/bf16 pair (kFlagNearEntries): at most
+// kEntPool 8-byte entries in all, split evenly over the main pass's waves;
+// kScatterMax blocks of the first tail launch place them.
+constexpr int64_t kEntPool = int64_t(1) << 21;
+constexpr int kScatterMax = 256;
+
+// How a single pair's near-zero diagnostics are taken: none, entries recorded
+// in the main pass, or the near-zero pass over the inputs after it.
+struct NearMode {
+  bool any() const { return exact || entries; }
+  bool exact = false, entries = false;
+  int64_t waves = 0, ent_total = 0;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -271,7 +314,7 @@ int64_t run_slot_bound(int64_t item_count) {
 }
 
 WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int64_t nslots, int64_t chunks,
-                          int64_t items, bool near, bool batch, int64_t nisel = 0, int64_t isel_chunks = 0) {
+                          int64_t items, const NearMode& near, bool batch, int64_t nisel = 0, int64_t isel_chunks = 0) {
   WsLayout L{};
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -289,12 +332,20 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
   L.slot_bytes = slot_part + (size_t)nisel * kIselStateWords * 4;
   L.slots = take(L.slot_bytes);
   L.isel_state = L.slots + slot_part;
-  if (near) {
+  if (near.exact) {
     L.item_near = take((size_t)items * 4);
     L.item_near_off = take((size_t)items * 8);
     L.item_near_sum = take((size_t)items * 8);
+  }
+  if (near.any()) {
     L.near_sample = take((size_t)samples * 4);
     L.near_cm = take((size_t)nseg * 16);
+  }
+  if (near.entries) {
+    L.ent = take((size_t)near.ent_total * 8);
+    L.near_wave = take((size_t)near.waves * 4);
+    L.ent_fill = take((size_t)near.waves * 4);
+    L.near_psum = take((size_t)kScatterMax * 8);
   }
   if (batch) {
     L.table = take((size_t)nseg * sizeof(SegDesc));
@@ -337,8 +388,9 @@ struct NearLaunch {
 // in one launch; with near-zero diagnostics the near-zero sample and its first
 // level; then select levels 1 and 2 and the final read-off of every array.
 int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchunk, int nseg, int64_t total_chunks,
-                int64_t nslots, bool near, const WsLayout& L, void* ws, kvv_result* out, hipStream_t st,
+                int64_t nslots, const NearMode& nm, const WsLayout& L, void* ws, kvv_result* out, hipStream_t st,
                 const std::vector<NearLaunch>& nears, bool stream_groups = false) {
+  const bool near = nm.any();
   TailArgs t{};
   if (seg0) t.seg0 = *seg0;
   t.table = dtable;
@@ -347,24 +399,35 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   t.total_chunks = total_chunks > 0 ? total_chunks : 1;
   t.res = out;
   t.runs = run_cols(L, ws);
-  t.reduce_roles = near ? 6 : 5;
+  t.reduce_roles = nm.exact ? 6 : 5;
   t.arr[0] = at<float>(ws, L.sample_abs);
   t.arr[1] = at<float>(ws, L.sample_rel);
   t.arr[2] = near ? at<float>(ws, L.near_sample) : nullptr;
   t.slots = at<uint32_t>(ws, L.slots);
-  t.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
-  t.item_near_off = near ? at<uint64_t>(ws, L.item_near_off) : nullptr;
-  t.item_near_sum = near ? at<double>(ws, L.item_near_sum) : nullptr;
+  t.item_near = nm.exact ? at<uint32_t>(ws, L.item_near) : nullptr;
+  t.item_near_off = nm.exact ? at<uint64_t>(ws, L.item_near_off) : nullptr;
+  t.item_near_sum = nm.exact ? at<double>(ws, L.item_near_sum) : nullptr;
+  int scatter = 0;
+  if (nm.entries) {
+    t.ent = at<uint2>(ws, L.ent);
+    t.near_wave = at<uint32_t>(ws, L.near_wave);
+    t.ent_fill = at<uint32_t>(ws, L.ent_fill);
+    t.nwaves = (int32_t)nm.waves;
+    t.ent_quota = (uint32_t)(nm.ent_total / nm.waves);
+    scatter = nm.waves < kScatterMax ? (int)nm.waves : kScatterMax;
+    t.scatter_blocks = scatter;
+    t.near_psum = at<double>(ws, L.near_psum);
+  }
   t.isel_sums = at<double>(ws, L.isel_sums);
   t.near_cm = near ? at<uint64_t>(ws, L.near_cm) : nullptr;
   const bool batch = dtable != nullptr;
-  auto launch = [&](int reduce_blocks, int level, int arr_lo, int narr) -> int {
+  auto launch = [&](int reduce_blocks, int level, int arr_lo, int narr, int extra = 0) -> int {
     TailArgs x = t;
     x.reduce_blocks = reduce_blocks;
     x.level = level;
     x.arr_lo = arr_lo;
     x.narr = narr;
-    const int64_t grid = reduce_blocks + (total_chunks > 0 ? (int64_t)narr * total_chunks : 0);
+    const int64_t grid = reduce_blocks + (total_chunks > 0 ? (int64_t)narr * total_chunks : 0) + extra;
     if (grid == 0) return KVV_OK;
     void (*fn)(TailArgs) = nullptr;
     switch (level) {
@@ -378,13 +441,19 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
     KVV_HIP(hipGetLastError());
     return KVV_OK;
   };
-  int rc = launch(nseg * t.reduce_roles, 0, 0, 2);
+  // (with near-zero entries the first launch's trailing blocks build the near-zero sample)
+  int rc = launch(nseg * t.reduce_roles, 0, 0, 2, scatter);
   if (rc) return rc;
   if (stream_groups) {
     rc = launch(0, 4, 0, 2);
     if (rc) return rc;
   }
-  if (near) {
+  if (nm.entries && nslots == 0) {
+    // a small near-zero sample is selected once the first launch has placed the entries
+    rc = launch(0, 1, 2, 1);
+    if (rc) return rc;
+  }
+  if (nm.exact) {
     for (const auto& nl : nears) {
       if (nl.items == 0) continue;
       NearArgs na{};
@@ -430,6 +499,11 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
 int plan_single(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, SegDesc& d) {
   int rc = plan_segment(g, r, p, d);
   if (rc) return rc;
+  // a vector-kind fp16/bf16 pair takes its near-zero diagnostics as entries in
+  // the main pass, unless the caller asks for the pass over the inputs
+  if ((d.flags & KVV_FLAG_NEAR_ZERO) && !(p->flags & KVV_FLAG_NEAR_EXACT) && d.mode == KVV_MODE_ISCLOSE &&
+      scan_kind(d) != K_SCALAR)
+    d.flags = (d.flags & ~KVV_FLAG_NEAR_ZERO) | kFlagNearEntries;
   if (scan_kind(d) == K_CONTIG) {
     const int64_t min_elems = d.item_elems / kUnroll;
     const int64_t want = 2 * 12 * (int64_t)device_cus();  // two items per wave of a full grid
@@ -472,6 +546,50 @@ void plan_rounds(ScanArgs& a, ScanFn scan, int64_t grid) {
   a.round_blocks = (int32_t)cus;
 }
 
+// The main-pass launch of a single pair: kernel, items per wave, grid, the
+// dispatch-round shares, and the near-zero mode with its entry quota.
+struct SingleGeom {
+  ScanFn scan = nullptr;
+  int64_t ipw = 1, grid = 0;
+  ScanArgs rounds{};  // the round fields
+  NearMode near;
+  uint32_t ent_quota = 0;
+};
+
+int single_geom(const SegDesc& d, SingleGeom& g) {
+  const bool nz = (d.flags & kFlagNearEntries) != 0;
+  g.scan = scan_fn(d.dtype, d.mode, scan_kind(d), false, nz);
+  if (!g.scan) return fail(KVV_E_INVALID, "no kernel for dtype");
+  const int64_t target = blocks_target(g.scan) * kWaves;  // waves of the grid
+  g.ipw = d.item_count > 0 ? (d.item_count + target - 1) / target : 1;  // items per wave
+  const int64_t per_block = g.ipw * kWaves;
+  g.grid = d.item_count > 0 ? (d.item_count + per_block - 1) / per_block : 0;
+  g.rounds.items = d.item_count;
+  plan_rounds(g.rounds, g.scan, g.grid);
+  int64_t max_ipw = g.ipw;
+  if (g.rounds.rounds > 1)
+    for (int r = 0; r < g.rounds.rounds; ++r) max_ipw = g.rounds.round_ipw[r] > max_ipw ? g.rounds.round_ipw[r] : max_ipw;
+  if ((uint64_t)max_ipw * kWaves * (uint64_t)d.item_elems >= (1ull << 32))
+    return fail(KVV_E_UNSUPPORTED, "tensor too large for 32-bit per-block counts");
+  g.near.exact = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
+  g.near.entries = nz;
+  if (nz) {
+    // an even share of the pool, but never more than a wave's elements
+    g.near.waves = g.grid * kWaves > 0 ? g.grid * kWaves : kWaves;
+    // a scatter block places the entries of at most 64 waves
+    if (g.near.waves > (int64_t)kScatterMax * 64) return fail(KVV_E_UNSUPPORTED, "main-pass grid too large for the near-zero scatter");
+    const int64_t share = kEntPool / g.near.waves, range = max_ipw * (int64_t)d.item_elems;
+    g.ent_quota = (uint32_t)(share < range ? share : range);
+    g.near.ent_total = (int64_t)g.ent_quota * g.near.waves;
+  }
+  return KVV_OK;
+}
+
+WsLayout single_layout(const SegDesc& d, const SingleGeom& g) {
+  return workspace_layout(run_slot_bound(d.item_count), d.m, 1, d.m > kSmall ? 1 : 0, d.chunk_count, d.item_count,
+                          g.near, false);
+}
+
 int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st,
                hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr) {
   SegDesc d = d0;
@@ -481,55 +599,54 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   d.out_index = 0;
   d.lslot = d.m > kSmall ? 0 : -1;
   const int64_t nslots = d.lslot >= 0 ? 1 : 0;
-  const bool near = (d.flags & KVV_FLAG_NEAR_ZERO) != 0;
   d.run_slot0 = 0;
-  const WsLayout L = workspace_layout(run_slot_bound(d.item_count), d.m, 1, nslots, d.chunk_count, d.item_count, near,
-                                      false);
-  int rc = check_ws(L, ws, ws_bytes, out);
+  SingleGeom g;
+  int rc = single_geom(d, g);
   if (rc) return rc;
-  const int kind = scan_kind(d);
-  ScanFn scan = scan_fn(d.dtype, d.mode, kind, false);
-  if (!scan) return fail(KVV_E_INVALID, "no kernel for dtype");
-  const int64_t target = blocks_target(scan) * kWaves;  // waves of the grid
-  const int64_t ipw = d.item_count > 0 ? (d.item_count + target - 1) / target : 1;  // items per wave
+  const WsLayout L = single_layout(d, g);
+  rc = check_ws(L, ws, ws_bytes, out);
+  if (rc) return rc;
   // one run record per block: its waves fold theirs (a single-segment launch)
   d.run_base = 0;
-  d.run_ipb = ipw * kWaves;
-  if ((uint64_t)d.run_ipb * (uint64_t)d.item_elems >= (1ull << 32))
-    return fail(KVV_E_UNSUPPORTED, "tensor too large for 32-bit per-block counts");
+  d.run_ipb = g.ipw * kWaves;
   if (d.item_count > 0) {
-    ScanArgs a{};
+    ScanArgs a = g.rounds;
     a.seg0 = d;
     a.table = nullptr;
     a.nseg = 1;
     a.item_lo = 0;
     a.items = d.item_count;
-    a.items_per_wave = ipw;
+    a.items_per_wave = g.ipw;
     a.runs = run_cols(L, ws);
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);
-    a.item_near = near ? at<uint32_t>(ws, L.item_near) : nullptr;
+    a.item_near = g.near.exact ? at<uint32_t>(ws, L.item_near) : nullptr;
     a.zero_ptr = at<uint4>(ws, L.slots);
     a.zero_n4 = (int64_t)(L.slot_bytes / 16);
-    const int64_t per_block = a.items_per_wave * kWaves;
-    const int64_t grid = (d.item_count + per_block - 1) / per_block;
-    plan_rounds(a, scan, grid);
-    for (int r = 0; r < a.rounds; ++r)
-      if ((uint64_t)a.round_ipw[r] * kWaves * (uint64_t)d.item_elems >= (1ull << 32))
-        return fail(KVV_E_UNSUPPORTED, "tensor too large for 32-bit per-block counts");
+    if (g.near.entries) {
+      a.ent = at<uint2>(ws, L.ent);
+      a.near_wave = at<uint32_t>(ws, L.near_wave);
+      a.ent_fill = at<uint32_t>(ws, L.ent_fill);
+      a.ent_quota = g.ent_quota;
+      // the near-zero sample starts at zero: entries fill in its nonzero values
+      a.zero2_ptr = at<uint4>(ws, L.near_sample);
+      a.zero2_n4 = (int64_t)((align256((size_t)d.m * 4)) / 16);
+    }
     if (ev_begin) KVV_HIP(hipEventRecord(ev_begin, st));
-    hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL(g.scan, dim3((unsigned)g.grid), dim3(kBlock), 0, st, a);
     KVV_HIP(hipGetLastError());
     if (ev_end) KVV_HIP(hipEventRecord(ev_end, st));
   }
   std::vector<NearLaunch> nears{{near_fn(d.dtype, d.mode), 0, 1, 0, d.item_count}};
-  return launch_tail(&d, nullptr, nullptr, 1, d.chunk_count, nslots, near, L, ws, out, st, nears);
+  return launch_tail(&d, nullptr, nullptr, 1, d.chunk_count, nslots, g.near, L, ws, out, st, nears);
 }
 
-size_t single_workspace_bytes(const SegDesc& d) {
-  return workspace_layout(run_slot_bound(d.item_count), d.m, 1, d.m > kSmall ? 1 : 0, d.chunk_count, d.item_count,
-                          (d.flags & KVV_FLAG_NEAR_ZERO) != 0, false)
-      .total;
+int single_workspace_bytes(const SegDesc& d, size_t* bytes) {
+  SingleGeom g;
+  const int rc = single_geom(d, g);
+  if (rc) return rc;
+  *bytes = single_layout(d, g).total;
+  return KVV_OK;
 }
 
 // ------------------------------------------------------------ no-alloc entry
@@ -696,7 +813,9 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   const int nseg = (int)bp.table.size();
   if (nseg == 0) return KVV_OK;
   const int64_t nisel = (int64_t)bp.isel_seg.size(), isel_chunks = (int64_t)bp.isel_chunk.size() / 2;
-  const WsLayout L = workspace_layout(bp.run_slots, bp.samples, nseg, bp.nslots, bp.chunks, bp.items, bp.near, true,
+  NearMode near;
+  near.exact = bp.near;
+  const WsLayout L = workspace_layout(bp.run_slots, bp.samples, nseg, bp.nslots, bp.chunks, bp.items, near, true,
                                       nisel, isel_chunks);
   int rc = check_ws(L, ws, ws_bytes, out);
   if (rc) return rc;
@@ -763,7 +882,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
       KVV_HIP(hipGetLastError());
     }
   }
-  return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, bp.near, L, ws, out, st, nears,
+  return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, near, L, ws, out, st, nears,
                      bp.stream_groups);
 }
 
@@ -782,8 +901,7 @@ int kvv_workspace_size(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_p
   kvv::SegDesc d;
   int rc = kvv::plan_single(gen, ref, policy, d);
   if (rc) return rc;
-  *bytes = kvv::single_workspace_bytes(d);
-  return KVV_OK;
+  return kvv::single_workspace_bytes(d, bytes);
 }
 
 int kvv_verdict(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy, kvv_result* out,
@@ -808,7 +926,9 @@ int kvv_verdict_noalloc(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_
   kvv::SegDesc d;
   int rc = kvv::plan_single(gen, ref, policy, d);
   if (rc) return rc;
-  const size_t need = kvv::single_workspace_bytes(d);
+  size_t need = 0;
+  rc = kvv::single_workspace_bytes(d, &need);
+  if (rc) return rc;
   if (need > kvv::kScratchBytes)
     return kvv::fail(KVV_E_WORKSPACE, "this verdict needs " + std::to_string(need) +
                                           " bytes of workspace; the no-alloc entry point holds " +
@@ -826,8 +946,10 @@ int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_te
   kvv::BatchPlan bp;
   int rc = kvv::plan_batch(count, gens, refs, policies, bp);
   if (rc) return rc;
+  kvv::NearMode near;
+  near.exact = bp.near;
   *bytes = kvv::workspace_layout(bp.run_slots, bp.samples, (int64_t)bp.table.size(), bp.nslots, bp.chunks, bp.items,
-                                 bp.near, true, (int64_t)bp.isel_seg.size(), (int64_t)bp.isel_chunk.size() / 2)
+                                 near, true, (int64_t)bp.isel_seg.size(), (int64_t)bp.isel_chunk.size() / 2)
                .total;
   return KVV_OK;
 }

@@ -36,6 +36,11 @@ constexpr int kSmall = 8192;          // groups of at most this many samples are
 constexpr int64_t kGroupStreamMax = 1 << 22;  // largest group one block streams in a many-group launch
 constexpr int kArrays = 3;            // abs, rel, near-zero abs
 constexpr uint32_t kFlagInputSelect = 0x80000000u;  // SegDesc.flags: abs/rel p99 selected from the inputs
+// SegDesc.flags: the near-zero diagnostics of a single fp16/bf16 pair, taken in the main pass as "entries"
+// (near-zero elements with a nonzero abs_diff: their rank among the wave's near-zero elements and value);
+// the other near-zero elements are the zeros of the compacted array (GCR:525-529)
+constexpr uint32_t kFlagNearEntries = 0x40000000u;
+constexpr uint32_t kFlagNearAny = KVV_FLAG_NEAR_ZERO | kFlagNearEntries;
 constexpr int64_t kIselChunk = 1 << 17;        // elements per input-select chunk (every element a sample)
 constexpr int64_t kIselChunkSampled = 1 << 15;  // samples per chunk at strided positions (element loads)
 // Per (large segment, array) slot: level-0 histogram (256), level-1 and level-2
@@ -89,6 +94,8 @@ struct SegDesc {
   int32_t sel_rounds;     // kSelChunk sub-chunks per select block of a large group (1..kMaxSelRounds)
   int32_t isel_slot;      // input-select state of the segment (kFlagInputSelect), else -1
   int32_t isel_chunk0;    // its first input-select chunk (batch-wide numbering)
+  int32_t nz_code;        // kFlagNearEntries: largest magnitude code with |value| <= nz_abs, -1 for none
+  int32_t pad_nz;
   int64_t run_slot0;      // first run slot of this segment (a multiple of 4)
   int64_t row_len;        // L_ROWS: contiguous inner length
   Dims dims;              // L_ROWS: outer dims; L_GENERIC: all dims
@@ -132,6 +139,15 @@ struct ScanArgs {
   uint32_t* item_near;     // near-zero count per item (KVV_FLAG_NEAR_ZERO)
   uint4* zero_ptr;         // select slots cleared by this launch (split over its blocks)
   int64_t zero_n4;         // their size in 16-byte words (0: none)
+  uint4* zero2_ptr;        // a second region cleared likewise (the near-zero sample built from entries)
+  int64_t zero2_n4;
+  // kFlagNearEntries: wave q owns entries [q * ent_quota, (q + 1) * ent_quota) and writes, when done,
+  // its near-zero count and its entry count (kNone32 when its entries did not fit)
+  uint2* ent;              // (rank among the wave's near-zero elements, abs_diff bits)
+  uint32_t* near_wave;
+  uint32_t* ent_fill;
+  uint32_t ent_quota;
+  uint32_t pad_ent;
 };
 
 // Per-lane accumulators.  Counts live in the per-wave LDS counters instead.
@@ -355,9 +371,10 @@ __device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem
     acc.s[2] = fma(g64, r64, acc.s[2]);
     acc.s[3] = fma(d64, d64, acc.s[3]);
   }
-  if (d.flags & KVV_FLAG_NEAR_ZERO) {
+  if (d.flags & kFlagNearAny) {
     const bool near = fabsf(rf) <= d.nz_abs;
-    wave_add(wc, LC_NEAR, act && near);
+    // (with near-zero entries, every element's near-zero count comes from the item's masks)
+    if (d.flags & KVV_FLAG_NEAR_ZERO) wave_add(wc, LC_NEAR, act && near);
     wave_add(wc, LC_NEARBAD, act && near && adf > d.nz_bad);
     wave_add(wc, LC_FARMM, mm && !near);
   }
@@ -995,6 +1012,121 @@ __device__ __forceinline__ void phase_b(const SegDesc& d, uint32_t R0, uint32_t 
   }
 }
 
+// ------------------------------------------------------------ near-zero entries
+// The near-zero elements (|ref| <= near_zero_abs) of a lane's vectors of 16-bit
+// codes, found on the codes, as a mask in the slow-mask layout: bit dd of the
+// low half and bit 16 + dd of the high half of dword dd = u * 4 + j, i.e.
+// elements 2j and 2j + 1 of vector u.  pre[u] counts the near-zero elements of
+// the item before vector u of this lane in row-major order (vectors u, then
+// lanes, then elements); preA holds u = 0, 1 and preB u = 2, 3 as 16-bit
+// halves.  total is the item's count (wave-uniform).
+struct NearItem {
+  uint32_t mask, preA, preB, total;
+};
+
+template <int DT>
+__device__ __forceinline__ NearItem near_item(const SegDesc& d, StageP stage, int64_t L0, int64_t L1) {
+  static_assert(VecIO<DT>::V == 8 && kUnroll == 4, "16-bit codes, four vectors per lane");
+  const int lane = lane_id();
+  const u16x2 t = {(uint16_t)d.nz_code, (uint16_t)d.nz_code};
+  uint32_t mask = 0;
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint4 rq = stage_vec(stage, (2 * u + 1) * 64 + lane);
+    const uint32_t rw[4] = {rq.x, rq.y, rq.z, rq.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // per half: 1 where the magnitude code is above the threshold code
+      const u16x2 mag = __builtin_bit_cast(u16x2, rw[j] & 0x7FFF7FFFu);
+      const uint32_t over = pk_nonzero16(__builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(mag, t)));
+      mask |= (over ^ 0x00010001u) << (u * 4 + j);
+    }
+  }
+  // only the elements inside the item (a partial last vector or item), and none
+  // when no magnitude is near zero (nz_code < 0)
+  uint32_t valid = 0;
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t left = L1 - (L0 + (int64_t)(u * 64 + lane) * 8);  // elements of vector u inside the item
+    const uint32_t lo = left >= 7 ? 0xFu : (left > 0 ? (1u << ((left + 1) >> 1)) - 1u : 0u);  // elements 2j < left
+    const uint32_t hi = left >= 8 ? 0xFu : (left > 1 ? (1u << (left >> 1)) - 1u : 0u);        // elements 2j + 1 < left
+    valid |= (lo << (u * 4)) | (hi << (16 + u * 4));
+  }
+  mask &= d.nz_code < 0 ? 0u : valid;
+  NearItem o;
+  o.mask = mask;
+  // counts per vector, two to a word, then one packed scan per word (each
+  // 16-bit field stays below 64 * 8)
+  const uint32_t c0 = __popc(mask & 0x000F000Fu), c1 = __popc(mask & 0x00F000F0u);
+  const uint32_t c2 = __popc(mask & 0x0F000F00u), c3 = __popc(mask & 0xF000F000u);
+  const uint32_t x = c0 | (c1 << 16), y = c2 | (c3 << 16);
+  const uint32_t ix = wave_incl_scan(x), iy = wave_incl_scan(y);
+  const uint32_t tx = (uint32_t)__builtin_amdgcn_readlane((int)ix, 63), ty = (uint32_t)__builtin_amdgcn_readlane((int)iy, 63);
+  const uint32_t ex = ix - x, ey = iy - y;
+  const uint32_t t0 = tx & 0xFFFFu, t1 = tx >> 16, t2 = ty & 0xFFFFu;
+  const uint32_t p0 = ex & 0xFFFFu, p1 = t0 + (ex >> 16);
+  const uint32_t p2 = t0 + t1 + (ey & 0xFFFFu), p3 = t0 + t1 + t2 + (ey >> 16);
+  o.preA = p0 | (p1 << 16);
+  o.preB = p2 | (p3 << 16);
+  o.total = uniform(t0 + t1 + t2 + (ty >> 16));
+  return o;
+}
+
+// Where a wave's near-zero entries go: its own stretch of `quota` entries.
+// run_near counts the near-zero elements of the wave's run before the current
+// item (an entry's rank is that plus its rank inside the item).
+struct NearSink {
+  uint2* ent;
+  uint32_t quota, n, run_near;
+  bool over;  // an entry did not fit: the wave's entries are not valid
+};
+
+// Appends (rank, v) for the lanes with p.
+__device__ __forceinline__ void near_put(NearSink& s, bool p, uint32_t rank, float v) {
+  const uint64_t b = __ballot(p);
+  if (!b) return;
+  const uint32_t k = (uint32_t)__popcll(b);
+  if (s.over || s.n + k > s.quota) {
+    s.over = true;
+    return;
+  }
+  const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+  if (p) s.ent[s.n + below] = make_uint2(rank, __float_as_uint(v));
+  s.n = uniform(s.n + k);
+}
+
+// The item's entries: each lane walks its own near-zero elements that are not
+// bit-identical finite pairs (slow, or in a partial vector: only those can have
+// a nonzero abs_diff) and records those whose abs_diff is nonzero (NaN
+// included), with their rank in the item from its own prefix and mask.
+template <int DT>
+__device__ __forceinline__ void near_entries(const NearItem& ni, uint64_t slow, uint32_t full, StageP stage,
+                                             NearSink& s) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  const int lane = lane_id();
+  uint32_t part = 0;  // slots of the vectors that phase A left to vec_tail
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u)
+    if (!((full >> u) & 1u)) part |= 0x000F000Fu << (u * 4);
+  uint32_t cand = ni.mask & ((uint32_t)slow | part);
+  while (__ballot(cand != 0)) {
+    const bool act = cand != 0;
+    const int p = act ? __builtin_ctz(cand) : 0;
+    cand &= cand - 1;
+    const int dd = p & 15, u = dd >> 2, j = dd & 3, h = p >> 4;
+    const T gc = stage_elem<T>(stage, (2 * u) * 64 + lane, 2 * j + h);
+    const T rc = stage_elem<T>(stage, (2 * u + 1) * 64 + lane, 2 * j + h);
+    const float adf = fabsf(E::f32(gc) - E::f32(rc));
+    // near-zero elements of vector u before element 2j + h
+    const uint32_t lo = (ni.mask >> (u * 4)) & 0xFu, hi = (ni.mask >> (16 + u * 4)) & 0xFu;
+    const uint32_t below = (uint32_t)__popc(lo & ((1u << j) - 1u)) + (uint32_t)__popc(hi & ((1u << j) - 1u)) +
+                           (h ? ((lo >> j) & 1u) : 0u);
+    const uint32_t pre = ((u < 2 ? ni.preA : ni.preB) >> ((u & 1) * 16)) & 0xFFFFu;
+    near_put(s, act && adf != 0.0f, s.run_near + pre + below, adf);
+  }
+}
+
 // Strided-sample cursor: the next sample index i, its logical position idx =
 // floor(i*(n-1)/(m-1)) and rem = i*(n-1) mod (m-1).  Kept identical in every
 // wave of the block (wave-uniform), advanced item by item.
@@ -1496,8 +1628,12 @@ __device__ inline void block_record_part(const ScanArgs& a, SM& sm, Acc& acc, ui
   fold_block_record(rec, a.runs, blockIdx.x);
 }
 
-template <int DT, int MODE, int KIND, bool BATCH>
+// NZ: a single fp16/bf16 pair whose near-zero diagnostics are taken as entries
+// (kFlagNearEntries); the vector kinds with the dtype's isclose test only.
+template <int DT, int MODE, int KIND, bool BATCH, bool NZ = false>
 __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a) {
+  static_assert(!NZ || (!BATCH && KIND != K_SCALAR && MODE == KVV_MODE_ISCLOSE && Elem<DT>::width == 16 &&
+                        Elem<DT>::is_float), "near-zero entries: single fp16/bf16 pairs, vector kinds");
   __shared__ typename ScanLds<DT, KIND>::type sm;
   // the wave index, and all that derives from it (item range, segment, run), is
   // wave-uniform: segment fields are then read with scalar loads, which the
@@ -1509,14 +1645,17 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
     if (tid == 0) sm.done = 0;
     __syncthreads();
   }
-  if (a.zero_n4) {
-    // the select histograms and counters of this call start at zero (the later
-    // launches accumulate into them; nothing in this kernel touches them)
-    const int64_t per = (a.zero_n4 + gridDim.x - 1) / gridDim.x;
+  // the select histograms and counters of this call (and a near-zero sample
+  // built from entries) start at zero: the later launches accumulate into
+  // them, and nothing in this kernel touches them
+  auto clear = [&](uint4* p, int64_t n4) {
+    const int64_t per = (n4 + gridDim.x - 1) / gridDim.x;
     const int64_t z0 = (int64_t)blockIdx.x * per;
-    const int64_t z1 = z0 + per < a.zero_n4 ? z0 + per : a.zero_n4;
-    for (int64_t i = z0 + tid; i < z1; i += kBlock) a.zero_ptr[i] = make_uint4(0, 0, 0, 0);
-  }
+    const int64_t z1 = z0 + per < n4 ? z0 + per : n4;
+    for (int64_t i = z0 + tid; i < z1; i += kBlock) p[i] = make_uint4(0, 0, 0, 0);
+  };
+  if (a.zero_n4) clear(a.zero_ptr, a.zero_n4);
+  if (a.zero2_n4) clear(a.zero2_ptr, a.zero2_n4);
   // each wave owns a contiguous range of items; the waves of a block never wait
   // for each other
   int64_t i0, i1;
@@ -1539,7 +1678,22 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
   }
   Acc acc;
   acc.init();
+  const uint32_t wave_id = blockIdx.x * kWaves + (uint32_t)w;  // wave ranges ascend with it
+  NearSink sink;
+  if constexpr (NZ) {
+    sink.ent = a.ent + (size_t)wave_id * a.ent_quota;
+    sink.quota = a.ent_quota;
+    sink.n = 0;
+    sink.run_near = 0;
+    sink.over = false;
+  }
   if (i0 >= i1) {
+    if constexpr (NZ) {
+      if (lane == 0) {
+        a.near_wave[wave_id] = 0;
+        a.ent_fill[wave_id] = 0;
+      }
+    }
     // a single-segment launch folds one record per block: an empty wave still
     // leaves its (empty) part
     if constexpr (!BATCH) block_record_part(a, sm, acc, wc, w, a.seg0.item_begin);
@@ -1605,7 +1759,10 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
         // (an input-select segment's samples and sampled sums come from the input-select kernels)
         if (!dense && !(d.flags & kFlagInputSelect))
           sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, sb, ba, br);
+        NearItem ni{};
+        if constexpr (NZ) ni = near_item<DT>(d, stage, L0, L1);
         const uint64_t slow = phase_a_any<DT>(d, L0, R0, stage, full_now, acc, careful);
+        if constexpr (NZ) near_entries<DT>(ni, slow, full_now, stage, sink);
         if (__ballot(slow != 0)) {
           uint32_t nq = queue_all(slow, sm.queue[w]);
           // more than the queue holds: kQSlots slots of every lane at a time
@@ -1618,6 +1775,11 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
           }
         }
         if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, R0, full_now, stage, acc, wc);
+        if constexpr (NZ) {
+          // every near-zero element of the item joins the run's count
+          if (lane == 0) acc.nnear_fast += ni.total;
+          sink.run_near = uniform(sink.run_near + ni.total);
+        }
         if (dense && !(d.flags & kFlagInputSelect))
           dense_samples<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel);
       }
@@ -1631,6 +1793,12 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
       while (it >= ctable[s].item_begin + ctable[s].item_count) ++s;
       s = (int)uniform((uint32_t)s);
     } else {
+      if constexpr (NZ) {
+        if (lane == 0) {
+          a.near_wave[wave_id] = sink.run_near;
+          a.ent_fill[wave_id] = sink.over ? kNone32 : sink.n;
+        }
+      }
       block_record_part(a, sm, acc, wc, w, base);
       break;
     }

@@ -16,7 +16,7 @@ using IselFn = void (*)(IselArgs);
 #define KVV_ISEL_FN(dt) KVV_CAT(kvv_isel_fn_, dt)
 
 #define KVV_DECLARE(dt)                          \
-  ScanFn KVV_SCAN_FN(dt)(int mode, int kind, bool batch); \
+  ScanFn KVV_SCAN_FN(dt)(int mode, int kind, bool batch, bool nz); \
   NearFn KVV_NEAR_FN(dt)(int mode);                      \
   IselFn KVV_ISEL_FN(dt)(bool gather);
 

@@ -23,12 +23,26 @@ template <int MODE, int KIND>
 ScanFn pick(bool batch) {
   return batch ? (ScanFn)scan_kernel<kDt, MODE, KIND, true> : (ScanFn)scan_kernel<kDt, MODE, KIND, false>;
 }
+
+// single fp16/bf16 pairs whose near-zero diagnostics are taken as entries
+constexpr bool kNearEntries = kDt == KVV_F16 || kDt == KVV_BF16;
+template <int KIND>
+ScanFn pick_nz() {
+  if constexpr (kNearEntries) return (ScanFn)scan_kernel<kDt, KVV_MODE_ISCLOSE, KIND, false, true>;
+  else return nullptr;
+}
 }  // namespace
 
 // The dtype's natural test (isclose for floats, max_abs_diff for integers) gets
 // the vector kinds; the other test, which only unusual tolerance configs ask
 // for, always takes the scalar kind.
-ScanFn KVV_SCAN_FN(KVV_DT)(int mode, int kind, bool batch) {
+ScanFn KVV_SCAN_FN(KVV_DT)(int mode, int kind, bool batch, bool nz) {
+  if (nz) {
+    if (batch || mode != KVV_MODE_ISCLOSE) return nullptr;
+    if (kind == K_CONTIG) return pick_nz<K_CONTIG>();
+    if (kind == K_ROWS) return pick_nz<K_ROWS>();
+    return nullptr;
+  }
   if (mode == kNative) {
     if (kind == K_CONTIG) return pick<kNative, K_CONTIG>(batch);
     if (kind == K_ROWS) return pick<kNative, K_ROWS>(batch);

@@ -45,6 +45,16 @@ struct TailArgs {
   const double* item_near_sum;
   const double* isel_sums;    // input-select segments: sampled sums per chunk (3 each)
   uint64_t* near_cm;          // near-zero count and sample count per segment (device copies of the fold's)
+  // near-zero entries (kFlagNearEntries, single pairs): what the main pass's waves left, and the
+  // blocks of the first launch that place them in the near-zero sample
+  const uint2* ent;
+  const uint32_t* near_wave;
+  const uint32_t* ent_fill;
+  uint32_t ent_quota;
+  int32_t nwaves;
+  int32_t scatter_blocks;
+  int32_t pad3;
+  double* near_psum;          // per scatter block: the sum of its sampled entries
 };
 
 struct ReduceLds {
@@ -182,7 +192,7 @@ __device__ inline void reduce_counts(const TailArgs& a, const SegDesc& d, int se
           a.near_cm[2 * seg + 1] = (uint64_t)nm;
         }
         // the near-zero selection writes these when it has a sample to work on
-        if (!(d.flags & KVV_FLAG_NEAR_ZERO) || nm == 0) o.near_zero_p99_abs = o.near_zero_mean_abs = qnan;
+        if (!(d.flags & kFlagNearAny) || nm == 0) o.near_zero_p99_abs = o.near_zero_mean_abs = qnan;
         break;
       }
       default:
@@ -190,7 +200,13 @@ __device__ inline void reduce_counts(const TailArgs& a, const SegDesc& d, int se
     }
   } else if (F0 == LC_HIST0) {  // ULP histogram
     if (tid < kBuckets) o.ulp_hist[tid] = cnt(LC_HIST0 + tid);
-  } else if (tid == 0) {  // mismatches, and the fields of no column
+  } else {  // mismatches, and the fields of no column
+    // a wave whose near-zero entries did not fit: the near-zero fields must come from the exact path
+    bool over = false;
+    if ((d.flags & kFlagNearEntries) && a.ent_fill)
+      for (int w = tid; w < a.nwaves; w += kBlock) over = over || a.ent_fill[w] == kNone32;
+    over = __syncthreads_or(over);
+    if (tid != 0) return;
     const bool imode = d.mode == KVV_MODE_MAX_ABS_DIFF;
     o.numel = d.n;
     const uint64_t mm = cnt(CU_MISM);
@@ -201,7 +217,7 @@ __device__ inline void reduce_counts(const TailArgs& a, const SegDesc& d, int se
     o.sample_count = d.m;
     // an empty sample has no selection to write its quantiles
     if (d.m == 0) o.p99_abs = o.p99_rel = qnan;
-    o.status = 0;
+    o.status = over ? KVV_STATUS_NEAR_RETRY : 0;
     o.reserved = 0;
   }
 }
@@ -516,12 +532,17 @@ __device__ inline void finalize_group(const TailArgs& a, const SegDesc& d, int a
   const int tid = threadIdx.x;
   if (tid == 0) store_p99(res, arr, key, wgt, has_nan);
   if (arr == 2) {
-    // near-zero sample mean: fixed-order sum of the per-item sampled sums
-    const int64_t per = (d.item_count + kBlock - 1) / kBlock;
-    const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
-    const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
+    // near-zero sample mean: fixed-order sum of the per-item sampled sums, or of
+    // the scatter blocks' sums when the sample was built from entries
     double t = 0.0;
-    for (int64_t k = k0; k < k1; ++k) t += a.item_near_sum[d.item_begin + k];
+    if (d.flags & kFlagNearEntries) {
+      for (int k = tid; k < a.scatter_blocks; k += kBlock) t += a.near_psum[k];
+    } else {
+      const int64_t per = (d.item_count + kBlock - 1) / kBlock;
+      const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
+      const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
+      for (int64_t k = k0; k < k1; ++k) t += a.item_near_sum[d.item_begin + k];
+    }
     L.part[tid] = t;
     __syncthreads();
     if (tid == 0) {
@@ -747,12 +768,14 @@ __device__ inline void select_group_stream(const TailArgs& a, const SegDesc& d, 
 // Prefixes and residual ranks of the two order statistics of a large group
 // after the digit levels below LEVEL, from the group's global histograms.  All
 // histogram words the block needs are loaded in one go.
+// zeros_add: values the level-0 histogram does not hold but the array does, all
+// +0 (a near-zero sample built from entries: its zeros were never histogrammed).
 template <int LEVEL>
 __device__ inline void group_state(const uint32_t* slot, const uint64_t rank64[2], uint32_t pfx[2], uint32_t resid[2],
-                                   SelectLds& L) {
+                                   SelectLds& L, uint32_t zeros_add = 0) {
   const int tid = threadIdx.x;
   uint32_t h0w = 0, h1a[16], h1b[16], h2a[16], h2b[16];
-  if (LEVEL >= 1) h0w = slot[kH0 + tid];
+  if (LEVEL >= 1) h0w = slot[kH0 + tid] + (tid == (int)(0x80000000u >> 24) ? zeros_add : 0u);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     if (LEVEL >= 2) {
@@ -792,6 +815,13 @@ __device__ inline void group_state(const uint32_t* slot, const uint64_t rank64[2
       resid[rr] -= below[rr];
     }
   }
+}
+
+// The near-zero sample's implicit zeros when it was built from entries: its
+// values minus the sampled entries the scatter counted (slot word kMisc + 1).
+__device__ __forceinline__ uint32_t entry_zeros(const SegDesc& d, int arr, int64_t count, const uint32_t* slot) {
+  if (arr != 2 || !(d.flags & kFlagNearEntries)) return 0u;
+  return (uint32_t)(count - (int64_t)slot[kMisc + 1]);
 }
 
 // One chunk of a large group at digit level LEVEL: 0 = bits 31..24, 1 = 23..12,
@@ -836,7 +866,7 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
   float wgt;
   q99_ranks(count, rank64, wgt);
   uint32_t pfx[2], resid[2];
-  group_state<LEVEL>(slot, rank64, pfx, resid, L);
+  group_state<LEVEL>(slot, rank64, pfx, resid, L, entry_zeros(d, arr, count, slot));
   const bool same = pfx[0] == pfx[1];
   const int nwords = LEVEL == 0 ? 128 : (same ? 2048 : 4096);
   for (int i = tid; i < nwords; i += kBlock) (&L.h[0][0])[i] = 0;
@@ -895,8 +925,142 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
   float wgt;
   q99_ranks(count, rank64, wgt);
   uint32_t key[2], resid[2];
-  group_state<3>(slot, rank64, key, resid, L);
+  group_state<3>(slot, rank64, key, resid, L, entry_zeros(d, arr, count, slot));
   finalize_group(a, d, arr, count, key, wgt, has_nan, L);
+}
+
+// ------------------------------------------------------------ near-zero entries
+// Scatter block b of the first tail launch (a single pair with
+// kFlagNearEntries).  The entries of waves [w0, w1) get their rank in the
+// compacted near-zero array (GCR:525-529: abs_diff over |ref| <= near_zero_abs,
+// row-major): the near-zero elements before wave w0 plus the entry's rank
+// within its wave.  A sampled rank j (every rank when c <= max_samples, else
+// j = i*(c-1)//(m-1) for some i, GCR:346-347) puts its value at position i of
+// the near-zero sample, which the main pass zeroed: the near-zero elements
+// without an entry are its zeros.  The block adds its sampled values to the
+// array's level-0 histogram (the zeros join when the next level reads it),
+// counts them and their NaNs, and leaves their fp64 sum for the mean.
+__device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
+  constexpr int kMaxW = 64;  // waves per scatter block (kScatterMax blocks cover 16384 waves)
+  const SegDesc& d = a.seg0;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int nw = a.nwaves;
+  const int per = (nw + a.scatter_blocks - 1) / a.scatter_blocks;
+  const int w0 = b * per < nw ? b * per : nw;
+  const int w1 = w0 + per < nw ? w0 + per : nw;
+  // the near-zero count c, and the near-zero elements of the waves before w0
+  uint64_t tot = 0, before = 0;
+  for (int w = tid; w < nw; w += kBlock) {
+    const uint64_t x = a.near_wave[w];
+    tot += x;
+    before += w < w0 ? x : 0u;
+  }
+  tot = wave_sum(tot);
+  before = wave_sum(before);
+  uint64_t* red = reinterpret_cast<uint64_t*>(L.part);
+  uint32_t* woff = &L.h[1][0];        // entry offset of each of the block's waves (+ the total)
+  uint64_t* wbase = red + 2 * kWaves;  // rank base of each of the block's waves
+  if (lane == 0) {
+    red[wv] = tot;
+    red[kWaves + wv] = before;
+  }
+  for (int i = tid; i < 256; i += kBlock) L.h[0][i] = 0;
+  // the block's waves: entry counts (a wave whose entries did not fit has none
+  // here; the fold marks the call for the exact path) and near-zero counts
+  uint32_t fill = 0, nnear = 0;
+  if (tid < w1 - w0) {
+    fill = a.ent_fill[w0 + tid];
+    fill = fill == kNone32 ? 0u : fill;
+    nnear = a.near_wave[w0 + tid];
+  }
+  __syncthreads();
+  uint64_t c = 0, base = 0;
+  for (int i = 0; i < kWaves; ++i) {
+    c += red[i];
+    base += red[kWaves + i];
+  }
+  // exclusive prefixes over the block's waves (at most kMaxW = 64, which the
+  // host's scatter block count guarantees): the first wave scans them
+  if (tid < kMaxW) {
+    const uint32_t fi = wave_incl_scan(fill);
+    const uint64_t ni = nnear;
+    uint64_t incl = ni;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t v = __shfl_up(incl, o);
+      if (lane >= o) incl += v;
+    }
+    woff[tid] = fi - fill;
+    wbase[tid] = base + incl - ni;
+    if (tid == 63) woff[kMaxW] = fi;
+  }
+  __syncthreads();
+  const uint32_t total = woff[kMaxW];
+  const uint64_t ms = (uint64_t)d.max_samples;
+  const uint64_t m = c < ms ? c : ms;
+  const bool strided = c > ms;
+  const uint64_t num = strided ? c - 1 : 1, den = strided ? m - 1 : 1;
+  const bool large = d.lslot >= 0;
+  uint32_t* slot = large ? a.slots + ((size_t)d.lslot * kArrays + 2) * kSlotWords : nullptr;
+  float* sample = const_cast<float*>(a.arr[2]) + d.sample_off;
+  double sum = 0.0;
+  uint32_t cnt = 0, nan = 0;
+  // the block's entries, wave after wave, all threads at once (k grows, so the
+  // wave index wi only moves forward)
+  int wi = 0;
+#pragma unroll 1
+  for (uint32_t k = tid; k < total; k += kBlock) {
+    while (wi + 1 < w1 - w0 && woff[wi + 1] <= k) ++wi;
+    const uint2 x = a.ent[(size_t)(w0 + wi) * a.ent_quota + (k - woff[wi])];
+    const uint64_t j = wbase[wi] + x.x;
+    uint64_t i = j;
+    bool take = j < c;
+    if (strided) {
+      // the first sample index i with i*(c-1) >= j*(m-1); rank j is sampled when
+      // i*(c-1) < (j+1)*(m-1) too (then floor(i*(c-1)/(m-1)) == j).  The
+      // estimate from doubles is off by at most one.
+      const uint64_t t = j * den;
+      i = (uint64_t)((double)t * (1.0 / (double)num));
+      if (i * num < t) ++i;
+      if (i > 0 && (i - 1) * num >= t) --i;
+      if (i * num < t) ++i;
+      take = i < m && i * num < t + den;
+    }
+    if (take) {
+      const float v = __uint_as_float(x.y);
+      sample[i] = v;
+      sum += (double)v;
+      ++cnt;
+      if (v != v) ++nan;
+      else if (large) atomicAdd(&L.h[0][fkey(v) >> 24], 1u);
+    }
+  }
+  sum = wave_sum(sum);
+  cnt = wave_sum(cnt);
+  nan = wave_sum(nan);
+  __syncthreads();  // (the rank bases in L.part are read above)
+  if (lane == 0) {
+    L.part[wv] = sum;
+    L.sh[wv] = cnt;
+    L.sh[kWaves + wv] = nan;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double s = 0.0;
+    for (int i = 0; i < kWaves; ++i) s += L.part[i];
+    a.near_psum[b] = s;
+    uint32_t tc = 0, tn = 0;
+    for (int i = 0; i < kWaves; ++i) {
+      tc += L.sh[i];
+      tn += L.sh[kWaves + i];
+    }
+    if (large && tc) atomicAdd(&slot[kMisc + 1], tc);
+    if (large && tn) atomicAdd(&slot[kMisc], tn);
+  }
+  if (large) {
+    for (int i = tid; i < 256; i += kBlock)
+      if (L.h[0][i]) atomicAdd(&slot[kH0 + i], L.h[0][i]);
+  }
 }
 
 #ifdef KVV_COMMON_KERNELS
@@ -913,6 +1077,11 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
     return;
   }
   const int64_t sb = b - a.reduce_blocks;
+  if (LEVEL == 0 && !BATCH && sb >= (int64_t)a.narr * a.total_chunks) {
+    // the trailing blocks of a single pair's first launch place its near-zero entries
+    near_scatter(a, (int)(sb - (int64_t)a.narr * a.total_chunks), lds.s);
+    return;
+  }
   const int arr = a.arr_lo + (int)(sb / a.total_chunks);
   const int64_t chunk = sb - (int64_t)(arr - a.arr_lo) * a.total_chunks;
   const int s = BATCH ? (int)a.chunk_seg[chunk] : 0;
@@ -928,7 +1097,9 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
     return;
   }
   if (count <= kSmall || d.lslot < 0) {
-    if (LEVEL == 0 && c == 0 && count <= kSmall) select_small(a, d, arr, count, lds.s);
+    // a near-zero sample built from entries is complete only after the first launch
+    const int small_level = arr == 2 && (d.flags & kFlagNearEntries) ? 1 : 0;
+    if (LEVEL == small_level && c == 0 && count <= kSmall) select_small(a, d, arr, count, lds.s);
     return;
   }
   if (LEVEL == 3) {

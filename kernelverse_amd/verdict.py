@@ -334,9 +334,25 @@ def _device_views(g: torch.Tensor, r: torch.Tensor):
 
 
 def _run_jobs(jobs: List[_Job]) -> None:
-    """Runs every job's pair through libkvv (one call for one pair, a batch call otherwise)."""
+    """Runs every job's pair through libkvv (one call for one pair, a batch call otherwise).
+
+    A single fp16/bf16 pair under the tolerant policy takes its near-zero
+    diagnostics from entries recorded in the main pass; when they do not fit
+    the workspace's pool the record says so (KVV_STATUS_NEAR_RETRY) and the
+    pair is run again with the near-zero pass over the inputs."""
     if not jobs:
         return
+    _launch(jobs)
+    retry = [j for j in jobs if j.record.status == _lib.STATUS_NEAR_RETRY]
+    for j in retry:
+        j.kpolicy.flags |= _lib.FLAG_NEAR_EXACT
+        _launch([j])
+    for j in jobs:
+        if j.record.status != 0:
+            raise _lib.KvvLibraryError(f"the device verdict of {j.path} reported status {j.record.status}")
+
+
+def _launch(jobs: List[_Job]) -> None:
     lib = _lib.load()
     dev = _device_for(*[j.ref for j in jobs], *[j.gen for j in jobs])
     keep = []
@@ -373,8 +389,6 @@ def _run_jobs(jobs: List[_Job]) -> None:
     del keep, ws
     for i, j in enumerate(jobs):
         j.record = _lib.KvvResult.from_buffer_copy(host, i * rec_size)
-        if j.record.status != 0:
-            raise _lib.KvvLibraryError(f"the device verdict of {j.path} reported status {j.record.status}")
 
 
 # ------------------------------------------------------------ meta assembly
