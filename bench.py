@@ -139,15 +139,23 @@ def cpu_baseline(pairs, policy=None, budget_s: float = 12.0):
 
 
 # HBM traffic of the main-pass kernel per launch, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (KiB per
-# dispatch) scaled by what the same counters read for a plain 512 MiB device copy (factors below); the runs and
-# commands are in profiles/scan_bf16_c1_traffic.md.  Keyed by config.
+# dispatch) scaled by what the same counters read for a plain 512 MiB device copy on the same box (factors
+# below); the runs and commands are in profiles/scan_bf16_c1_traffic.md (c1) and
+# profiles/scan_traffic_c0_c2_c3fp8_c3int8_c1tolerant.md (the others).  Keyed by config, and by
+# config/policy where the policy changes the main pass (tolerant: near-zero entries).
+_F2 = 524288.0 / 262156.5
 PMC_TRAFFIC = {
     "c1": {"fetch_kib": 524479.7, "write_kib": 9091.1, "fetch_factor": 524288.0 / 262157.4, "write_factor": 1.0},
+    "c1/tolerant": {"fetch_kib": 524521.8, "write_kib": 23600.2, "fetch_factor": _F2, "write_factor": 1.0},
+    "c0": {"fetch_kib": 4277.7, "write_kib": 8732.1, "fetch_factor": _F2, "write_factor": 1.0},
+    "c2": {"fetch_kib": 262465.8, "write_kib": 9061.3, "fetch_factor": _F2, "write_factor": 1.0},
+    "c3fp8": {"fetch_kib": 131273.0, "write_kib": 9060.4, "fetch_factor": _F2, "write_factor": 1.0},
+    "c3int8": {"fetch_kib": 131256.1, "write_kib": 9063.4, "fetch_factor": _F2, "write_factor": 1.0},
 }
 
 
-def traffic_bytes(config: str):
-    t = PMC_TRAFFIC.get(config)
+def traffic_bytes(config: str, policy: str = "strict"):
+    t = PMC_TRAFFIC.get(f"{config}/{policy}") or (PMC_TRAFFIC.get(config) if policy != "tolerant" else None)
     if not t or t["fetch_kib"] is None:
         return None
     return int(round((t["fetch_kib"] * t["fetch_factor"] + t["write_kib"] * t["write_factor"]) * 1024))
@@ -380,7 +388,7 @@ def main():
     recs = [_lib.KvvResult.from_buffer_copy(host.numpy().tobytes(), i * rec_size) for i in range(n_pairs)]
     value = bytes_read / (ms_per_step * 1e-3) / 1e9
     achieved = bytes_read / (main_avg * 1e-3) / 1e9
-    traffic = traffic_bytes(args.config)
+    traffic = traffic_bytes(args.config, args.policy)
     result = {
         "metric": METRIC,
         "value": round(value, 2),
