@@ -1025,10 +1025,14 @@ struct NearItem {
 };
 
 template <int DT>
-__device__ __forceinline__ NearItem near_item(const SegDesc& d, StageP stage, int64_t L0, int64_t L1) {
+__device__ __forceinline__ NearItem near_item(const SegDesc& d, StageP stage, int64_t L0, int64_t L1, uint32_t full) {
   static_assert(VecIO<DT>::V == 8 && kUnroll == 4, "16-bit codes, four vectors per lane");
   const int lane = lane_id();
-  const u16x2 t = {(uint16_t)d.nz_code, (uint16_t)d.nz_code};
+  // per half: |code| <= nz_code exactly when bit 15 of (code - (nz_code + 1)) differs
+  // from the sign bit (the 16-bit difference of two values below 0x8000 borrows
+  // exactly when the magnitude is below t1; a set sign bit flips bit 15)
+  const uint32_t t1 = (uint32_t)(d.nz_code + 1) & 0xFFFFu;
+  const u16x2 t = {(uint16_t)t1, (uint16_t)t1};
   uint32_t mask = 0;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
@@ -1036,21 +1040,25 @@ __device__ __forceinline__ NearItem near_item(const SegDesc& d, StageP stage, in
     const uint32_t rw[4] = {rq.x, rq.y, rq.z, rq.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      // per half: 1 where the magnitude code is above the threshold code
-      const u16x2 mag = __builtin_bit_cast(u16x2, rw[j] & 0x7FFF7FFFu);
-      const uint32_t over = pk_nonzero16(__builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(mag, t)));
-      mask |= (over ^ 0x00010001u) << (u * 4 + j);
+      const u16x2 diff = __builtin_bit_cast(u16x2, rw[j]) - t;
+      // the flags at bits 0 and 16, then at bits u*4+j and 16+u*4+j
+      const u16x2 f = (diff ^ __builtin_bit_cast(u16x2, rw[j])) >> (u16x2){15, 15};
+      mask |= __builtin_bit_cast(uint32_t, f) << (u * 4 + j);
     }
   }
-  // only the elements inside the item (a partial last vector or item), and none
-  // when no magnitude is near zero (nz_code < 0)
-  uint32_t valid = 0;
+  // only the elements inside the item: a lane's full vectors are inside it; a
+  // partial or absent vector keeps the elements before L1.  None when no
+  // magnitude is near zero (nz_code < 0).
+  uint32_t valid = 0xFFFFFFFFu;
+  if (full != (1u << kUnroll) - 1) {
+    valid = 0;
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t left = L1 - (L0 + (int64_t)(u * 64 + lane) * 8);  // elements of vector u inside the item
-    const uint32_t lo = left >= 7 ? 0xFu : (left > 0 ? (1u << ((left + 1) >> 1)) - 1u : 0u);  // elements 2j < left
-    const uint32_t hi = left >= 8 ? 0xFu : (left > 1 ? (1u << (left >> 1)) - 1u : 0u);        // elements 2j + 1 < left
-    valid |= (lo << (u * 4)) | (hi << (16 + u * 4));
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t left = L1 - (L0 + (int64_t)(u * 64 + lane) * 8);  // elements of vector u inside the item
+      const uint32_t lo = left >= 7 ? 0xFu : (left > 0 ? (1u << ((left + 1) >> 1)) - 1u : 0u);  // elements 2j < left
+      const uint32_t hi = left >= 8 ? 0xFu : (left > 1 ? (1u << (left >> 1)) - 1u : 0u);        // elements 2j + 1 < left
+      valid |= ((full >> u) & 1u) ? 0x000F000Fu << (u * 4) : (lo << (u * 4)) | (hi << (16 + u * 4));
+    }
   }
   mask &= d.nz_code < 0 ? 0u : valid;
   NearItem o;
@@ -1063,12 +1071,12 @@ __device__ __forceinline__ NearItem near_item(const SegDesc& d, StageP stage, in
   const uint32_t ix = wave_incl_scan(x), iy = wave_incl_scan(y);
   const uint32_t tx = (uint32_t)__builtin_amdgcn_readlane((int)ix, 63), ty = (uint32_t)__builtin_amdgcn_readlane((int)iy, 63);
   const uint32_t ex = ix - x, ey = iy - y;
-  const uint32_t t0 = tx & 0xFFFFu, t1 = tx >> 16, t2 = ty & 0xFFFFu;
+  const uint32_t t0 = tx & 0xFFFFu, t1c = tx >> 16, t2 = ty & 0xFFFFu;
   const uint32_t p0 = ex & 0xFFFFu, p1 = t0 + (ex >> 16);
-  const uint32_t p2 = t0 + t1 + (ey & 0xFFFFu), p3 = t0 + t1 + t2 + (ey >> 16);
+  const uint32_t p2 = t0 + t1c + (ey & 0xFFFFu), p3 = t0 + t1c + t2 + (ey >> 16);
   o.preA = p0 | (p1 << 16);
   o.preB = p2 | (p3 << 16);
-  o.total = uniform(t0 + t1 + t2 + (ty >> 16));
+  o.total = uniform(t0 + t1c + t2 + (ty >> 16));
   return o;
 }
 
@@ -1106,9 +1114,11 @@ __device__ __forceinline__ void near_entries(const NearItem& ni, uint64_t slow, 
   using T = typename E::T;
   const int lane = lane_id();
   uint32_t part = 0;  // slots of the vectors that phase A left to vec_tail
+  if (full != (1u << kUnroll) - 1) {
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u)
-    if (!((full >> u) & 1u)) part |= 0x000F000Fu << (u * 4);
+    for (int u = 0; u < kUnroll; ++u)
+      if (!((full >> u) & 1u)) part |= 0x000F000Fu << (u * 4);
+  }
   uint32_t cand = ni.mask & ((uint32_t)slow | part);
   while (__ballot(cand != 0)) {
     const bool act = cand != 0;
@@ -1760,7 +1770,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
         if (!dense && !(d.flags & kFlagInputSelect))
           sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, sb, ba, br);
         NearItem ni{};
-        if constexpr (NZ) ni = near_item<DT>(d, stage, L0, L1);
+        if constexpr (NZ) ni = near_item<DT>(d, stage, L0, L1, full_now);
         const uint64_t slow = phase_a_any<DT>(d, L0, R0, stage, full_now, acc, careful);
         if constexpr (NZ) near_entries<DT>(ni, slow, full_now, stage, sink);
         if (__ballot(slow != 0)) {
