@@ -383,6 +383,22 @@ def main():
         stream.synchronize()
         lat.append(time.perf_counter() - t0)
     us_sync = 1e6 * statistics.median(lat)
+    # the drop-in (kernelverse_amd.verdict._compare_tensors, what the reference's callers invoke, GCR:672-786)
+    # end to end: job planning, workspace sizing, the launches, the synchronisation and the meta dict
+    dropin = None
+    if n_pairs == 1:
+        g0, r0, tol0 = pairs[0]
+        for _ in range(3):
+            verdict._compare_tensors(g0, r0, "output", tol0, policy)
+        dl = []
+        for _ in range(20):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            verdict._compare_tensors(g0, r0, "output", tol0, policy)
+            dl.append(time.perf_counter() - t0)
+        dropin = {"us_per_call_median": round(1e6 * statistics.median(dl), 1), "calls": len(dl),
+                  "call": "kernelverse_amd.verdict._compare_tensors(gen, ref, 'output', tolerance, policy)",
+                  "raw_us_per_verdict_synchronous": round(us_sync, 1)}
     main_ms = [a.elapsed_time(b) for a, b in evs]
     main_avg = sum(main_ms) / len(main_ms)
     recs = [_lib.KvvResult.from_buffer_copy(host.numpy().tobytes(), i * rec_size) for i in range(n_pairs)]
@@ -418,6 +434,7 @@ def main():
             "kernel_avg_us": round(main_avg * 1e3, 2),
             "algorithmic_bytes": bytes_read,
         },
+        "dropin": dropin,
         "verdict_check": {"mismatch_count": sum(r.mismatch_count for r in recs),
                           "ulp_hist_b0_b1_b2": [sum(r.ulp_hist[k] for r in recs) for k in range(3)],
                           "finite_violations": sum(r.finite_violations for r in recs),

@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import threading
 from typing import Any, Dict, List, Optional, Sequence, Tuple
 
 import torch
@@ -352,6 +353,43 @@ def _run_jobs(jobs: List[_Job]) -> None:
             raise _lib.KvvLibraryError(f"the device verdict of {j.path} reported status {j.record.status}")
 
 
+class _Buffers:
+    """The workspace and the pinned record buffer of one (device, stream), kept between calls.
+
+    Every call synchronises its stream before it returns, so consecutive calls
+    on one stream can reuse both; the lock serialises threads that share the
+    stream.  Each grows to the largest call seen (``release_buffers`` frees them)."""
+
+    __slots__ = ("lock", "ws", "out")
+
+    def __init__(self):
+        self.lock = threading.Lock()
+        self.ws = None
+        self.out = None
+
+
+_BUFFERS: Dict[Tuple[int, int], _Buffers] = {}
+_BUFFERS_LOCK = threading.Lock()
+
+
+def _buffers_for(dev: torch.device, stream: int) -> _Buffers:
+    key = (dev.index, stream)
+    b = _BUFFERS.get(key)
+    if b is None:
+        with _BUFFERS_LOCK:
+            b = _BUFFERS.setdefault(key, _Buffers())
+    return b
+
+
+def release_buffers() -> None:
+    """Frees the workspaces and record buffers the drop-in keeps between calls."""
+    with _BUFFERS_LOCK:
+        for b in _BUFFERS.values():
+            with b.lock:
+                b.ws = b.out = None
+        _BUFFERS.clear()
+
+
 def _launch(jobs: List[_Job]) -> None:
     lib = _lib.load()
     dev = _device_for(*[j.ref for j in jobs], *[j.gen for j in jobs])
@@ -366,8 +404,13 @@ def _launch(jobs: List[_Job]) -> None:
         rts.append(rt)
     n = len(jobs)
     rec_size = ctypes.sizeof(_lib.KvvResult)
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
+    switch = dev.index != torch.cuda.current_device()
+    ctx = torch.cuda.device(dev) if switch else None
+    if ctx is not None:
+        ctx.__enter__()
+    try:
+        cur = torch.cuda.current_stream(dev)
+        stream = cur.cuda_stream
         size = ctypes.c_size_t()
         if n == 1:
             _lib.check(lib.kvv_workspace_size(gts[0], rts[0], jobs[0].kpolicy, ctypes.byref(size)), "kvv_workspace_size")
@@ -375,18 +418,27 @@ def _launch(jobs: List[_Job]) -> None:
             GA, PA = _lib.KvvTensor * n, _lib.KvvPolicy * n
             garr, rarr, parr = GA(*gts), GA(*rts), PA(*[j.kpolicy for j in jobs])
             _lib.check(lib.kvv_batch_workspace_size(n, garr, rarr, parr, ctypes.byref(size)), "kvv_batch_workspace_size")
-        ws = torch.empty(size.value, dtype=torch.uint8, device=dev)
-        # the records are written by the kernels straight into pinned host memory
-        out = torch.empty(rec_size * n, dtype=torch.uint8, pin_memory=True)
-        if n == 1:
-            rc = lib.kvv_verdict(gts[0], rts[0], jobs[0].kpolicy, out.data_ptr(), ws.data_ptr(), size.value, stream)
-            _lib.check(rc, "kvv_verdict")
-        else:
-            rc = lib.kvv_verdict_batch(n, garr, rarr, parr, out.data_ptr(), ws.data_ptr(), size.value, stream)
-            _lib.check(rc, "kvv_verdict_batch")
-        torch.cuda.current_stream(dev).synchronize()
-        host = out.numpy().tobytes()
-    del keep, ws
+        buf = _buffers_for(dev, stream)
+        with buf.lock:
+            if buf.ws is None or buf.ws.numel() < size.value:
+                buf.ws = None
+                buf.ws = torch.empty(max(size.value, 1 << 20), dtype=torch.uint8, device=dev)
+            if buf.out is None or buf.out.numel() < rec_size * n:
+                # the records are written by the kernels straight into pinned host memory
+                buf.out = torch.empty(max(rec_size * n, 64 * rec_size), dtype=torch.uint8, pin_memory=True)
+            ws, out = buf.ws, buf.out
+            if n == 1:
+                rc = lib.kvv_verdict(gts[0], rts[0], jobs[0].kpolicy, out.data_ptr(), ws.data_ptr(), size.value, stream)
+                _lib.check(rc, "kvv_verdict")
+            else:
+                rc = lib.kvv_verdict_batch(n, garr, rarr, parr, out.data_ptr(), ws.data_ptr(), size.value, stream)
+                _lib.check(rc, "kvv_verdict_batch")
+            cur.synchronize()
+            host = ctypes.string_at(out.data_ptr(), rec_size * n)
+    finally:
+        if ctx is not None:
+            ctx.__exit__(None, None, None)
+    del keep
     for i, j in enumerate(jobs):
         j.record = _lib.KvvResult.from_buffer_copy(host, i * rec_size)
 
