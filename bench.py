@@ -386,9 +386,15 @@ def main():
     # the drop-in (kernelverse_amd.verdict._compare_tensors, what the reference's callers invoke, GCR:672-786)
     # end to end: job planning, workspace sizing, the launches, the synchronisation and the meta dict
     dropin = None
-    if n_pairs == 1:
-        g0, r0, tol0 = pairs[0]
-        for _ in range(3):
+    g0, r0, tol0 = pairs[0]
+    try:
+        if n_pairs == 1:
+            verdict._compare_tensors(g0, r0, "output", tol0, policy)
+    except NotImplementedError as e:
+        # float8 e4m3fn: the reference's verdict raises (torch-CPU has no isfinite for it), and so does the drop-in
+        dropin = {"raises": f"NotImplementedError: {e}"}
+    if n_pairs == 1 and dropin is None:
+        for _ in range(2):
             verdict._compare_tensors(g0, r0, "output", tol0, policy)
         dl = []
         for _ in range(20):
