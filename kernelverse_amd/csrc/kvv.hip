@@ -286,7 +286,8 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
 struct WsLayout {
   int64_t run_stride;
   size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample,
-      near_cm, ent, near_wave, ent_fill, near_psum, table, chunk_seg, isel_state, isel_seg, isel_chunk, isel_sums, total;
+      near_cm, ent, near_wave, ent_fill, near_psum, table, chunk_seg, isel_state, isel_seg, isel_chunk, isel_sums, subtab,
+      submm, total;
 };
 
 // Near-zero entries of a single fp16/bf16 pair (kFlagNearEntries): at most
@@ -314,7 +315,8 @@ int64_t run_slot_bound(int64_t item_count) {
 }
 
 WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int64_t nslots, int64_t chunks,
-                          int64_t items, const NearMode& near, bool batch, int64_t nisel = 0, int64_t isel_chunks = 0) {
+                          int64_t items, const NearMode& near, bool batch, int64_t nisel = 0, int64_t isel_chunks = 0,
+                          int rounds = 1) {
   WsLayout L{};
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -346,6 +348,11 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
     L.near_wave = take((size_t)near.waves * 4);
     L.ent_fill = take((size_t)near.waves * 4);
     L.near_psum = take((size_t)kScatterMax * 8);
+  }
+  if (nslots > 0) {
+    // level-1 candidate tables: kSubTab u16 per select round, per array
+    L.subtab = take((size_t)kArrays * chunks * rounds * kSubTab * 2);
+    L.submm = take((size_t)kArrays * chunks * rounds * 256 * 4);
   }
   if (batch) {
     L.table = take((size_t)nseg * sizeof(SegDesc));
@@ -386,10 +393,10 @@ struct NearLaunch {
 // The launches after the main pass, shared by the single and batch paths:
 // run-record fold + first select level (+ small groups) of the abs/rel samples
 // in one launch; with near-zero diagnostics the near-zero sample and its first
-// level; then select levels 1 and 2 and the final read-off of every array.
+// level; then select level 1 and the final read-off of every array.
 int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchunk, int nseg, int64_t total_chunks,
                 int64_t nslots, const NearMode& nm, const WsLayout& L, void* ws, kvv_result* out, hipStream_t st,
-                const std::vector<NearLaunch>& nears, bool stream_groups = false) {
+                const std::vector<NearLaunch>& nears, bool stream_groups = false, int rounds = 1) {
   const bool near = nm.any();
   TailArgs t{};
   if (seg0) t.seg0 = *seg0;
@@ -404,6 +411,11 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   t.arr[1] = at<float>(ws, L.sample_rel);
   t.arr[2] = near ? at<float>(ws, L.near_sample) : nullptr;
   t.slots = at<uint32_t>(ws, L.slots);
+  if (nslots > 0) {
+    t.subtab = at<uint16_t>(ws, L.subtab);
+    t.submm = at<uint32_t>(ws, L.submm);
+    t.total_sub = (total_chunks > 0 ? total_chunks : 1) * rounds;
+  }
   t.item_near = nm.exact ? at<uint32_t>(ws, L.item_near) : nullptr;
   t.item_near_off = nm.exact ? at<uint64_t>(ws, L.item_near_off) : nullptr;
   t.item_near_sum = nm.exact ? at<double>(ws, L.item_near_sum) : nullptr;
@@ -434,7 +446,6 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
       case 0: fn = batch ? tail_kernel<0, true> : tail_kernel<0, false>; break;
       case 1: fn = batch ? tail_kernel<1, true> : tail_kernel<1, false>; break;
       case 2: fn = batch ? tail_kernel<2, true> : tail_kernel<2, false>; break;
-      case 3: fn = batch ? tail_kernel<3, true> : tail_kernel<3, false>; break;
       default: fn = tail_kernel<4, true>; break;  // many-group launches are batches
     }
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
@@ -484,8 +495,6 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
     rc = launch(0, 1, 0, narr);
     if (rc) return rc;
     rc = launch(0, 2, 0, narr);
-    if (rc) return rc;
-    rc = launch(0, 3, 0, narr);
     if (rc) return rc;
   }
   return KVV_OK;
@@ -692,6 +701,7 @@ struct BatchPlan {
   std::vector<int32_t> isel_chunk;    // (segment, chunk of the segment) pairs, grouped like the scans
   std::vector<Group> groups;
   bool stream_groups = false;  // large groups selected one block each (tail level 4)
+  int rounds = 1;              // select rounds per chunk block (every segment of the batch)
   int64_t items = 0, samples = 0, chunks = 0, nslots = 0, run_slots = 0;
   bool near = false;
 };
@@ -725,6 +735,7 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   bp.stream_groups = group_mode;
   const int rounds = chunks1 >= 4 * 8192 ? 4 : (chunks1 >= 2 * 8192 ? 2 : 1);
   static_assert(kMaxSelRounds >= 4, "select rounds");
+  bp.rounds = group_mode ? 1 : rounds;
   for (int i = 0; i < count; ++i) {
     SegDesc& d = segs[i];
     d.sel_rounds = group_mode ? 1 : rounds;
@@ -816,7 +827,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   NearMode near;
   near.exact = bp.near;
   const WsLayout L = workspace_layout(bp.run_slots, bp.samples, nseg, bp.nslots, bp.chunks, bp.items, near, true,
-                                      nisel, isel_chunks);
+                                      nisel, isel_chunks, bp.rounds);
   int rc = check_ws(L, ws, ws_bytes, out);
   if (rc) return rc;
   SegDesc* dtable = at<SegDesc>(ws, L.table);
@@ -883,7 +894,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     }
   }
   return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, near, L, ws, out, st, nears,
-                     bp.stream_groups);
+                     bp.stream_groups, bp.rounds);
 }
 
 }  // namespace
@@ -949,7 +960,7 @@ int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_te
   kvv::NearMode near;
   near.exact = bp.near;
   *bytes = kvv::workspace_layout(bp.run_slots, bp.samples, (int64_t)bp.table.size(), bp.nslots, bp.chunks, bp.items,
-                                 near, true, (int64_t)bp.isel_seg.size(), (int64_t)bp.isel_chunk.size() / 2)
+                                 near, true, (int64_t)bp.isel_seg.size(), (int64_t)bp.isel_chunk.size() / 2, bp.rounds)
                .total;
   return KVV_OK;
 }

@@ -43,10 +43,14 @@ constexpr uint32_t kFlagNearEntries = 0x40000000u;
 constexpr uint32_t kFlagNearAny = KVV_FLAG_NEAR_ZERO | kFlagNearEntries;
 constexpr int64_t kIselChunk = 1 << 17;        // elements per input-select chunk (every element a sample)
 constexpr int64_t kIselChunkSampled = 1 << 15;  // samples per chunk at strided positions (element loads)
-// Per (large segment, array) slot: level-0 histogram (256), level-1 and level-2
-// histograms (2 ranks x 4096 each) and the NaN count.
-constexpr int kH0 = 0, kH1 = 256, kH2 = 256 + 8192, kMisc = 256 + 16384;
+// Per (large segment, array) slot: level-0 histogram (256), level-1 histograms
+// (2 ranks x 4096) and the NaN count.
+constexpr int kH0 = 0, kH1 = 256, kMisc = 256 + 8192;
 constexpr int kSlotWords = kMisc + 64;
+// Level-1 candidates of a select round (kSelChunk samples): its values under the
+// ranks' level-0 prefixes, grouped by (rank, level-1 digit), with the start of
+// every 64th of those 8192 groups (and the total) in a table of kSubTab u16.
+constexpr int kSubTab = 130;
 
 enum Layout { L_CONTIG = 0, L_ROWS = 1, L_GENERIC = 2 };
 enum ScanKind { K_CONTIG = 0, K_ROWS = 1, K_SCALAR = 2 };

@@ -10,13 +10,15 @@
 // fold run records (one segment each), the others select.  A (segment, array)
 // group of at most kSmall samples is selected by one block entirely in
 // registers and LDS (4 digit passes of 8 bits).  A larger group is selected by
-// all of its chunk blocks in three launches, one per digit level of the
-// ordering key: bits 31..24, 23..12 and 11..0.  Each level histograms, in LDS,
-// the digit of the values whose higher digits match the prefix found so far,
-// and adds the block histogram to the group's global histogram; the next
-// level's blocks locate the ranks in it.  A fourth launch (one block per large
-// group) reads the full keys off the three histograms, interpolates like
-// torch.quantile and writes the result.  The main pass cleared the histograms.
+// all of its chunk blocks in three launches.  Level 0 histograms the top 8
+// bits of every value's ordering key into the group's global histogram.  Level
+// 1 locates both ranks' level-0 bins, histograms bits 23..12 of the values
+// under those prefixes, and keeps those values' keys in the round's own span
+// of the sample array, grouped by (rank, level-1 digit), with a small table of
+// where every 64th group starts.  The final launch (one block per large group)
+// locates the 20-bit prefixes, reads only the kept keys of the target groups,
+// counts their last 12 bits in LDS, interpolates like torch.quantile and
+// writes the result.  The main pass cleared the histograms.
 //
 // A launch with at least as many large groups as the device has CUs (a big
 // batch) needs no global histograms or level launches: a contiguous pair's
@@ -31,7 +33,7 @@ struct TailArgs {
   int32_t nseg;
   int32_t reduce_blocks;      // leading blocks that fold run records (reduce_roles per segment), 0 for none
   int32_t reduce_roles;       // 5, or 6 with the near-zero prefix
-  int32_t level;              // select digit level 0, 1 or 2 (small groups are done at level 0)
+  int32_t level;              // select level of the launch: 0 (with the fold and small groups), 1, 2 = final
   int32_t arr_lo;             // select blocks cover arrays [arr_lo, arr_lo + narr)
   int32_t narr;
   int32_t pad;
@@ -40,6 +42,9 @@ struct TailArgs {
   RunCols runs;
   const float* arr[kArrays];
   uint32_t* slots;            // kArrays * kSlotWords words per large segment
+  uint16_t* subtab;           // level-1 candidate tables: kSubTab per select round, per array
+  uint32_t* submm;            // per select round and array: min and max kept key of each of its 128 cells
+  int64_t total_sub;          // select rounds per array (total_chunks * rounds)
   const uint32_t* item_near;
   uint64_t* item_near_off;
   const double* item_near_sum;
@@ -772,43 +777,30 @@ __device__ inline void select_group_stream(const TailArgs& a, const SegDesc& d, 
 // +0 (a near-zero sample built from entries: its zeros were never histogrammed).
 template <int LEVEL>
 __device__ inline void group_state(const uint32_t* slot, const uint64_t rank64[2], uint32_t pfx[2], uint32_t resid[2],
-                                   SelectLds& L, uint32_t zeros_add = 0) {
+                                   SelectLds& L, uint32_t zeros_add = 0, uint32_t* pfx0 = nullptr) {
+  static_assert(LEVEL == 1 || LEVEL == 2, "prefixes after one or two digit levels");
   const int tid = threadIdx.x;
-  uint32_t h0w = 0, h1a[16], h1b[16], h2a[16], h2b[16];
-  if (LEVEL >= 1) h0w = slot[kH0 + tid] + (tid == (int)(0x80000000u >> 24) ? zeros_add : 0u);
+  uint32_t h0w = 0, h1a[16], h1b[16];
+  h0w = slot[kH0 + tid] + (tid == (int)(0x80000000u >> 24) ? zeros_add : 0u);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     if (LEVEL >= 2) {
       h1a[i] = slot[kH1 + tid * 16 + i];
       h1b[i] = slot[kH1 + 4096 + tid * 16 + i];
     }
-    if (LEVEL >= 3) {
-      h2a[i] = slot[kH2 + tid * 16 + i];
-      h2b[i] = slot[kH2 + 4096 + tid * 16 + i];
-    }
   }
-  pfx[0] = pfx[1] = 0u;
   resid[0] = (uint32_t)rank64[0];
   resid[1] = (uint32_t)rank64[1];
   uint32_t bin[2], below[2];
-  if (LEVEL >= 1) {
-    block_find2<1>(&h0w, &h0w, true, resid, bin, below, L.sh);
+  block_find2<1>(&h0w, &h0w, true, resid, bin, below, L.sh);
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      pfx[rr] = bin[rr];
-      resid[rr] -= below[rr];
-    }
+  for (int rr = 0; rr < 2; ++rr) {
+    pfx[rr] = bin[rr];
+    resid[rr] -= below[rr];
+    if (pfx0) pfx0[rr] = bin[rr];
   }
   if (LEVEL >= 2) {
     block_find2<16>(h1a, h1b, pfx[0] == pfx[1], resid, bin, below, L.sh);
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      pfx[rr] = (pfx[rr] << 12) | bin[rr];
-      resid[rr] -= below[rr];
-    }
-  }
-  if (LEVEL >= 3) {
-    block_find2<16>(h2a, h2b, pfx[0] == pfx[1], resid, bin, below, L.sh);
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       pfx[rr] = (pfx[rr] << 12) | bin[rr];
@@ -824,23 +816,55 @@ __device__ __forceinline__ uint32_t entry_zeros(const SegDesc& d, int arr, int64
   return (uint32_t)(count - (int64_t)slot[kMisc + 1]);
 }
 
-// One chunk of a large group at digit level LEVEL: 0 = bits 31..24, 1 = 23..12,
-// 2 = 11..0.  The chunk is d.sel_rounds consecutive rounds of kSelChunk
-// samples, each read with 16-byte loads (thread t takes 4 consecutive values of
-// every 4 * kBlock), histogrammed into one block histogram that is added to the
-// group's once.
+// Exclusive prefix, in place, of a packed block histogram of `nwords` words
+// (two 16-bit counts each, nwords a multiple of kBlock): afterwards each half
+// holds the number of values in lower bins.  Returns the total.  Called by all
+// threads of the block.
+__device__ inline uint32_t block_offsets16(uint32_t* h, int nwords, SelectLds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int per = nwords / kBlock;  // consecutive words per thread (8 or 16)
+  uint32_t sum = 0;
+  for (int k = 0; k < per; ++k) {
+    const uint32_t v = h[tid * per + k];
+    sum += (v & 0xFFFFu) + (v >> 16);
+  }
+  const uint32_t incl = wave_incl_scan(sum);
+  __syncthreads();
+  if (lane == 63) L.misc[w] = incl;
+  __syncthreads();
+  uint32_t base = incl - sum;
+  for (int i = 0; i < w; ++i) base += L.misc[i];
+  const uint32_t total = L.misc[0] + L.misc[1] + L.misc[2] + L.misc[3];
+  for (int k = 0; k < per; ++k) {
+    const uint32_t v = h[tid * per + k];
+    const uint32_t lo = base, hi = base + (v & 0xFFFFu);
+    base = hi + (v >> 16);
+    h[tid * per + k] = lo | (hi << 16);
+  }
+  __syncthreads();
+  return total;
+}
+
+// One chunk of a large group at digit level LEVEL: 0 = bits 31..24 of every
+// value, 1 = bits 23..12 of the values under either rank's level-0 prefix,
+// whose keys are then kept, grouped by (rank, level-1 digit), in the round's
+// own span of the sample array (its values are all in registers by then) with
+// the round's table of group starts.  The chunk is d.sel_rounds consecutive
+// rounds of kSelChunk samples, each read with 16-byte loads (thread t takes 4
+// consecutive values of every 4 * kBlock).  Level 0 histograms the rounds into
+// one block histogram added to the group's once; level 1 adds each round's.
 template <int LEVEL>
 __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr, int64_t count, int64_t c,
                                     SelectLds& L) {
+  static_assert(LEVEL == 0 || LEVEL == 1, "two histogram levels");
   constexpr int PER = kSelChunk / kBlock;  // values per thread and round
   constexpr int NV = PER / 4;
-  constexpr int HS = LEVEL == 2 ? 12 : 24;                     // prefix = key >> HS
-  constexpr int DS = LEVEL == 0 ? 24 : (LEVEL == 1 ? 12 : 0);  // digit = (key >> DS) & DM
+  constexpr int DS = LEVEL == 0 ? 24 : 12;               // digit = (key >> DS) & DM
   constexpr uint32_t DM = LEVEL == 0 ? 255u : 4095u;
   const int tid = threadIdx.x;
   const int rounds = d.sel_rounds;
   uint32_t* slot = a.slots + ((size_t)d.lslot * kArrays + arr) * kSlotWords;
-  const float* v = a.arr[arr] + d.sample_off;
+  float* v = const_cast<float*>(a.arr[arr]) + d.sample_off;
   auto load_round = [&](float (&x)[PER], int64_t c0, int64_t c1) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -862,15 +886,23 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
   int64_t c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
   float x[PER];
   load_round(x, c0, c1);
-  uint64_t rank64[2];
-  float wgt;
-  q99_ranks(count, rank64, wgt);
-  uint32_t pfx[2], resid[2];
-  group_state<LEVEL>(slot, rank64, pfx, resid, L, entry_zeros(d, arr, count, slot));
-  const bool same = pfx[0] == pfx[1];
+  uint32_t pfx[2] = {0u, 0u};
+  bool same = true;
+  if (LEVEL == 1) {
+    uint64_t rank64[2];
+    float wgt;
+    q99_ranks(count, rank64, wgt);
+    uint32_t resid[2];
+    group_state<1>(slot, rank64, pfx, resid, L, entry_zeros(d, arr, count, slot));
+    same = pfx[0] == pfx[1];
+  }
+  // level 1: bins (rank, digit), the second rank's 4096 only when its prefix differs
   const int nwords = LEVEL == 0 ? 128 : (same ? 2048 : 4096);
-  for (int i = tid; i < nwords; i += kBlock) (&L.h[0][0])[i] = 0;
-  __syncthreads();
+  uint32_t* h = &L.h[0][0];
+  if (LEVEL == 0) {
+    for (int i = tid; i < nwords; i += kBlock) h[i] = 0;
+    __syncthreads();
+  }
   uint32_t nans = 0;
   BinRun run0;
 #pragma unroll 1
@@ -881,6 +913,11 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
       c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
       load_round(x, c0, c1);
     }
+    if (LEVEL == 1) {
+      for (int i = tid; i < nwords; i += kBlock) h[i] = 0;
+      __syncthreads();
+    }
+    uint32_t keep = 0;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int64_t idx = c0 + (int64_t)(i >> 2) * (4 * kBlock) + 4 * tid + (i & 3);
@@ -890,42 +927,202 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
       const uint32_t key = fkey(x[i]);
       const uint32_t dig = (key >> DS) & DM;
       if (LEVEL == 0) {
-        run0.add(L.h[0], dig, ok);
+        run0.add(h, dig, ok);
       } else {
-        const uint32_t top = key >> HS;
-        lds_hist_add(L.h[0], dig, ok && top == pfx[0]);
-        if (!same) lds_hist_add(L.h[1], dig, ok && top == pfx[1]);
+        const uint32_t top = key >> 24;
+        const bool m0 = ok && top == pfx[0], m1 = ok && !same && top == pfx[1];
+        lds_hist_add(h, (m1 ? 4096u : 0u) | dig, m0 || m1);
+        keep |= (m0 || m1 ? 1u : 0u) << i;
+      }
+    }
+    if (LEVEL == 1) {
+      __syncthreads();
+      // this round's histogram joins the group's
+      for (int i = tid; i < nwords; i += kBlock) {
+        const uint32_t wv = h[i];
+        uint32_t* dst = slot + kH1 + 2 * i;  // rank 1's bins follow rank 0's (words 2048.. -> bins 4096..)
+        if (wv & 0xFFFFu) atomicAdd(dst, wv & 0xFFFFu);
+        if (wv >> 16) atomicAdd(dst + 1, wv >> 16);
+      }
+      __syncthreads();
+      // the kept keys, grouped by bin, into the round's span of the sample array
+      const uint32_t total = block_offsets16(h, nwords, L);
+      const int64_t sub = (d.chunk_begin + c) * (int64_t)rounds + r;
+      uint16_t* tab = a.subtab + ((size_t)arr * a.total_sub + (size_t)sub) * kSubTab;
+      if (tid < 129) {
+        const int bin = tid * 64;
+        tab[tid] = (uint16_t)(bin < 2 * nwords ? (h[bin >> 1] & 0xFFFFu) : total);
+      }
+      // the smallest and largest kept key of each cell of 64 groups
+      uint32_t* cmin = reinterpret_cast<uint32_t*>(L.part);
+      uint32_t* cmax = cmin + 128;
+      if (tid < 128) {
+        cmin[tid] = 0xFFFFFFFFu;
+        cmax[tid] = 0u;
+      }
+      __syncthreads();  // (the offsets are read before the scatter advances them)
+      uint32_t* out = reinterpret_cast<uint32_t*>(v + c0);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        if ((keep >> i) & 1u) {
+          const uint32_t key = fkey(x[i]);
+          const uint32_t bin = ((key >> 24) == pfx[0] ? 0u : 4096u) | ((key >> 12) & 4095u);
+          const uint32_t sh = (bin & 1u) << 4;
+          const uint32_t old = atomicAdd(&h[bin >> 1], 1u << sh);
+          out[(old >> sh) & 0xFFFFu] = key;
+          atomicMin(&cmin[bin >> 6], key);
+          atomicMax(&cmax[bin >> 6], key);
+        }
+      }
+      __syncthreads();
+      uint32_t* mm = a.submm + ((size_t)arr * a.total_sub + (size_t)sub) * 256;
+      if (tid < 128) {
+        mm[2 * tid] = cmin[tid];
+        mm[2 * tid + 1] = cmax[tid];
       }
     }
   }
   if (LEVEL == 0) {
-    run0.flush(L.h[0]);
+    run0.flush(h);
     nans = block_sum_nan(nans, L);
+    __syncthreads();
+    // add the block histogram to the group's: bins 2w and 2w+1 of word w
+    for (int i = tid; i < nwords; i += kBlock) {
+      const uint32_t wv = h[i];
+      uint32_t* dst = slot + kH0 + 2 * i;
+      if (wv & 0xFFFFu) atomicAdd(dst, wv & 0xFFFFu);
+      if (wv >> 16) atomicAdd(dst + 1, wv >> 16);
+    }
+    if (tid == 0 && nans) atomicAdd(&slot[kMisc], nans);
   }
-  __syncthreads();
-  // add the block histogram to the group's: bins 2w and 2w+1 of word w
-  uint32_t* gh = slot + (LEVEL == 0 ? kH0 : (LEVEL == 1 ? kH1 : kH2));
-  for (int i = tid; i < nwords; i += kBlock) {
-    const uint32_t wv = (&L.h[0][0])[i];
-    const int rr = LEVEL == 0 ? 0 : i / 2048;
-    const int bw = LEVEL == 0 ? i : i % 2048;
-    uint32_t* dst = gh + rr * 4096 + 2 * bw;
-    if (wv & 0xFFFFu) atomicAdd(dst, wv & 0xFFFFu);
-    if (wv >> 16) atomicAdd(dst + 1, wv >> 16);
-  }
-  if (LEVEL == 0 && tid == 0 && nans) atomicAdd(&slot[kMisc], nans);
 }
 
-// After the last level: one block per large group reads the full keys off the
-// histograms and finishes the group.
+// The final read-off of a large group (one block): the 20-bit prefixes and
+// residual ranks from the group's two histograms, then the last 12 bits from
+// the kept keys of the target (rank, level-1 digit) groups only: each round's
+// table bounds the 64 groups around the target, a block prefix over the rounds
+// spreads those keys over all threads, and the keys under the prefix are
+// counted in LDS (per-thread run merging: the target often holds one repeated
+// value).  Ranks under different prefixes take one pass each.
 __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr, int64_t count, SelectLds& L) {
+  const int tid = threadIdx.x;
   const uint32_t* slot = a.slots + ((size_t)d.lslot * kArrays + arr) * kSlotWords;
   const bool has_nan = slot[kMisc] != 0;
   uint64_t rank64[2];
   float wgt;
   q99_ranks(count, rank64, wgt);
-  uint32_t key[2], resid[2];
-  group_state<3>(slot, rank64, key, resid, L, entry_zeros(d, arr, count, slot));
+  uint32_t pfx[2], resid[2], p0[2];
+  group_state<2>(slot, rank64, pfx, resid, L, entry_zeros(d, arr, count, slot), p0);
+  uint32_t key0 = 0u, key1 = 0u;
+  if (!has_nan) {
+    const int rounds = d.sel_rounds;
+    const int64_t nsub = (count + kSelChunk - 1) / kSelChunk;
+    const uint16_t* tab0 = a.subtab + ((size_t)arr * a.total_sub + (size_t)d.chunk_begin * rounds) * kSubTab;
+    const uint32_t* keys = reinterpret_cast<const uint32_t*>(a.arr[arr] + d.sample_off);
+    uint32_t* H = &L.h[0][0];                              // 4096 bins, one per word
+    uint32_t* pre = reinterpret_cast<uint32_t*>(L.part);   // round prefix (256 + 1) and starts (255)
+    uint32_t* beg = pre + 257;
+    const int passes = pfx[0] == pfx[1] ? 1 : 2;
+#pragma unroll 1
+    for (int rr = 0; rr < passes; ++rr) {
+      for (int i = tid; i < 4096; i += kBlock) H[i] = 0;
+      const uint32_t pr = rr == 0 ? pfx[0] : pfx[1];
+      const uint32_t group = (p0[0] != p0[1] && rr == 1 ? 4096u : 0u) | (pr & 4095u);
+      const int cell = (int)(group >> 6);
+      // one value throughout the target's cell (e.g. equal power-of-two steps): that is the key
+      const uint32_t* mm0 = a.submm + ((size_t)arr * a.total_sub + (size_t)d.chunk_begin * rounds) * 256;
+      uint32_t lo_key = 0xFFFFFFFFu, hi_key = 0u;
+      for (int64_t k = tid; k < nsub; k += kBlock) {
+        const uint32_t a0 = mm0[(size_t)k * 256 + 2 * cell], a1 = mm0[(size_t)k * 256 + 2 * cell + 1];
+        lo_key = a0 < lo_key ? a0 : lo_key;
+        hi_key = a1 > hi_key ? a1 : hi_key;
+      }
+      lo_key = wave_min(lo_key);
+      hi_key = wave_max(hi_key);
+      __syncthreads();
+      if ((tid & 63) == 0) {
+        L.misc[tid >> 6] = lo_key;
+        L.sh[tid >> 6] = hi_key;
+      }
+      __syncthreads();
+      for (int w = 0; w < kWaves; ++w) {
+        lo_key = L.misc[w] < lo_key ? L.misc[w] : lo_key;
+        hi_key = L.sh[w] > hi_key ? L.sh[w] : hi_key;
+      }
+      __syncthreads();
+      if (lo_key == hi_key) {
+        if (passes == 1 || rr == 0) key0 = lo_key;
+        if (passes == 1 || rr == 1) key1 = lo_key;
+        continue;
+      }
+      BinRun32 run;
+#pragma unroll 1
+      for (int64_t s0 = 0; s0 < nsub; s0 += 255) {
+        const int nb = nsub - s0 < 255 ? (int)(nsub - s0) : 255;
+        uint32_t lo = 0, len = 0;
+        if (tid < nb) {
+          const uint16_t* t = tab0 + (size_t)(s0 + tid) * kSubTab;
+          lo = t[cell];
+          len = (uint32_t)t[cell + 1] - lo;
+        }
+        const uint32_t incl = wave_incl_scan(len);
+        __syncthreads();  // (pre/beg of the previous batch are read)
+        if ((tid & 63) == 63) L.misc[tid >> 6] = incl;
+        __syncthreads();
+        uint32_t base = incl - len;
+        for (int w = 0; w < (tid >> 6); ++w) base += L.misc[w];
+        if (tid < nb) {
+          pre[tid] = base;
+          beg[tid] = lo;
+        }
+        if (tid == 0) pre[nb] = L.misc[0] + L.misc[1] + L.misc[2] + L.misc[3];
+        __syncthreads();
+        const uint32_t total = pre[nb];
+        // 8 positions per thread at a time: their loads are all in flight together
+#pragma unroll 1
+        for (uint32_t f0 = 0; f0 < total; f0 += 8 * kBlock) {
+          uint32_t kk[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const uint32_t f = f0 + (uint32_t)(u * kBlock + tid);
+            kk[u] = 0u;
+            if (f < total) {
+              int lo_k = 0, hi_k = nb - 1;  // the round holding flat position f: pre[k] <= f < pre[k + 1]
+              while (lo_k < hi_k) {
+                const int mid = (lo_k + hi_k + 1) >> 1;
+                if (pre[mid] <= f) lo_k = mid; else hi_k = mid - 1;
+              }
+              kk[u] = keys[(size_t)(s0 + lo_k) * kSelChunk + beg[lo_k] + (f - pre[lo_k])];
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const uint32_t f = f0 + (uint32_t)(u * kBlock + tid);
+            run.add(H, kk[u] & 4095u, f < total && (kk[u] >> 12) == pr);
+          }
+        }
+      }
+      run.flush(H);
+      __syncthreads();
+      uint32_t hc[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) hc[i] = H[tid * 16 + i];
+      const uint32_t r_this = rr == 0 ? resid[0] : resid[1];
+      uint32_t rs[2] = {r_this, passes == 1 ? resid[1] : r_this};
+      uint32_t bin[2], below[2];
+      block_find2<16>(hc, hc, true, rs, bin, below, L.sh);
+      if (passes == 1) {
+        key0 = (pfx[0] << 12) | bin[0];
+        key1 = (pfx[1] << 12) | bin[1];
+      } else if (rr == 0) {
+        key0 = (pfx[0] << 12) | bin[0];
+      } else {
+        key1 = (pfx[1] << 12) | bin[0];
+      }
+      __syncthreads();
+    }
+  }
+  const uint32_t key[2] = {key0, key1};
   finalize_group(a, d, arr, count, key, wgt, has_nan, L);
 }
 
@@ -1064,8 +1261,11 @@ __device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
 }
 
 #ifdef KVV_COMMON_KERNELS
-// Level 0 also folds run records (leading blocks) and selects small groups;
-// "level" 4 selects the large groups of a many-group launch (select_group_stream).
+// LEVEL 0: the first launch: leading blocks fold run records, trailing blocks
+// place near-zero entries, the others run select level 0 and select small
+// groups.  LEVEL 1: select level 1.  LEVEL 2: the final read-off, by the first
+// chunk block of each large group.
+// "Level" 4 selects the large groups of a many-group launch (select_group_stream).
 // BATCH: the segments come from the device table; otherwise the single pair's
 // descriptor is a kernel argument, read with scalar loads.
 template <int LEVEL, bool BATCH>
@@ -1102,11 +1302,14 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
     if (LEVEL == small_level && c == 0 && count <= kSmall) select_small(a, d, arr, count, lds.s);
     return;
   }
-  if (LEVEL == 3) {
+  if constexpr (LEVEL == 0) {
+    if (c * d.sel_rounds * (int64_t)kSelChunk >= count) return;
+    select_chunk<0>(a, d, arr, count, c, lds.s);
+  } else if constexpr (LEVEL == 1) {
+    if (c * d.sel_rounds * (int64_t)kSelChunk >= count) return;
+    select_chunk<1>(a, d, arr, count, c, lds.s);
+  } else if constexpr (LEVEL == 2) {
     if (c == 0) select_final(a, d, arr, count, lds.s);
-    return;
   }
-  if (c * d.sel_rounds * (int64_t)kSelChunk >= count) return;
-  select_chunk<LEVEL>(a, d, arr, count, c, lds.s);
 }
 #endif  // KVV_COMMON_KERNELS
