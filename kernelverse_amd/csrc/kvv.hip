@@ -446,6 +446,7 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
       case 0: fn = batch ? tail_kernel<0, true> : tail_kernel<0, false>; break;
       case 1: fn = batch ? tail_kernel<1, true> : tail_kernel<1, false>; break;
       case 2: fn = batch ? tail_kernel<2, true> : tail_kernel<2, false>; break;
+      case 3: fn = tail_kernel<3, false>; break;  // single pairs only
       default: fn = tail_kernel<4, true>; break;  // many-group launches are batches
     }
     hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
@@ -453,7 +454,9 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
     return KVV_OK;
   };
   // (with near-zero entries the first launch's trailing blocks build the near-zero sample)
-  int rc = launch(nseg * t.reduce_roles, 0, 0, 2, scatter);
+  // a single pair whose main pass did select level 0 of abs/rel starts at level 1 there
+  const bool main_hist = seg0 && (seg0->flags & kFlagMainHist);
+  int rc = launch(nseg * t.reduce_roles, main_hist ? 3 : 0, 0, 2, scatter);
   if (rc) return rc;
   if (stream_groups) {
     rc = launch(0, 4, 0, 2);
@@ -492,7 +495,8 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   }
   if (nslots > 0) {
     const int narr = near ? 3 : 2;
-    rc = launch(0, 1, 0, narr);
+    if (!main_hist) rc = launch(0, 1, 0, narr);
+    else if (near) rc = launch(0, 1, 2, 1);  // abs/rel took level 1 in the first launch
     if (rc) return rc;
     rc = launch(0, 2, 0, narr);
     if (rc) return rc;
@@ -615,6 +619,19 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   const WsLayout L = single_layout(d, g);
   rc = check_ws(L, ws, ws_bytes, out);
   if (rc) return rc;
+  // A large group of a vector layout: the main pass's blocks histogram select
+  // level 0 of abs/rel (two 16-bit LDS counts per word: a block's samples must
+  // stay below 2^16), so the tail starts at level 1 for them.  Elements wider
+  // than 16 bits keep the histogram in a sample buffer, so only when every
+  // element is a sample (no buffer in use).
+  if (nslots > 0 && scan_kind(d) != K_SCALAR && (elem_size(d.dtype) <= 2 || d.m == d.n)) {
+    int64_t max_ipw = g.ipw;
+    if (g.rounds.rounds > 1)
+      for (int r = 0; r < g.rounds.rounds; ++r) max_ipw = g.rounds.round_ipw[r] > max_ipw ? g.rounds.round_ipw[r] : max_ipw;
+    const int64_t elems = max_ipw * kWaves * (int64_t)d.item_elems;
+    const int64_t per_block = d.m == d.n ? elems : elems * d.m / d.n + 2;
+    if (per_block < 65536) d.flags |= kFlagMainHist;
+  }
   // one run record per block: its waves fold theirs (a single-segment launch)
   d.run_base = 0;
   d.run_ipb = g.ipw * kWaves;
@@ -632,6 +649,16 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     a.item_near = g.near.exact ? at<uint32_t>(ws, L.item_near) : nullptr;
     a.zero_ptr = at<uint4>(ws, L.slots);
     a.zero_n4 = (int64_t)(L.slot_bytes / 16);
+    a.slots = nullptr;
+    if (d.flags & kFlagMainHist) {
+      // the main pass adds into the slots: they are cleared by a launch before it
+      const int64_t n4 = a.zero_n4;
+      const int64_t blocks = (n4 + kBlock * 4 - 1) / (kBlock * 4);
+      hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, st, a.zero_ptr, n4);
+      KVV_HIP(hipGetLastError());
+      a.zero_n4 = 0;
+      a.slots = at<uint32_t>(ws, L.slots);
+    }
     if (g.near.entries) {
       a.ent = at<uint2>(ws, L.ent);
       a.near_wave = at<uint32_t>(ws, L.near_wave);

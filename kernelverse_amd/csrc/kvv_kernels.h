@@ -41,11 +41,18 @@ constexpr uint32_t kFlagInputSelect = 0x80000000u;  // SegDesc.flags: abs/rel p9
 // the other near-zero elements are the zeros of the compacted array (GCR:525-529)
 constexpr uint32_t kFlagNearEntries = 0x40000000u;
 constexpr uint32_t kFlagNearAny = KVV_FLAG_NEAR_ZERO | kFlagNearEntries;
+// SegDesc.flags: a single pair whose main pass also histograms the top 8 key bits of its abs/rel
+// samples (select level 0) into the select slots, which a launch before it cleared
+constexpr uint32_t kFlagMainHist = 0x20000000u;
 constexpr int64_t kIselChunk = 1 << 17;        // elements per input-select chunk (every element a sample)
 constexpr int64_t kIselChunkSampled = 1 << 15;  // samples per chunk at strided positions (element loads)
-// Per (large segment, array) slot: level-0 histogram (256), level-1 histograms
+// Per (large segment, array) slot: level-0 histogram (256), its kH0Copies
+// copies that the main pass's blocks add into (block b into copy b mod
+// kH0Copies: the bins every block touches, e.g. the zeros, would otherwise
+// serialise 768 device-scope atomics on one address), level-1 histograms
 // (2 ranks x 4096) and the NaN count.
-constexpr int kH0 = 0, kH1 = 256, kMisc = 256 + 8192;
+constexpr int kH0Copies = 16;
+constexpr int kH0 = 0, kH0R = 256, kH1 = 256 + kH0Copies * 256, kMisc = kH1 + 8192;
 constexpr int kSlotWords = kMisc + 64;
 // Level-1 candidates of a select round (kSelChunk samples): its values under the
 // ranks' level-0 prefixes, grouped by (rank, level-1 digit), with the start of
@@ -152,6 +159,7 @@ struct ScanArgs {
   uint32_t* ent_fill;
   uint32_t ent_quota;
   uint32_t pad_ent;
+  uint32_t* slots;         // kFlagMainHist: the select slots (abs, rel) the blocks' level-0 histograms join
 };
 
 // Per-lane accumulators.  Counts live in the per-wave LDS counters instead.
@@ -1207,28 +1215,74 @@ struct SampleBuf {
 template <int DT>
 struct SampleWords {
   static constexpr bool codes = sizeof(typename Elem<DT>::T) <= 4;
+  // codes of at most 16 bits share one word (generated code in the low half), so the
+  // buffer's second word array is not needed
+  static constexpr int W = Elem<DT>::width;
+  static constexpr bool one = codes && W <= 16;
+  static constexpr int words = one ? 1 : 2;
 };
 
 // Writes the buffered positions out (coalesced), finishing their values first
 // when the buffer holds codes.  d is the segment the positions belong to.
+// kFlagMainHist: a block's level-0 histograms of its abs/rel samples, two
+// 16-bit counts per LDS word (256 bins per array), and their NaN counts.
+struct MainHist {
+  uint32_t* h;    // [2][128] in LDS
+  uint32_t* nan;  // [2] in LDS
+};
+
+// Adds every active lane's value to array k's block histogram: one aggregated
+// add when the wave's values share a bin (e.g. the zeros of identical pairs),
+// else one LDS atomic per lane.  Called by every lane of the wave.
+__device__ __forceinline__ void main_hist_add(const MainHist& mh, int k, float v, bool act) {
+  const bool isn = v != v;
+  const uint64_t nb = __ballot(act && isn);
+  if (nb && lane_id() == 0) atomicAdd(&mh.nan[k], (uint32_t)__popcll(nb));
+  const bool ok = act && !isn;
+  const uint32_t bin = fkey(v) >> 24;
+  const uint64_t m = __ballot(ok);
+  if (!m) return;
+  const int l0 = __ffsll((long long)m) - 1;
+  const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane((int)bin, l0);
+  const uint64_t same = __ballot(ok && bin == b0);
+  uint32_t* h = mh.h + k * 128;
+  if (same == m) {
+    if (lane_id() == l0) atomicAdd(&h[b0 >> 1], (uint32_t)__popcll(m) << ((b0 & 1u) << 4));
+  } else if (ok) {
+    atomicAdd(&h[bin >> 1], 1u << ((bin & 1u) << 4));
+  }
+}
+
 template <int DT, int MODE>
 __device__ __forceinline__ void sbuf_store(const SegDesc& d, SampleBuf& b, KVV_LDS uint32_t* ba, KVV_LDS uint32_t* br,
-                                           float* sabs, float* srel, Acc& acc) {
+                                           float* sabs, float* srel, Acc& acc, const MainHist& mh) {
   using T = typename Elem<DT>::T;
   if (b.at0 != kNone) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (uint32_t k = (uint32_t)lane_id(); k < b.fill; k += 64) {
-      float adf, rel;
-      if constexpr (SampleWords<DT>::codes) {
-        sample_value<DT, MODE>(d, (T)ba[k], (T)br[k], acc, adf, rel);
-      } else {
-        adf = __uint_as_float(ba[k]);
-        rel = __uint_as_float(br[k]);
+    const bool hist = (d.flags & kFlagMainHist) != 0;
+    for (uint32_t k0 = 0; k0 < b.fill; k0 += 64) {
+      const uint32_t k = k0 + (uint32_t)lane_id();
+      const bool act = k < b.fill;
+      float adf = 0.0f, rel = 0.0f;
+      if (act) {
+        if constexpr (SampleWords<DT>::one) {
+          const uint32_t wv = ba[k];
+          sample_value<DT, MODE>(d, (T)wv, (T)(wv >> SampleWords<DT>::W), acc, adf, rel);
+        } else if constexpr (SampleWords<DT>::codes) {
+          sample_value<DT, MODE>(d, (T)ba[k], (T)br[k], acc, adf, rel);
+        } else {
+          adf = __uint_as_float(ba[k]);
+          rel = __uint_as_float(br[k]);
+        }
+        sabs[b.at0 + k] = adf;
+        srel[b.at0 + k] = rel;
       }
-      sabs[b.at0 + k] = adf;
-      srel[b.at0 + k] = rel;
+      if (hist) {
+        main_hist_add(mh, 0, adf, act);
+        main_hist_add(mh, 1, rel, act);
+      }
     }
   }
   b.at0 = kNone;
@@ -1240,14 +1294,18 @@ __device__ __forceinline__ void sbuf_store(const SegDesc& d, SampleBuf& b, KVV_L
 template <int DT, int MODE>
 __device__ __forceinline__ void sbuf_put(const SegDesc& d, SampleBuf& b, uint64_t at, int c, uint32_t w0,
                                          uint32_t w1, KVV_LDS uint32_t* ba, KVV_LDS uint32_t* br, float* sabs,
-                                         float* srel, Acc& acc) {
+                                         float* srel, Acc& acc, const MainHist& mh) {
   if (b.at0 != kNone && (at != b.at0 + b.fill || b.fill + (uint32_t)c > (uint32_t)kSampleBuf))
-    sbuf_store<DT, MODE>(d, b, ba, br, sabs, srel, acc);
+    sbuf_store<DT, MODE>(d, b, ba, br, sabs, srel, acc, mh);
   if (b.at0 == kNone) b.at0 = at;
   const int lane = lane_id();
   if (lane < c) {
-    ba[b.fill + lane] = w0;
-    br[b.fill + lane] = w1;
+    if constexpr (SampleWords<DT>::one) {
+      ba[b.fill + lane] = w0 | (w1 << SampleWords<DT>::W);
+    } else {
+      ba[b.fill + lane] = w0;
+      br[b.fill + lane] = w1;
+    }
   }
   b.fill = uniform(b.fill + (uint32_t)c);
   b.at0 = uniform(b.at0);
@@ -1273,7 +1331,7 @@ __device__ __forceinline__ typename Elem<DT>::T vec_code(const uint4& q, int e) 
 // take phase A's packed dot form, which is only accurate to 7.2e-7).
 template <int DT, int MODE>
 __device__ __forceinline__ void dense_samples(const SegDesc& d, int64_t L0, int64_t L1, StageP stage, Acc& acc,
-                                              float* sabs, float* srel) {
+                                              float* sabs, float* srel, const MainHist& mh) {
   using E = Elem<DT>;
   constexpr int V = VecIO<DT>::V;
   constexpr int S = V >= 4 ? 4 : V;  // floats per store
@@ -1299,6 +1357,19 @@ __device__ __forceinline__ void dense_samples(const SegDesc& d, int64_t L0, int6
         xa[j] = fa;
         xr[j] = fr;
         if (v0 + k + j < L1) {
+          if (d.flags & kFlagMainHist) {
+            // one LDS atomic per value (this loop is per lane)
+            const float vv[2] = {fa, fr};
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              if (vv[q] != vv[q]) {
+                atomicAdd(&mh.nan[q], 1u);
+              } else {
+                const uint32_t bin = fkey(vv[q]) >> 24;
+                atomicAdd(&mh.h[q * 128 + (bin >> 1)], 1u << ((bin & 1u) << 4));
+              }
+            }
+          }
           const double g64 = E::f64(gc), r64 = E::f64(rc);
           acc.s[4] = fma(g64, g64, acc.s[4]);
           acc.s[5] = fma(r64, r64, acc.s[5]);
@@ -1329,7 +1400,7 @@ __device__ __forceinline__ void dense_samples(const SegDesc& d, int64_t L0, int6
 template <int DT, int MODE>
 __device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_t L1, StageP stage, Acc& acc,
                                             float* sabs, float* srel, SampleCursor& cur, SampleBuf& sb,
-                                            KVV_LDS uint32_t* ba, KVV_LDS uint32_t* br) {
+                                            KVV_LDS uint32_t* ba, KVV_LDS uint32_t* br, const MainHist& mh) {
   using IO = VecIO<DT>;
   using T = typename IO::T;
   constexpr int V = IO::V;
@@ -1368,7 +1439,7 @@ __device__ __forceinline__ void sample_item(const SegDesc& d, int64_t L0, int64_
         w1 = __float_as_uint(rel);
       }
     }
-    sbuf_put<DT, MODE>(d, sb, d.sample_off + cur.i, c, w0, w1, ba, br, sabs, srel, acc);
+    sbuf_put<DT, MODE>(d, sb, d.sample_off + cur.i, c, w0, w1, ba, br, sabs, srel, acc, mh);
     const uint32_t offl = (uint32_t)__builtin_amdgcn_readlane((int)off, c - 1);
     uint32_t nr = (uint32_t)__builtin_amdgcn_readlane((int)rem, c - 1) + smod;
     uint64_t nidx = (uint64_t)L0 + offl + d.s_div;
@@ -1551,20 +1622,26 @@ __device__ inline void fold_block_record(const LdsRecord* rec, const RunCols& ou
 // vectors of each tensor per lane), its queue of stage positions (NQ = 64 lanes
 // x kQSlots), its sample buffer (two words for each of kSampleBuf consecutive
 // sample positions) and its counters.  Waves never touch each other's part.
-template <int SW, int NQ>
+template <int SW, int NQ, int SBW>
 struct ScanShared {
   uint32_t done;  // waves of the block that have left their record (single-segment launches)
   uint4 stage[kWaves][SW];
   uint16_t queue[kWaves][NQ];
-  uint32_t sbuf[kWaves][2][kSampleBuf];
+  uint32_t sbuf[kWaves][SBW][kSampleBuf];
   uint32_t wcnt[kWaves][WC_COUNT];
+  // kFlagMainHist: the block's level-0 histograms (2 x 128 words) and NaN counts (2)
+  // (SBW == 2: in wave 0's sample buffer, which a dense segment, the only kind
+  // those element types histogram, never fills)
+  uint32_t hist0[SBW == 1 ? 2 * 128 + 2 : 1];
+  static constexpr bool hist_in_sbuf = SBW != 1;
 };
 
 template <int DT, int KIND>
 struct ScanLds {
   static constexpr bool vec = KIND != K_SCALAR;
   // (the scalar kind stages nothing, but its waves leave their run records there)
-  using type = ScanShared<vec ? 2 * kUnroll * 64 : (kColU32 * 4 + kColU64 * 8 + 15) / 16, vec ? 64 * kQSlots : 2>;
+  using type = ScanShared<vec ? 2 * kUnroll * 64 : (kColU32 * 4 + kColU64 * 8 + 15) / 16, vec ? 64 * kQSlots : 2,
+                         SampleWords<DT>::words>;
 };
 
 // Per-item near-zero count of the wave (feeds the compacted-rank prefix of near_kernel).
@@ -1640,6 +1717,18 @@ __device__ inline void block_record_part(const ScanArgs& a, SM& sm, Acc& acc, ui
   LdsRecord rec[kWaves];
   for (int x = 0; x < kWaves; ++x) rec[x] = rec_of(x);
   fold_block_record(rec, a.runs, blockIdx.x);
+  if (a.slots) {
+    // kFlagMainHist: the block's level-0 histograms and NaN counts join the group's
+    const int lane = lane_id();
+    const uint32_t* hb = SM::hist_in_sbuf ? &sm.sbuf[0][0][0] : &sm.hist0[0];
+    for (int i = lane; i < 256; i += 64) {
+      const uint32_t wv = hb[i];
+      uint32_t* dst = a.slots + (size_t)(i >> 7) * kSlotWords + kH0R + (blockIdx.x % kH0Copies) * 256 + 2 * (i & 127);
+      if (wv & 0xFFFFu) atomicAdd(dst, wv & 0xFFFFu);
+      if (wv >> 16) atomicAdd(dst + 1, wv >> 16);
+    }
+    if (lane < 2 && hb[256 + lane]) atomicAdd(a.slots + (size_t)lane * kSlotWords + kMisc, hb[256 + lane]);
+  }
 }
 
 // NZ: a single fp16/bf16 pair whose near-zero diagnostics are taken as entries
@@ -1657,6 +1746,12 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
   if (lane < WC_COUNT) wc[lane] = 0;
   if constexpr (!BATCH) {
     if (tid == 0) sm.done = 0;
+  }
+  uint32_t* const hist_base = SampleWords<DT>::one ? &sm.hist0[0] : &sm.sbuf[0][0][0];
+  const MainHist mh{hist_base, hist_base + 256};
+  if constexpr (!BATCH) {
+    if (a.slots)
+      for (int i = tid; i < 258; i += kBlock) hist_base[i] = 0;
     __syncthreads();
   }
   // the select histograms and counters of this call (and a near-zero sample
@@ -1731,7 +1826,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
   sb.at0 = kNone;
   sb.fill = 0;
   KVV_LDS uint32_t* ba = (KVV_LDS uint32_t*)sm.sbuf[w][0];
-  KVV_LDS uint32_t* br = (KVV_LDS uint32_t*)sm.sbuf[w][1];
+  KVV_LDS uint32_t* br = (KVV_LDS uint32_t*)sm.sbuf[w][SampleWords<DT>::words - 1];
   // one pass per run of items of one segment (a single-segment launch has one);
   // the prefetched registers are dead between runs, where the record is written
   for (int64_t it = i0;;) {
@@ -1772,7 +1867,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
         }
         // (an input-select segment's samples and sampled sums come from the input-select kernels)
         if (!dense && !(d.flags & kFlagInputSelect))
-          sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, sb, ba, br);
+          sample_item<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, cur, sb, ba, br, mh);
         NearItem ni{};
         if constexpr (NZ) ni = near_item<DT>(d, stage, L0, L1, full_now);
         const uint64_t slow = phase_a_any<DT>(d, L0, R0, stage, full_now, acc, careful);
@@ -1795,12 +1890,12 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
           sink.run_near = uniform(sink.run_near + ni.total);
         }
         if (dense && !(d.flags & kFlagInputSelect))
-          dense_samples<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel);
+          dense_samples<DT, MODE>(d, L0, L1, stage, acc, a.sample_abs, a.sample_rel, mh);
       }
       if (d.flags & KVV_FLAG_NEAR_ZERO) near_item_count(a, it, acc, wc, near_prev);
     }
     // the run's buffered samples join its record
-    if constexpr (KIND != K_SCALAR) sbuf_store<DT, MODE>(d, sb, ba, br, a.sample_abs, a.sample_rel, acc);
+    if constexpr (KIND != K_SCALAR) sbuf_store<DT, MODE>(d, sb, ba, br, a.sample_abs, a.sample_rel, acc, mh);
     if constexpr (BATCH) {
       flush_run(acc, wc, ColSink{&a.runs, run_slot(d, run_start)}, base);
       if (it >= i1) break;

@@ -780,8 +780,10 @@ __device__ inline void group_state(const uint32_t* slot, const uint64_t rank64[2
                                    SelectLds& L, uint32_t zeros_add = 0, uint32_t* pfx0 = nullptr) {
   static_assert(LEVEL == 1 || LEVEL == 2, "prefixes after one or two digit levels");
   const int tid = threadIdx.x;
-  uint32_t h0w = 0, h1a[16], h1b[16];
-  h0w = slot[kH0 + tid] + (tid == (int)(0x80000000u >> 24) ? zeros_add : 0u);
+  uint32_t h1a[16], h1b[16];
+  uint32_t h0w = slot[kH0 + tid] + (tid == (int)(0x80000000u >> 24) ? zeros_add : 0u);
+#pragma unroll
+  for (int r = 0; r < kH0Copies; ++r) h0w += slot[kH0R + r * 256 + tid];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     if (LEVEL >= 2) {
@@ -1261,23 +1263,33 @@ __device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
 }
 
 #ifdef KVV_COMMON_KERNELS
+// Clears n4 16-byte words (the select slots of a single pair whose main pass
+// adds into them); a kernel rather than a memset, so a captured graph replays it.
+__global__ __launch_bounds__(kBlock) void fill_zero_kernel(uint4* p, int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kBlock)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
 // LEVEL 0: the first launch: leading blocks fold run records, trailing blocks
 // place near-zero entries, the others run select level 0 and select small
-// groups.  LEVEL 1: select level 1.  LEVEL 2: the final read-off, by the first
-// chunk block of each large group.
+// groups.  LEVEL 3: the first launch of a single pair whose main pass did
+// level 0 of its abs/rel samples (kFlagMainHist): as LEVEL 0, with select
+// level 1 for those arrays.  LEVEL 1: select level 1.  LEVEL 2: the final
+// read-off, by the first chunk block of each large group.
 // "Level" 4 selects the large groups of a many-group launch (select_group_stream).
 // BATCH: the segments come from the device table; otherwise the single pair's
 // descriptor is a kernel argument, read with scalar loads.
 template <int LEVEL, bool BATCH>
 __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
   __shared__ TailLds lds;
+  constexpr bool kFirst = LEVEL == 0 || LEVEL == 3;
   const int64_t b = blockIdx.x;
-  if (LEVEL == 0 && b < a.reduce_blocks) {
+  if (kFirst && b < a.reduce_blocks) {
     reduce_segment<BATCH>(a, (int)(b / a.reduce_roles), (int)(b % a.reduce_roles), lds.r);
     return;
   }
   const int64_t sb = b - a.reduce_blocks;
-  if (LEVEL == 0 && !BATCH && sb >= (int64_t)a.narr * a.total_chunks) {
+  if (kFirst && !BATCH && sb >= (int64_t)a.narr * a.total_chunks) {
     // the trailing blocks of a single pair's first launch place its near-zero entries
     near_scatter(a, (int)(sb - (int64_t)a.narr * a.total_chunks), lds.s);
     return;
@@ -1299,13 +1311,13 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
   if (count <= kSmall || d.lslot < 0) {
     // a near-zero sample built from entries is complete only after the first launch
     const int small_level = arr == 2 && (d.flags & kFlagNearEntries) ? 1 : 0;
-    if (LEVEL == small_level && c == 0 && count <= kSmall) select_small(a, d, arr, count, lds.s);
+    if ((kFirst ? 0 : LEVEL) == small_level && c == 0 && count <= kSmall) select_small(a, d, arr, count, lds.s);
     return;
   }
   if constexpr (LEVEL == 0) {
     if (c * d.sel_rounds * (int64_t)kSelChunk >= count) return;
     select_chunk<0>(a, d, arr, count, c, lds.s);
-  } else if constexpr (LEVEL == 1) {
+  } else if constexpr (LEVEL == 1 || LEVEL == 3) {
     if (c * d.sel_rounds * (int64_t)kSelChunk >= count) return;
     select_chunk<1>(a, d, arr, count, c, lds.s);
   } else if constexpr (LEVEL == 2) {
