@@ -207,6 +207,7 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
   d.nz_code = near_code(r->dtype, d.nz_abs);
   d.dtype = r->dtype;
   d.item_elems = item_elems_for(r->dtype);
+  d.row_items = 0;
 
   // joint coalescing: drop size-1 dims, merge i into i+1 when both strides chain
   int64_t sz[KVV_MAX_DIMS], gs[KVV_MAX_DIMS], rs[KVV_MAX_DIMS];
@@ -242,6 +243,9 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
       ok = ok && ((gs[i] * es) % 16 == 0) && ((rs[i] * es) % 16 == 0);
     }
     d.vec = ok;
+    // one outer dim and rows of whole items: each item lies in one row
+    if (ok && nd == 2 && d.row_len % d.item_elems == 0 && d.row_len / d.item_elems < (1ll << 31))
+      d.row_items = (int32_t)(d.row_len / d.item_elems);
   } else {
     d.layout = L_GENERIC;
     d.dims.ndim = nd;

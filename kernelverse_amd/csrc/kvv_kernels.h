@@ -106,7 +106,7 @@ struct SegDesc {
   int32_t isel_slot;      // input-select state of the segment (kFlagInputSelect), else -1
   int32_t isel_chunk0;    // its first input-select chunk (batch-wide numbering)
   int32_t nz_code;        // kFlagNearEntries: largest magnitude code with |value| <= nz_abs, -1 for none
-  int32_t pad_nz;
+  int32_t row_items;      // L_ROWS with one outer dim and rows of whole items: items per row, else 0
   int64_t run_slot0;      // first run slot of this segment (a multiple of 4)
   int64_t row_len;        // L_ROWS: contiguous inner length
   Dims dims;              // L_ROWS: outer dims; L_GENERIC: all dims
@@ -470,12 +470,48 @@ __device__ __forceinline__ uint4 stage_vec(StageP stage, int slot) {
 }
 
 // Issues the 16-byte loads of one item (kUnroll vectors per thread per tensor).
+// The (row, item of the row) of the next item a wave loads, for rows made of
+// whole items (d.row_items > 0): the item's offsets are then one wave-uniform
+// base plus the lane's position, with no per-lane division.
+struct RowCursor {
+  int64_t row;
+  int32_t col_item;
+};
+
+__device__ __forceinline__ RowCursor row_cursor_at(const SegDesc& d, int64_t item) {
+  RowCursor c{0, 0};
+  if (d.row_items > 0) {
+    c.row = item / d.row_items;
+    c.col_item = (int32_t)(item - c.row * d.row_items);
+  }
+  return c;
+}
+
 template <int DT, int KIND>
-__device__ __forceinline__ uint32_t load_item(const SegDesc& d, int64_t L0, int64_t L1, uint4* gv, uint4* rv) {
+__device__ __forceinline__ uint32_t load_item(const SegDesc& d, int64_t L0, int64_t L1, uint4* gv, uint4* rv,
+                                              RowCursor* rc = nullptr) {
   using IO = VecIO<DT>;
   using T = typename IO::T;
   constexpr int V = IO::V;
   uint32_t full = 0;
+  if constexpr (KIND == K_ROWS) {
+    if (rc && d.row_items > 0) {
+      // every vector of the item lies in row rc->row (no partial vectors: n is whole items)
+      const int64_t col0 = (int64_t)rc->col_item * d.item_elems;
+      const int64_t og0 = rc->row * d.dims.gstr[0] + col0, or0 = rc->row * d.dims.rstr[0] + col0;
+      if (++rc->col_item == d.row_items) {
+        rc->col_item = 0;
+        ++rc->row;
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t off = (int64_t)(u * 64 + lane_id()) * V;
+        gv[u] = nt_load16(reinterpret_cast<const T*>(d.g) + og0 + off);
+        rv[u] = nt_load16(reinterpret_cast<const T*>(d.r) + or0 + off);
+      }
+      return (1u << kUnroll) - 1;
+    }
+  }
   // rows: one division per lane and item; a lane's later vectors step the
   // (row, column) pair, rows being at least one step (64 vectors) long
   int64_t row = 0, col = 0;
@@ -1840,9 +1876,10 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
     SampleCursor cur = cursor_at(d, base);
     uint4 gv[kUnroll], rv[kUnroll];
     uint32_t full = 0;
+    RowCursor rcur = row_cursor_at(d, run_start - d.item_begin);
     if constexpr (KIND != K_SCALAR) {
       const int64_t L1 = base + d.item_elems < d.n ? base + d.item_elems : d.n;
-      full = load_item<DT, KIND>(d, base, L1, gv, rv);
+      full = load_item<DT, KIND>(d, base, L1, gv, rv, &rcur);
     }
     for (; it < run_end; ++it) {
       const int64_t L0 = (it - d.item_begin) * (int64_t)d.item_elems;
@@ -1863,7 +1900,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
         // the next item of the run: its loads fly while this one finishes
         if (it + 1 < run_end) {
           const int64_t N1 = L1 + d.item_elems < d.n ? L1 + d.item_elems : d.n;
-          full = load_item<DT, KIND>(d, L1, N1, gv, rv);
+          full = load_item<DT, KIND>(d, L1, N1, gv, rv, &rcur);
         }
         // (an input-select segment's samples and sampled sums come from the input-select kernels)
         if (!dense && !(d.flags & kFlagInputSelect))
