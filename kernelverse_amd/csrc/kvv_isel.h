@@ -33,7 +33,6 @@
 // (sample_pair), so the result equals the selection over sample arrays.
 
 constexpr int kIselStage = 512;          // per-wave LDS stage of the gather, values per array
-constexpr uint32_t kZeroKey = 0x80000000u;  // fkey(+0.0f)
 
 // Per-segment state (u32 words), cleared by the main pass.
 enum IselWord {

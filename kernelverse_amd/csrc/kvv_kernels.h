@@ -58,6 +58,9 @@ constexpr int kSlotWords = kMisc + 64;
 // ranks' level-0 prefixes, grouped by (rank, level-1 digit), with the start of
 // every 64th of those 8192 groups (and the total) in a table of kSubTab u16.
 constexpr int kSubTab = 130;
+// fkey(+0.0f), the abs and rel diffs of identical pairs.  Select level 1
+// leaves these exact zeros out of its histograms and candidates.
+constexpr uint32_t kZeroKey = 0x80000000u;
 
 enum Layout { L_CONTIG = 0, L_ROWS = 1, L_GENERIC = 2 };
 enum ScanKind { K_CONTIG = 0, K_ROWS = 1, K_SCALAR = 2 };

@@ -458,7 +458,8 @@ __device__ __forceinline__ uint32_t packed_count(const uint32_t* h, uint32_t bin
 // last bin.  One DPP scan per histogram, three barriers.  Called by all threads.
 template <int PER>
 __device__ inline void block_find2(const uint32_t* cA, const uint32_t* cB, bool one, const uint32_t resid[2],
-                                   uint32_t bin[2], uint32_t below[2], uint32_t* sh) {
+                                   uint32_t bin[2], uint32_t below[2], uint32_t* sh, uint32_t* cnt = nullptr,
+                                   const uint32_t* expect = nullptr, uint32_t* added = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   uint32_t sA = 0, sB = 0;
 #pragma unroll
@@ -476,7 +477,7 @@ __device__ inline void block_find2(const uint32_t* cA, const uint32_t* cB, bool 
   }
   if (tid == 0) {
     sh[8] = sh[10] = PER * kBlock - 1;
-    sh[9] = sh[11] = 0;
+    sh[9] = sh[11] = sh[12] = sh[13] = 0;
   }
   __syncthreads();
   uint32_t baseA = 0, baseB = 0;
@@ -484,20 +485,46 @@ __device__ inline void block_find2(const uint32_t* cA, const uint32_t* cB, bool 
     baseA += sh[i];
     baseB += sh[kWaves + i];
   }
+  uint32_t eA = baseA + iA - sA, eB = baseB + iB - sB;  // counts of the bins before the thread's
+  // expect: totals that A and B must reach (0: none); the shortfall joins bin 0,
+  // the first of thread 0, which moves every other thread's bins up by it
+  uint32_t zA = 0, zB = 0;
+  if (expect) {
+    uint32_t tA = 0, tB = 0;
+    for (int i = 0; i < kWaves; ++i) {
+      tA += sh[i];
+      tB += sh[kWaves + i];
+    }
+    zA = expect[0] ? expect[0] - tA : 0u;
+    zB = one ? zA : (expect[1] ? expect[1] - tB : 0u);
+    if (added) {
+      added[0] = zA;
+      added[1] = zB;
+    }
+    if (tid > 0) {
+      eA += zA;
+      eB += zB;
+    } else {
+      sA += zA;
+      sB += zB;
+    }
+  }
+  const uint32_t z0A = tid == 0 ? zA : 0u, z0B = tid == 0 ? zB : 0u;
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
     const bool useB = rr == 1 && !one;
     const uint32_t sum = useB ? sB : sA;
-    uint32_t e = useB ? baseB + iB - sB : baseA + iA - sA;
+    uint32_t e = useB ? eB : eA;
     const uint32_t r = resid[rr];
     if (sum > 0 && e <= r && r < e + sum) {
-      uint32_t b = tid * PER;
+      uint32_t b = tid * PER, bc = 0;
       bool found = false;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
-        const uint32_t c = useB ? cB[i] : cA[i];
+        const uint32_t c = (useB ? cB[i] : cA[i]) + (i == 0 ? (useB ? z0B : z0A) : 0u);
         if (!found && r < e + c) {
           b = tid * PER + i;
+          if (cnt) bc = c;
           found = true;
         } else if (!found) {
           e += c;
@@ -505,6 +532,7 @@ __device__ inline void block_find2(const uint32_t* cA, const uint32_t* cB, bool 
       }
       sh[8 + 2 * rr] = b;
       sh[9 + 2 * rr] = e;
+      if (cnt) sh[12 + rr] = bc;
     }
   }
   __syncthreads();
@@ -512,6 +540,10 @@ __device__ inline void block_find2(const uint32_t* cA, const uint32_t* cB, bool 
   below[0] = sh[9];
   bin[1] = sh[10];
   below[1] = sh[11];
+  if (cnt) {
+    cnt[0] = sh[12];
+    cnt[1] = sh[13];
+  }
 }
 
 // torch's quantile interpolation between the order statistics (NaN when the
@@ -775,9 +807,14 @@ __device__ inline void select_group_stream(const TailArgs& a, const SegDesc& d, 
 // histogram words the block needs are loaded in one go.
 // zeros_add: values the level-0 histogram does not hold but the array does, all
 // +0 (a near-zero sample built from entries: its zeros were never histogrammed).
+// zeros (LEVEL 2): the exact zeros under the +0 prefix, which level 1 left out
+// of its histograms and candidates: the +0 bin's level-0 count minus the
+// level-1 counts under it.  They join digit 0 here, and the final read-off
+// adds them to the target group when that is the zeros' group.
 template <int LEVEL>
 __device__ inline void group_state(const uint32_t* slot, const uint64_t rank64[2], uint32_t pfx[2], uint32_t resid[2],
-                                   SelectLds& L, uint32_t zeros_add = 0, uint32_t* pfx0 = nullptr) {
+                                   SelectLds& L, uint32_t zeros_add = 0, uint32_t* pfx0 = nullptr,
+                                   uint32_t* zeros = nullptr) {
   static_assert(LEVEL == 1 || LEVEL == 2, "prefixes after one or two digit levels");
   const int tid = threadIdx.x;
   uint32_t h1a[16], h1b[16];
@@ -793,8 +830,8 @@ __device__ inline void group_state(const uint32_t* slot, const uint64_t rank64[2
   }
   resid[0] = (uint32_t)rank64[0];
   resid[1] = (uint32_t)rank64[1];
-  uint32_t bin[2], below[2];
-  block_find2<1>(&h0w, &h0w, true, resid, bin, below, L.sh);
+  uint32_t bin[2], below[2], bcnt[2];
+  block_find2<1>(&h0w, &h0w, true, resid, bin, below, L.sh, bcnt);
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
     pfx[rr] = bin[rr];
@@ -802,7 +839,13 @@ __device__ inline void group_state(const uint32_t* slot, const uint64_t rank64[2
     if (pfx0) pfx0[rr] = bin[rr];
   }
   if (LEVEL >= 2) {
-    block_find2<16>(h1a, h1b, pfx[0] == pfx[1], resid, bin, below, L.sh);
+    // the level-1 histogram under the +0 prefix must reach that bin's level-0 count
+    const bool za = pfx[0] == (kZeroKey >> 24);
+    const bool zb = pfx[0] != pfx[1] && pfx[1] == (kZeroKey >> 24);
+    const uint32_t expect[2] = {za ? bcnt[0] : 0u, zb ? bcnt[1] : 0u};
+    uint32_t added[2];
+    block_find2<16>(h1a, h1b, pfx[0] == pfx[1], resid, bin, below, L.sh, nullptr, expect, added);
+    if (zeros) *zeros = za ? added[0] : added[1];
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       pfx[rr] = (pfx[rr] << 12) | bin[rr];
@@ -891,13 +934,22 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
   uint32_t pfx[2] = {0u, 0u};
   bool same = true;
   if (LEVEL == 1) {
+    const uint32_t nan_count = slot[kMisc];  // (read with the group's state, in one round trip)
     uint64_t rank64[2];
     float wgt;
     q99_ranks(count, rank64, wgt);
     uint32_t resid[2];
     group_state<1>(slot, rank64, pfx, resid, L, entry_zeros(d, arr, count, slot));
+    // a NaN among the samples makes the quantile NaN: nothing to locate (the final read-off checks the same count)
+    if (nan_count != 0) return;
     same = pfx[0] == pfx[1];
   }
+  // the keys under each rank's 8-bit prefix, [lo, lo + span); the +0 prefix
+  // leaves out the exact zeros (identical pairs): the final read-off takes their
+  // count from the two histograms instead of keeping them as candidates
+  const uint32_t lo0 = (pfx[0] << 24) + (pfx[0] == (kZeroKey >> 24) ? 1u : 0u);
+  const uint32_t lo1 = (pfx[1] << 24) + (pfx[1] == (kZeroKey >> 24) ? 1u : 0u);
+  const uint32_t span0 = (1u << 24) - (lo0 & 1u), span1 = (1u << 24) - (lo1 & 1u);
   // level 1: bins (rank, digit), the second rank's 4096 only when its prefix differs
   const int nwords = LEVEL == 0 ? 128 : (same ? 2048 : 4096);
   uint32_t* h = &L.h[0][0];
@@ -931,8 +983,9 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
       if (LEVEL == 0) {
         run0.add(h, dig, ok);
       } else {
-        const uint32_t top = key >> 24;
-        const bool m0 = ok && top == pfx[0], m1 = ok && !same && top == pfx[1];
+        // under a rank's prefix: key - lo < span (exact zeros left out of the +0 prefix)
+        const bool m0 = LEVEL == 1 ? ok && key - lo0 < span0 : false;
+        const bool m1 = LEVEL == 1 ? ok && !same && key - lo1 < span1 : false;
         lds_hist_add(h, (m1 ? 4096u : 0u) | dig, m0 || m1);
         keep |= (m0 || m1 ? 1u : 0u) << i;
       }
@@ -1013,8 +1066,8 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
   uint64_t rank64[2];
   float wgt;
   q99_ranks(count, rank64, wgt);
-  uint32_t pfx[2], resid[2], p0[2];
-  group_state<2>(slot, rank64, pfx, resid, L, entry_zeros(d, arr, count, slot), p0);
+  uint32_t pfx[2], resid[2], p0[2], zeros;
+  group_state<2>(slot, rank64, pfx, resid, L, entry_zeros(d, arr, count, slot), p0, &zeros);
   uint32_t key0 = 0u, key1 = 0u;
   if (!has_nan) {
     const int rounds = d.sel_rounds;
@@ -1050,6 +1103,11 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
       for (int w = 0; w < kWaves; ++w) {
         lo_key = L.misc[w] < lo_key ? L.misc[w] : lo_key;
         hi_key = L.sh[w] > hi_key ? L.sh[w] : hi_key;
+      }
+      const bool zg = zeros != 0u && pr == (kZeroKey >> 12);  // the target group holds the zeros
+      if (zg) {
+        lo_key = kZeroKey < lo_key ? kZeroKey : lo_key;
+        hi_key = kZeroKey > hi_key ? kZeroKey : hi_key;
       }
       __syncthreads();
       if (lo_key == hi_key) {
@@ -1105,6 +1163,7 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
         }
       }
       run.flush(H);
+      if (zg && tid == 0) atomicAdd(&H[0], zeros);
       __syncthreads();
       uint32_t hc[16];
 #pragma unroll
