@@ -164,10 +164,11 @@ KVV_API int kvv_workspace_size(const kvv_tensor* gen, const kvv_tensor* ref, con
 KVV_API int kvv_verdict(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy,
                 kvv_result* out, void* workspace, size_t workspace_bytes, void* stream);
 
-/* kvv_verdict with hipEventRecord(main_begin) just before and
- * hipEventRecord(main_end) just after the main-pass kernel, on `stream`
- * (either event may be NULL).  Nothing synchronises: the caller reads the
- * elapsed time once the stream has passed the events.  Used to time the
+/* kvv_verdict whose main-pass kernel records its own start in main_begin and
+ * its end in main_end (hipEvent_t, created with timing; either may be NULL),
+ * taken from the kernel's dispatch (hipExtLaunchKernel), so no marker packet
+ * sits between the verdict's launches.  Nothing synchronises: the caller reads
+ * the elapsed time once the stream has passed the kernel.  Used to time the
  * dominant kernel live inside a benchmark's timed region. */
 KVV_API int kvv_verdict_timed(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy,
                               kvv_result* out, void* workspace, size_t workspace_bytes, void* stream,

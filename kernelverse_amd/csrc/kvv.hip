@@ -1,6 +1,7 @@
 // libkvv: MI355X verdict library -- C ABI entry points (include/kvv.h),
 // planning (dimension coalescing, layout and access choice, workspace
 // layout) and the launch sequence of the verdict kernels.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -672,10 +673,16 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
       a.zero2_ptr = at<uint4>(ws, L.near_sample);
       a.zero2_n4 = (int64_t)((align256((size_t)d.m * 4)) / 16);
     }
-    if (ev_begin) KVV_HIP(hipEventRecord(ev_begin, st));
-    hipLaunchKernelGGL(g.scan, dim3((unsigned)g.grid), dim3(kBlock), 0, st, a);
-    KVV_HIP(hipGetLastError());
-    if (ev_end) KVV_HIP(hipEventRecord(ev_end, st));
+    if (ev_begin || ev_end) {
+      // the events take the kernel's own start and end from its dispatch
+      // (no marker packets between the launches of the verdict)
+      void* args[] = {&a};
+      KVV_HIP(hipExtLaunchKernel(reinterpret_cast<const void*>(g.scan), dim3((unsigned)g.grid), dim3(kBlock), args,
+                                 0, st, ev_begin, ev_end, 0));
+    } else {
+      hipLaunchKernelGGL(g.scan, dim3((unsigned)g.grid), dim3(kBlock), 0, st, a);
+      KVV_HIP(hipGetLastError());
+    }
   }
   std::vector<NearLaunch> nears{{near_fn(d.dtype, d.mode), 0, 1, 0, d.item_count}};
   return launch_tail(&d, nullptr, nullptr, 1, d.chunk_count, nslots, g.near, L, ws, out, st, nears);
