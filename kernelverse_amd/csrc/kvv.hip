@@ -626,10 +626,8 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   if (rc) return rc;
   // A large group of a vector layout: the main pass's blocks histogram select
   // level 0 of abs/rel (two 16-bit LDS counts per word: a block's samples must
-  // stay below 2^16), so the tail starts at level 1 for them.  Elements wider
-  // than 16 bits keep the histogram in a sample buffer, so only when every
-  // element is a sample (no buffer in use).
-  if (nslots > 0 && scan_kind(d) != K_SCALAR && (elem_size(d.dtype) <= 2 || d.m == d.n)) {
+  // stay below 2^16), so the tail starts at level 1 for them.
+  if (nslots > 0 && scan_kind(d) != K_SCALAR) {
     int64_t max_ipw = g.ipw;
     if (g.rounds.rounds > 1)
       for (int r = 0; r < g.rounds.rounds; ++r) max_ipw = g.rounds.round_ipw[r] > max_ipw ? g.rounds.round_ipw[r] : max_ipw;

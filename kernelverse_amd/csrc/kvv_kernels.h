@@ -1240,8 +1240,7 @@ __device__ __forceinline__ void sample_value(const SegDesc& d, typename Elem<DT>
 // [at0, at0 + fill).  It is written out (coalesced) when full, at the end of a
 // segment and at the end of the wave's range.  Sample values written to HBM while the scan streams its
 // inputs cost far more read bandwidth than their bytes, so a wave whose samples
-// fit (kSampleBuf) writes them all at the end.
-constexpr int kSampleBuf = 384;
+// fit (SampleWords::cap) writes them all at the end.
 struct SampleBuf {
   uint64_t at0;  // kNone: empty
   uint32_t fill;
@@ -1259,6 +1258,9 @@ struct SampleWords {
   static constexpr int W = Elem<DT>::width;
   static constexpr bool one = codes && W <= 16;
   static constexpr int words = one ? 1 : 2;
+  // positions per wave: two word arrays take fewer, so that a block's LDS
+  // (with its level-0 histograms) stays within three blocks per CU
+  static constexpr int cap = one ? 384 : 320;
 };
 
 // Writes the buffered positions out (coalesced), finishing their values first
@@ -1334,7 +1336,7 @@ template <int DT, int MODE>
 __device__ __forceinline__ void sbuf_put(const SegDesc& d, SampleBuf& b, uint64_t at, int c, uint32_t w0,
                                          uint32_t w1, KVV_LDS uint32_t* ba, KVV_LDS uint32_t* br, float* sabs,
                                          float* srel, Acc& acc, const MainHist& mh) {
-  if (b.at0 != kNone && (at != b.at0 + b.fill || b.fill + (uint32_t)c > (uint32_t)kSampleBuf))
+  if (b.at0 != kNone && (at != b.at0 + b.fill || b.fill + (uint32_t)c > (uint32_t)SampleWords<DT>::cap))
     sbuf_store<DT, MODE>(d, b, ba, br, sabs, srel, acc, mh);
   if (b.at0 == kNone) b.at0 = at;
   const int lane = lane_id();
@@ -1659,20 +1661,17 @@ __device__ inline void fold_block_record(const LdsRecord* rec, const RunCols& ou
 // ------------------------------------------------------------ scan kernel
 // LDS of one scan block: per wave, its item's vectors (SW uint4: kUnroll
 // vectors of each tensor per lane), its queue of stage positions (NQ = 64 lanes
-// x kQSlots), its sample buffer (two words for each of kSampleBuf consecutive
-// sample positions) and its counters.  Waves never touch each other's part.
+// x kQSlots), its sample buffer (SBW words for each of its consecutive sample
+// positions) and its counters.  Waves never touch each other's part.
 template <int SW, int NQ, int SBW>
 struct ScanShared {
   uint32_t done;  // waves of the block that have left their record (single-segment launches)
   uint4 stage[kWaves][SW];
   uint16_t queue[kWaves][NQ];
-  uint32_t sbuf[kWaves][SBW][kSampleBuf];
+  uint32_t sbuf[kWaves][SBW][SBW == 1 ? 384 : 320];
   uint32_t wcnt[kWaves][WC_COUNT];
   // kFlagMainHist: the block's level-0 histograms (2 x 128 words) and NaN counts (2)
-  // (SBW == 2: in wave 0's sample buffer, which a dense segment, the only kind
-  // those element types histogram, never fills)
-  uint32_t hist0[SBW == 1 ? 2 * 128 + 2 : 1];
-  static constexpr bool hist_in_sbuf = SBW != 1;
+  uint32_t hist0[2 * 128 + 2];
 };
 
 template <int DT, int KIND>
@@ -1759,7 +1758,7 @@ __device__ inline void block_record_part(const ScanArgs& a, SM& sm, Acc& acc, ui
   if (a.slots) {
     // kFlagMainHist: the block's level-0 histograms and NaN counts join the group's
     const int lane = lane_id();
-    const uint32_t* hb = SM::hist_in_sbuf ? &sm.sbuf[0][0][0] : &sm.hist0[0];
+    const uint32_t* hb = &sm.hist0[0];
     for (int i = lane; i < 256; i += 64) {
       const uint32_t wv = hb[i];
       uint32_t* dst = a.slots + (size_t)(i >> 7) * kSlotWords + kH0R + (blockIdx.x % kH0Copies) * 256 + 2 * (i & 127);
@@ -1786,7 +1785,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
   if constexpr (!BATCH) {
     if (tid == 0) sm.done = 0;
   }
-  uint32_t* const hist_base = SampleWords<DT>::one ? &sm.hist0[0] : &sm.sbuf[0][0][0];
+  uint32_t* const hist_base = &sm.hist0[0];
   const MainHist mh{hist_base, hist_base + 256};
   if constexpr (!BATCH) {
     if (a.slots)
