@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <limits>
 #include <type_traits>
 
 #include "kvv.h"
@@ -224,53 +225,79 @@ __device__ __forceinline__ int pair_bucket(typename Elem<DT>::T g, typename Elem
 }
 
 // ----------------------------------------------------------------- reductions
+// Wave reductions through DPP: row shifts by 1, 2, 4 and 8, then the row
+// broadcasts of lanes 15 and 31, leave lane 63 with the result of the whole
+// wave, which readlane hands to every lane.  No LDS round trips (a shuffle is
+// a ds_bpermute each), and the tree is fixed, so fp64 sums are reproducible.
+// `ident` fills lanes whose DPP source lies outside the row.
+template <int CTRL, int RM, typename T>
+__device__ __forceinline__ T dpp_move(T v, T ident) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, ident), __builtin_bit_cast(int, v),
+                                                             CTRL, RM, 0xf, false));
+  } else {
+    static_assert(sizeof(T) == 8, "32- or 64-bit lanes");
+    const uint64_t b = __builtin_bit_cast(uint64_t, v), o = __builtin_bit_cast(uint64_t, ident);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)o, (int)(uint32_t)b, CTRL, RM, 0xf, false);
+    const uint32_t hi =
+        (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(o >> 32), (int)(uint32_t)(b >> 32), CTRL, RM, 0xf, false);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+template <typename T>
+__device__ __forceinline__ T lane63(T v) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+  } else {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, T ident, Op op) {
+  v = op(v, dpp_move<0x111, 0xf>(v, ident));  // row_shr:1
+  v = op(v, dpp_move<0x112, 0xf>(v, ident));  // row_shr:2
+  v = op(v, dpp_move<0x114, 0xf>(v, ident));  // row_shr:4
+  v = op(v, dpp_move<0x118, 0xf>(v, ident));  // row_shr:8
+  v = op(v, dpp_move<0x142, 0xa>(v, ident));  // row_bcast:15 into rows 1 and 3
+  v = op(v, dpp_move<0x143, 0xc>(v, ident));  // row_bcast:31 into rows 2 and 3
+  return lane63(v);
+}
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  return wave_reduce(v, (T)0, [](T x, T y) { return x + y; });
 }
 template <typename T>
 __device__ __forceinline__ T wave_max(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    T w = __shfl_xor(v, o);
-    v = w > v ? w : v;
-  }
-  return v;
+  return wave_reduce(v, std::numeric_limits<T>::lowest(), [](T x, T y) { return y > x ? y : x; });
 }
 template <typename T>
 __device__ __forceinline__ T wave_min(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    T w = __shfl_xor(v, o);
-    v = w < v ? w : v;
-  }
-  return v;
+  return wave_reduce(v, std::numeric_limits<T>::max(), [](T x, T y) { return y < x ? y : x; });
 }
 // (key, index) argmax: larger key wins, equal keys -> smaller index.
-__device__ __forceinline__ void wave_argmax(uint32_t& key, uint64_t& idx) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t k = __shfl_xor(key, o);
-    uint64_t i = __shfl_xor(idx, o);
+template <typename I>
+__device__ __forceinline__ void wave_argmax_t(uint32_t& key, I& idx) {
+  auto step = [&](uint32_t k, I i) {
     if (k > key || (k == key && i < idx)) {
       key = k;
       idx = i;
     }
-  }
+  };
+  const I none = std::numeric_limits<I>::max();
+  step(dpp_move<0x111, 0xf>(key, 0u), dpp_move<0x111, 0xf>(idx, none));
+  step(dpp_move<0x112, 0xf>(key, 0u), dpp_move<0x112, 0xf>(idx, none));
+  step(dpp_move<0x114, 0xf>(key, 0u), dpp_move<0x114, 0xf>(idx, none));
+  step(dpp_move<0x118, 0xf>(key, 0u), dpp_move<0x118, 0xf>(idx, none));
+  step(dpp_move<0x142, 0xa>(key, 0u), dpp_move<0x142, 0xa>(idx, none));
+  step(dpp_move<0x143, 0xc>(key, 0u), dpp_move<0x143, 0xc>(idx, none));
+  key = lane63(key);
+  idx = lane63(idx);
 }
-__device__ __forceinline__ void wave_argmax32(uint32_t& key, uint32_t& idx) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t k = __shfl_xor(key, o);
-    const uint32_t i = __shfl_xor(idx, o);
-    if (k > key || (k == key && i < idx)) {
-      key = k;
-      idx = i;
-    }
-  }
-}
+__device__ __forceinline__ void wave_argmax(uint32_t& key, uint64_t& idx) { wave_argmax_t(key, idx); }
+__device__ __forceinline__ void wave_argmax32(uint32_t& key, uint32_t& idx) { wave_argmax_t(key, idx); }
 __device__ __forceinline__ bool better(uint32_t k, uint64_t i, uint32_t bk, uint64_t bi) {
   return k > bk || (k == bk && i < bi);
 }
