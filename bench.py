@@ -10,7 +10,9 @@ to back between two synchronisations; ``value`` is algorithmic input bytes
 (both tensors read once) per second of step time.  Inputs below 512 MiB
 (c0) are evicted from the MALL before every verdict; each verdict is then timed
 with its own pair of events.  ``us_per_verdict_synchronous`` is the latency of
-one verdict issued and waited for on its own, host overheads included.
+one verdict issued and waited for on its own, host overheads included.  The
+latency and drop-in measurements run before the W warm-up and K timed steps:
+the device reaches its full clocks only after some 10 ms of sustained load.
 
 The ``roofline`` object covers the dominant kernel (the main pass): its
 duration is measured live with HIP events that the main-pass launch itself
@@ -336,6 +338,41 @@ def main():
         if rc:
             _lib.check(rc, "kvv_verdict")
 
+    # Single-call measurements first, then the throughput steps.  The device reaches its full clocks only
+    # after some 10 ms of sustained load: on one box back-to-back C1 verdicts took 233 us each for the first
+    # 20 after 5 warm-ups and 206 us from the 50th on, and 234 us again after 0.5 s idle.  The latency and
+    # drop-in calls below (28 verdicts) therefore precede the W warm-up and K timed steps.
+    # latency of one verdict issued and waited for on its own (the reference's usage: one compare, then read)
+    lat = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step()
+        stream.synchronize()
+        lat.append(time.perf_counter() - t0)
+    us_sync = 1e6 * statistics.median(lat)
+    # the drop-in (kernelverse_amd.verdict._compare_tensors, what the reference's callers invoke, GCR:672-786)
+    # end to end: job planning, workspace sizing, the launches, the synchronisation and the meta dict
+    dropin = None
+    g0, r0, tol0 = pairs[0]
+    try:
+        if n_pairs == 1:
+            verdict._compare_tensors(g0, r0, "output", tol0, policy)
+    except NotImplementedError as e:
+        # float8 e4m3fn: the reference's verdict raises (torch-CPU has no isfinite for it), and so does the drop-in
+        dropin = {"raises": f"NotImplementedError: {e}"}
+    if n_pairs == 1 and dropin is None:
+        for _ in range(2):
+            verdict._compare_tensors(g0, r0, "output", tol0, policy)
+        dl = []
+        for _ in range(20):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            verdict._compare_tensors(g0, r0, "output", tol0, policy)
+            dl.append(time.perf_counter() - t0)
+        dropin = {"us_per_call_median": round(1e6 * statistics.median(dl), 1), "calls": len(dl),
+                  "call": "kernelverse_amd.verdict._compare_tensors(gen, ref, 'output', tolerance, policy)",
+                  "raw_us_per_verdict_synchronous": round(us_sync, 1)}
     log(f"[bench] warmup {args.warmup}")
     for _ in range(args.warmup):
         step()
@@ -384,37 +421,6 @@ def main():
             flush.fill_(i & 255)
         step(*evs[i])
     torch.cuda.synchronize()
-    # latency of one verdict issued and waited for on its own (the reference's usage: one compare, then read)
-    lat = []
-    for _ in range(5):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        step()
-        stream.synchronize()
-        lat.append(time.perf_counter() - t0)
-    us_sync = 1e6 * statistics.median(lat)
-    # the drop-in (kernelverse_amd.verdict._compare_tensors, what the reference's callers invoke, GCR:672-786)
-    # end to end: job planning, workspace sizing, the launches, the synchronisation and the meta dict
-    dropin = None
-    g0, r0, tol0 = pairs[0]
-    try:
-        if n_pairs == 1:
-            verdict._compare_tensors(g0, r0, "output", tol0, policy)
-    except NotImplementedError as e:
-        # float8 e4m3fn: the reference's verdict raises (torch-CPU has no isfinite for it), and so does the drop-in
-        dropin = {"raises": f"NotImplementedError: {e}"}
-    if n_pairs == 1 and dropin is None:
-        for _ in range(2):
-            verdict._compare_tensors(g0, r0, "output", tol0, policy)
-        dl = []
-        for _ in range(20):
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            verdict._compare_tensors(g0, r0, "output", tol0, policy)
-            dl.append(time.perf_counter() - t0)
-        dropin = {"us_per_call_median": round(1e6 * statistics.median(dl), 1), "calls": len(dl),
-                  "call": "kernelverse_amd.verdict._compare_tensors(gen, ref, 'output', tolerance, policy)",
-                  "raw_us_per_verdict_synchronous": round(us_sync, 1)}
     main_ms = [a.elapsed_time(b) for a, b in evs]
     main_avg = sum(main_ms) / len(main_ms)
     recs = [_lib.KvvResult.from_buffer_copy(host.numpy().tobytes(), i * rec_size) for i in range(n_pairs)]
