@@ -93,6 +93,14 @@ enum kvv_mode {
                                      inputs instead of from entries recorded in the main pass (see
                                      KVV_STATUS_NEAR_RETRY) */
 
+#define KVV_FLAG_WS_KEPT 0x4u    /* the workspace is the one the previous single-pair verdict on this device was
+                                     given, and nothing has written it since (a caller that keeps one workspace
+                                     per stream, as the Python layer does).  Every single-pair verdict leaves its
+                                     select slots clear; with this flag the next one on the same workspace skips
+                                     clearing them (one launch fewer) when its slots lie where the previous
+                                     call's did.  Without the flag, or on any other workspace, they are cleared.
+                                     No counterpart in the reference (GCR:672-786 allocates per call). */
+
 /* kvv_result.status values. */
 #define KVV_STATUS_NEAR_RETRY 1   /* a single fp16/bf16 pair's near-zero elements with a nonzero abs_diff did not fit
                                      the workspace's entry pool: the near-zero fields are not valid (the others

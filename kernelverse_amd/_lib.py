@@ -23,6 +23,7 @@ F32, F16, BF16, F64, F8E4M3FN, F8E5M2, I8, U8, I16, I32, I64, BOOL, U16, U32, U6
 MODE_ISCLOSE, MODE_MAX_ABS_DIFF = 0, 1
 FLAG_NEAR_ZERO = 0x1
 FLAG_NEAR_EXACT = 0x2
+FLAG_WS_KEPT = 0x4
 # kvv_result.status: the near-zero fields need the exact path (KVV_STATUS_NEAR_RETRY)
 STATUS_NEAR_RETRY = 1
 

@@ -608,7 +608,51 @@ WsLayout single_layout(const SegDesc& d, const SingleGeom& g) {
                           g.near, false);
 }
 
-int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st,
+// ------------------------------------------------------------ kept workspaces
+// Byte ranges of caller workspaces whose select slots a single-pair verdict left
+// clear (its final read-off zeroes them), per device.  KVV_FLAG_WS_KEPT lets the
+// next verdict on the same workspace skip its clearing launch when its slots lie
+// inside that range.  Any call on a workspace first drops its record: whatever
+// the call writes voids it.
+struct KeptRange {
+  int dev;
+  const void* ws;
+  size_t off, len;
+};
+std::mutex g_kept_mu;
+std::vector<KeptRange> g_kept;
+constexpr size_t kKeptMax = 64;
+
+// Drops the record of ws on the current device; returns whether [off, off + len)
+// lay inside it (only asked when the caller set KVV_FLAG_WS_KEPT).
+bool take_kept(const void* ws, size_t off, size_t len) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lock(g_kept_mu);
+  for (size_t i = 0; i < g_kept.size(); ++i) {
+    const KeptRange k = g_kept[i];
+    if (k.dev == dev && k.ws == ws) {
+      g_kept.erase(g_kept.begin() + (std::ptrdiff_t)i);
+      return len > 0 && off >= k.off && off + len <= k.off + k.len;
+    }
+  }
+  return false;
+}
+
+void put_kept(const void* ws, size_t off, size_t len) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  std::lock_guard<std::mutex> lock(g_kept_mu);
+  for (size_t i = 0; i < g_kept.size(); ++i)
+    if (g_kept[i].dev == dev && g_kept[i].ws == ws) {
+      g_kept.erase(g_kept.begin() + (std::ptrdiff_t)i);
+      break;
+    }
+  if (g_kept.size() >= kKeptMax) g_kept.erase(g_kept.begin());
+  g_kept.push_back(KeptRange{dev, ws, off, len});
+}
+
+int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st, bool kept,
                hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr) {
   SegDesc d = d0;
   d.item_begin = 0;
@@ -635,6 +679,9 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     const int64_t per_block = d.m == d.n ? elems : elems * d.m / d.n + 2;
     if (per_block < 65536) d.flags |= kFlagMainHist;
   }
+  const bool main_hist = (d.flags & kFlagMainHist) != 0;
+  // slots left clear by the previous call on this workspace need no clearing launch
+  const bool slots_clear = take_kept(ws, L.slots, L.slot_bytes) && kept && main_hist;
   // one run record per block: its waves fold theirs (a single-segment launch)
   d.run_base = 0;
   d.run_ipb = g.ipw * kWaves;
@@ -653,12 +700,16 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     a.zero_ptr = at<uint4>(ws, L.slots);
     a.zero_n4 = (int64_t)(L.slot_bytes / 16);
     a.slots = nullptr;
-    if (d.flags & kFlagMainHist) {
-      // the main pass adds into the slots: they are cleared by a launch before it
-      const int64_t n4 = a.zero_n4;
-      const int64_t blocks = (n4 + kBlock * 4 - 1) / (kBlock * 4);
-      hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, st, a.zero_ptr, n4);
-      KVV_HIP(hipGetLastError());
+    if (main_hist) {
+      // the main pass adds into the slots: they are cleared by a launch before it,
+      // unless the previous call on this workspace left them clear
+      if (!slots_clear) {
+        const int64_t n4 = a.zero_n4;
+        const int64_t blocks = (n4 + kBlock * 4 - 1) / (kBlock * 4);
+        hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)(blocks > 0 ? blocks : 1)), dim3(kBlock), 0, st,
+                           a.zero_ptr, n4);
+        KVV_HIP(hipGetLastError());
+      }
       a.zero_n4 = 0;
       a.slots = at<uint32_t>(ws, L.slots);
     }
@@ -683,7 +734,10 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
     }
   }
   std::vector<NearLaunch> nears{{near_fn(d.dtype, d.mode), 0, 1, 0, d.item_count}};
-  return launch_tail(&d, nullptr, nullptr, 1, d.chunk_count, nslots, g.near, L, ws, out, st, nears);
+  rc = launch_tail(&d, nullptr, nullptr, 1, d.chunk_count, nslots, g.near, L, ws, out, st, nears);
+  // the final read-off zeroes every slot it read: the next call may skip the clearing
+  if (rc == KVV_OK && main_hist && d.item_count > 0) put_kept(ws, L.slots, L.slot_bytes);
+  return rc;
 }
 
 int single_workspace_bytes(const SegDesc& d, size_t* bytes) {
@@ -956,7 +1010,8 @@ int kvv_verdict(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* 
   kvv::SegDesc d;
   int rc = kvv::plan_single(gen, ref, policy, d);
   if (rc) return rc;
-  return kvv::run_single(d, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  return kvv::run_single(d, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                         (policy->flags & KVV_FLAG_WS_KEPT) != 0);
 }
 
 int kvv_verdict_timed(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy, kvv_result* out,
@@ -965,7 +1020,8 @@ int kvv_verdict_timed(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_po
   int rc = kvv::plan_single(gen, ref, policy, d);
   if (rc) return rc;
   return kvv::run_single(d, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
-                         static_cast<hipEvent_t>(main_begin), static_cast<hipEvent_t>(main_end));
+                         (policy->flags & KVV_FLAG_WS_KEPT) != 0, static_cast<hipEvent_t>(main_begin),
+                         static_cast<hipEvent_t>(main_end));
 }
 
 int kvv_verdict_noalloc(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy, kvv_result* out,
@@ -984,7 +1040,8 @@ int kvv_verdict_noalloc(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_
   void* ws = nullptr;
   rc = kvv::scratch_address(&ws);
   if (rc) return rc;
-  return kvv::run_single(d, out, ws, kvv::kScratchBytes, static_cast<hipStream_t>(stream));
+  // the scratch array is the library's own: only its calls write it
+  return kvv::run_single(d, out, ws, kvv::kScratchBytes, static_cast<hipStream_t>(stream), true);
 }
 
 int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs,
@@ -1006,6 +1063,7 @@ int kvv_verdict_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* r
   kvv::BatchPlan bp;
   int rc = kvv::plan_batch(count, gens, refs, policies, bp);
   if (rc) return rc;
+  kvv::take_kept(workspace, 0, 0);  // a batch writes the workspace its own way
   return kvv::run_batch(bp, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 

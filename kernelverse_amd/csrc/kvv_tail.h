@@ -84,6 +84,7 @@ struct SelectLds {
   uint32_t fill[2];  // input select: compacted values per array
 };
 static_assert(kSelChunk * kMaxSelRounds <= 65535 && kSmall <= 65535, "16-bit block bin counts");
+static_assert(kSlotWords % 4 == 0, "slots are cleared in 16-byte stores");
 
 union TailLds {
   ReduceLds r;
@@ -1185,6 +1186,11 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
   }
   const uint32_t key[2] = {key0, key1};
   finalize_group(a, d, arr, count, key, wgt, has_nan, L);
+  // this block was the slot's last reader: it leaves the slot clear for the next
+  // call on the workspace (KVV_FLAG_WS_KEPT skips the clearing launch then)
+  __syncthreads();
+  uint4* z = reinterpret_cast<uint4*>(const_cast<uint32_t*>(slot));
+  for (int i = tid; i < kSlotWords / 4; i += kBlock) z[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
 // ------------------------------------------------------------ near-zero entries

@@ -358,14 +358,18 @@ class _Buffers:
 
     Every call synchronises its stream before it returns, so consecutive calls
     on one stream can reuse both; the lock serialises threads that share the
-    stream.  Each grows to the largest call seen (``release_buffers`` frees them)."""
+    stream.  Each grows to the largest call seen (``release_buffers`` frees them).
+    ``kept``: the workspace went through a previous call and nothing else writes
+    it, so single-pair calls pass KVV_FLAG_WS_KEPT (the library then skips
+    clearing the select slots that call left clear)."""
 
-    __slots__ = ("lock", "ws", "out")
+    __slots__ = ("lock", "ws", "out", "kept")
 
     def __init__(self):
         self.lock = threading.Lock()
         self.ws = None
         self.out = None
+        self.kept = False
 
 
 _BUFFERS: Dict[Tuple[int, int], _Buffers] = {}
@@ -422,18 +426,25 @@ def _launch(jobs: List[_Job]) -> None:
         with buf.lock:
             if buf.ws is None or buf.ws.numel() < size.value:
                 buf.ws = None
+                buf.kept = False
                 buf.ws = torch.empty(max(size.value, 1 << 20), dtype=torch.uint8, device=dev)
             if buf.out is None or buf.out.numel() < rec_size * n:
                 # the records are written by the kernels straight into pinned host memory
                 buf.out = torch.empty(max(rec_size * n, 64 * rec_size), dtype=torch.uint8, pin_memory=True)
             ws, out = buf.ws, buf.out
             if n == 1:
-                rc = lib.kvv_verdict(gts[0], rts[0], jobs[0].kpolicy, out.data_ptr(), ws.data_ptr(), size.value, stream)
+                pol = _lib.KvvPolicy.from_buffer_copy(jobs[0].kpolicy)
+                if buf.kept:
+                    pol.flags |= _lib.FLAG_WS_KEPT
+                buf.kept = False  # (until this call has gone through)
+                rc = lib.kvv_verdict(gts[0], rts[0], pol, out.data_ptr(), ws.data_ptr(), size.value, stream)
                 _lib.check(rc, "kvv_verdict")
             else:
+                buf.kept = False
                 rc = lib.kvv_verdict_batch(n, garr, rarr, parr, out.data_ptr(), ws.data_ptr(), size.value, stream)
                 _lib.check(rc, "kvv_verdict_batch")
             cur.synchronize()
+            buf.kept = True
             host = ctypes.string_at(out.data_ptr(), rec_size * n)
     finally:
         if ctx is not None:
