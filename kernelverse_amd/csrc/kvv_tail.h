@@ -1125,6 +1125,11 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
           const uint16_t* t = tab0 + (size_t)(s0 + tid) * kSubTab;
           lo = t[cell];
           len = (uint32_t)t[cell + 1] - lo;
+          // the round's own span bounds every read below, whatever the table holds
+          const int64_t left = count - (int64_t)(s0 + tid) * kSelChunk;
+          const uint32_t rsz = left < kSelChunk ? (uint32_t)left : (uint32_t)kSelChunk;
+          lo = lo < rsz ? lo : rsz;
+          len = len <= rsz - lo ? len : rsz - lo;
         }
         const uint32_t incl = wave_incl_scan(len);
         __syncthreads();  // (pre/beg of the previous batch are read)
