@@ -1274,14 +1274,31 @@ __device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
   float* sample = const_cast<float*>(a.arr[2]) + d.sample_off;
   double sum = 0.0;
   uint32_t cnt = 0, nan = 0;
-  // the block's entries, wave after wave, all threads at once (k grows, so the
-  // wave index wi only moves forward)
+  // the block's entries, wave after wave, all threads at once, 8 per thread per
+  // pass with their loads in flight together (k grows, so the wave index wi only
+  // moves forward)
+  constexpr int kEnt = 8;
   int wi = 0;
 #pragma unroll 1
-  for (uint32_t k = tid; k < total; k += kBlock) {
-    while (wi + 1 < w1 - w0 && woff[wi + 1] <= k) ++wi;
-    const uint2 x = a.ent[(size_t)(w0 + wi) * a.ent_quota + (k - woff[wi])];
-    const uint64_t j = wbase[wi] + x.x;
+  for (uint32_t k0 = tid; k0 < total; k0 += kEnt * kBlock) {
+    uint2 xs[kEnt];
+    uint64_t jb[kEnt];
+#pragma unroll
+    for (int u = 0; u < kEnt; ++u) {
+      const uint32_t k = k0 + (uint32_t)u * kBlock;
+      xs[u] = make_uint2(0u, 0u);
+      jb[u] = ~0ull;
+      if (k < total) {
+        while (wi + 1 < w1 - w0 && woff[wi + 1] <= k) ++wi;
+        xs[u] = a.ent[(size_t)(w0 + wi) * a.ent_quota + (k - woff[wi])];
+        jb[u] = wbase[wi];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kEnt; ++u) {
+    if (jb[u] == ~0ull) continue;
+    const uint2 x = xs[u];
+    const uint64_t j = jb[u] + x.x;
     uint64_t i = j;
     bool take = j < c;
     if (strided) {
@@ -1302,6 +1319,7 @@ __device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
       ++cnt;
       if (v != v) ++nan;
       else if (large) atomicAdd(&L.h[0][fkey(v) >> 24], 1u);
+    }
     }
   }
   sum = wave_sum(sum);
