@@ -618,49 +618,6 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   return v;
 }
 
-// Wave totals through the same DPP sweep (lane 63 ends with the sum; the tree
-// is fixed, so fp64 totals are reproducible).  No LDS round trips.
-__device__ __forceinline__ uint64_t wave_total_u64(uint64_t v) {
-  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-#define KVV_DPP_ADD64(ctrl, rm, bc)                                                       \
-  {                                                                                       \
-    const uint32_t ol = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, ctrl, rm, 0xf, bc); \
-    const uint32_t oh = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, ctrl, rm, 0xf, bc); \
-    const uint32_t sl = lo + ol;                                                          \
-    hi = hi + oh + (sl < lo ? 1u : 0u);                                                   \
-    lo = sl;                                                                              \
-  }
-  KVV_DPP_ADD64(0x111, 0xf, true)
-  KVV_DPP_ADD64(0x112, 0xf, true)
-  KVV_DPP_ADD64(0x114, 0xf, true)
-  KVV_DPP_ADD64(0x118, 0xf, true)
-  KVV_DPP_ADD64(0x142, 0xa, false)
-  KVV_DPP_ADD64(0x143, 0xc, false)
-#undef KVV_DPP_ADD64
-  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi, 63) << 32) |
-         (uint32_t)__builtin_amdgcn_readlane((int)lo, 63);
-}
-
-__device__ __forceinline__ double wave_total_f64(double v) {
-#define KVV_DPP_ADDF(ctrl, rm, bc)                                                                 \
-  {                                                                                                \
-    const uint64_t b = (uint64_t)__double_as_longlong(v);                                          \
-    const uint32_t ol = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, ctrl, rm, 0xf, bc); \
-    const uint32_t oh = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), ctrl, rm, 0xf, bc); \
-    v = v + __longlong_as_double((long long)(((uint64_t)oh << 32) | ol));                           \
-  }
-  KVV_DPP_ADDF(0x111, 0xf, true)
-  KVV_DPP_ADDF(0x112, 0xf, true)
-  KVV_DPP_ADDF(0x114, 0xf, true)
-  KVV_DPP_ADDF(0x118, 0xf, true)
-  KVV_DPP_ADDF(0x142, 0xa, false)
-  KVV_DPP_ADDF(0x143, 0xc, false)
-#undef KVV_DPP_ADDF
-  const uint64_t b = (uint64_t)__double_as_longlong(v);
-  return __longlong_as_double((long long)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63) << 32) |
-                                          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63)));
-}
-
 // ------------------------------------------------------------ phase A (SWAR)
 // Phase A classifies every element of a lane's full vectors as "fast" (the
 // pair is bit-identical and finite: abs_diff = rel_diff = 0, ULP bucket 0,
