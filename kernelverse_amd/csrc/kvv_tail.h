@@ -954,6 +954,12 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
   // level 1: bins (rank, digit), the second rank's 4096 only when its prefix differs
   const int nwords = LEVEL == 0 ? 128 : (same ? 2048 : 4096);
   uint32_t* h = &L.h[0][0];
+  // level 1: each wave's kept keys of the round (at most its PER * 64 values)
+  uint32_t* klist = nullptr;
+  if constexpr (LEVEL == 1) {
+    __shared__ uint32_t kl[kWaves][PER * 64];
+    klist = kl[tid >> 6];
+  }
   if (LEVEL == 0) {
     for (int i = tid; i < nwords; i += kBlock) h[i] = 0;
     __syncthreads();
@@ -987,11 +993,26 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
         // under a rank's prefix: key - lo < span (exact zeros left out of the +0 prefix)
         const bool m0 = LEVEL == 1 ? ok && key - lo0 < span0 : false;
         const bool m1 = LEVEL == 1 ? ok && !same && key - lo1 < span1 : false;
-        lds_hist_add(h, (m1 ? 4096u : 0u) | dig, m0 || m1);
         keep |= (m0 || m1 ? 1u : 0u) << i;
       }
     }
+    uint32_t wkept = 0;
     if (LEVEL == 1) {
+      // the wave's kept keys, compacted in lane order into its LDS list; the
+      // histogram and the scatter below then run over the list, every lane busy
+      // (a walk over each thread's 32 values left most lanes idle)
+      const uint32_t nk = (uint32_t)__popc(keep);
+      const uint32_t incl = wave_incl_scan(nk);
+      wkept = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+      uint32_t o = incl - nk;
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        if ((keep >> i) & 1u) klist[o++] = fkey(x[i]);
+      __builtin_amdgcn_wave_barrier();
+      for (uint32_t e = (uint32_t)(tid & 63); e < wkept; e += 64) {
+        const uint32_t key = klist[e];
+        lds_hist_add(h, ((key >> 24) == pfx[0] ? 0u : 4096u) | ((key >> 12) & 4095u), true);
+      }
       __syncthreads();
       // this round's histogram joins the group's
       for (int i = tid; i < nwords; i += kBlock) {
@@ -1018,17 +1039,14 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
       }
       __syncthreads();  // (the offsets are read before the scatter advances them)
       uint32_t* out = reinterpret_cast<uint32_t*>(v + c0);
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        if ((keep >> i) & 1u) {
-          const uint32_t key = fkey(x[i]);
-          const uint32_t bin = ((key >> 24) == pfx[0] ? 0u : 4096u) | ((key >> 12) & 4095u);
-          const uint32_t sh = (bin & 1u) << 4;
-          const uint32_t old = atomicAdd(&h[bin >> 1], 1u << sh);
-          out[(old >> sh) & 0xFFFFu] = key;
-          atomicMin(&cmin[bin >> 6], key);
-          atomicMax(&cmax[bin >> 6], key);
-        }
+      for (uint32_t e = (uint32_t)(tid & 63); e < wkept; e += 64) {
+        const uint32_t key = klist[e];
+        const uint32_t bin = ((key >> 24) == pfx[0] ? 0u : 4096u) | ((key >> 12) & 4095u);
+        const uint32_t sh = (bin & 1u) << 4;
+        const uint32_t old = atomicAdd(&h[bin >> 1], 1u << sh);
+        out[(old >> sh) & 0xFFFFu] = key;
+        atomicMin(&cmin[bin >> 6], key);
+        atomicMax(&cmax[bin >> 6], key);
       }
       __syncthreads();
       uint32_t* mm = a.submm + ((size_t)arr * a.total_sub + (size_t)sub) * 256;
