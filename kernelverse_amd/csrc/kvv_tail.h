@@ -156,15 +156,18 @@ __device__ inline void reduce_counts(const TailArgs& a, const SegDesc& d, int se
   const bool is_max = col_i == CU_MMABS || col_i == CU_MMREL;
   L.pu[threadIdx.x] = is_max ? fold_u32<true>(col, j0, j1) : fold_u32<false>(col, j0, j1);
   __syncthreads();
-  const int tid = threadIdx.x;
-  if (tid < F) {
-    const int c = F0 + tid;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // field i's parts are folded by wave i mod 4: a few parts per lane, then the lanes (DPP)
+  for (int i = tid >> 6; i < F; i += kWaves) {
+    const int c = F0 + i;
+    const bool mx = c == CU_MMABS || c == CU_MMREL;
     uint64_t t = 0;
-    for (int q = 0; q < P; ++q) {
-      const uint64_t v = L.pu[tid * P + q];
-      if (c == CU_MMABS || c == CU_MMREL) t = v > t ? v : t; else t += v;
+    for (int q = lane; q < P; q += 64) {
+      const uint64_t v = L.pu[i * P + q];
+      t = mx ? (v > t ? v : t) : t + v;
     }
-    L.tu[c] = t;
+    t = mx ? wave_max(t) : wave_sum(t);
+    if (lane == 0) L.tu[c] = t;
   }
   __syncthreads();
   kvv_result& o = a.res[d.out_index];
@@ -265,37 +268,27 @@ __device__ inline void reduce_extrema(const TailArgs& a, const SegDesc& d, int64
       }
     }
   }
-  L.pu[tid] = bi;
-  L.pk[tid] = bk;
-  __syncthreads();
-  if (tid < F) {
-    uint32_t tk = 0;
-    uint64_t ti = kNone;
-    for (int q = 0; q < P; ++q) {
-      const uint64_t vi = L.pu[tid * P + q];
-      const uint32_t vk = L.pk[tid * P + q];
-      if (tid < 2) {
-        ti = vi < ti ? vi : ti;
-      } else if (better(vk, vi, tk, ti)) {
-        tk = vk;
-        ti = vi;
-      }
-    }
+  // F * P is the block: wave f holds field f's parts, folded in registers (DPP)
+  static_assert(F == kWaves && P == 64, "one wave per field");
+  uint32_t tk = bk;
+  uint64_t ti = bi;
+  if (f < 2) ti = wave_min(ti); else wave_argmax(tk, ti);
+  if ((tid & 63) == 0) {
     kvv_result& o = a.res[d.out_index];
     const bool imode = d.mode == KVV_MODE_MAX_ABS_DIFF;
-    if (tid == 0) {
+    if (f == 0) {
       o.first_mismatch_index = ti == kNone ? -1 : (int64_t)ti;
-    } else if (tid == 1) {
+    } else if (f == 1) {
       o.first_finite_violation = ti == kNone ? -1 : (int64_t)ti;
     } else if (d.n == 0) {
-      if (tid == 2) {
+      if (f == 2) {
         o.max_abs = 0.0;
         o.max_abs_index = -1;
       } else {
         o.max_rel = 0.0;
         o.max_rel_index = -1;
       }
-    } else if (tid == 2) {
+    } else if (f == 2) {
       o.max_abs = imode ? (double)ikey_value(tk) : (double)fkey_value(tk);
       o.max_abs_index = (int64_t)ti;
     } else {
@@ -307,6 +300,7 @@ __device__ inline void reduce_extrema(const TailArgs& a, const SegDesc& d, int64
 
 __device__ inline void reduce_sums(const TailArgs& a, const SegDesc& d, int64_t nruns, ReduceLds& L) {
   constexpr int F = 7, P = kBlock / F;
+  static_assert(P <= 64, "one part per lane in the combine");
   int f, p;
   int64_t j0, j1;
   role_split<F, P>(nruns, f, p, j0, j1);
@@ -327,10 +321,12 @@ __device__ inline void reduce_sums(const TailArgs& a, const SegDesc& d, int64_t 
   }
   L.pd[tid] = t;
   __syncthreads();
-  if (tid < F) {
-    double u = 0.0;
-    for (int q = 0; q < P; ++q) u += L.pd[tid * P + q];
-    L.td[tid] = u;
+  // field i's parts summed by wave i mod 4 in a fixed tree (DPP): reproducible
+  for (int i = tid >> 6; i < F; i += kWaves) {
+    const int q = tid & 63;
+    double u = q < P ? L.pd[i * P + q] : 0.0;
+    u = wave_sum(u);
+    if (q == 0) L.td[i] = u;
   }
   __syncthreads();
   auto sum = [&](int i) { return L.td[i]; };
