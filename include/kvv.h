@@ -185,7 +185,7 @@ KVV_API int kvv_verdict_timed(const kvv_tensor* gen, const kvv_tensor* ref, cons
 /* kvv_verdict without a workspace argument and without any allocation.
  * No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  The workspace is a 32 MiB array in the
+ * harnesses that forbid hipMalloc).  The workspace is a 64 MiB array in the
  * library's code object, one per GPU, held until the process ends; a verdict
  * whose workspace (kvv_workspace_size) exceeds it fails with
  * KVV_E_WORKSPACE and leaves the stream untouched.  Calls on one GPU share

@@ -115,7 +115,7 @@ EXPORTED = ("kvv_abi_version", "kvv_last_error", "kvv_workspace_size", "kvv_verd
             "kvv_verdict_noalloc", "kvv_batch_workspace_size", "kvv_verdict_batch")
 
 # the fixed workspace of kvv_verdict_noalloc (bytes)
-NOALLOC_SCRATCH_BYTES = 32 << 20
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _lib = None
 

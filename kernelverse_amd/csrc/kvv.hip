@@ -357,7 +357,7 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
   if (nslots > 0) {
     // level-1 candidate tables: kSubTab u16 per select round, per array
     L.subtab = take((size_t)kArrays * chunks * rounds * kSubTab * 2);
-    L.submm = take((size_t)kArrays * chunks * rounds * 256 * 4);
+    L.submm = take((size_t)kArrays * chunks * rounds * kSubMM * 4);
   }
   if (batch) {
     L.table = take((size_t)nseg * sizeof(SegDesc));
@@ -753,7 +753,7 @@ int single_workspace_bytes(const SegDesc& d, size_t* bytes) {
 // the call needs no allocation.  Each GPU holds its own copy from the library's
 // first use until the process ends.  In host code `scratch` only names the
 // symbol: its device address, per device, comes from hipGetSymbolAddress.
-constexpr size_t kScratchBytes = size_t(32) << 20;
+constexpr size_t kScratchBytes = size_t(64) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxScratchDevices = 64;

@@ -56,8 +56,15 @@ constexpr int kH0 = 0, kH0R = 256, kH1 = 256 + kH0Copies * 256, kMisc = kH1 + 81
 constexpr int kSlotWords = kMisc + 64;
 // Level-1 candidates of a select round (kSelChunk samples): its values under the
 // ranks' level-0 prefixes, grouped by (rank, level-1 digit), with the start of
-// every 64th of those 8192 groups (and the total) in a table of kSubTab u16.
-constexpr int kSubTab = 130;
+// every cell of 8 of those 8192 groups (and the total) in a table of kSubTab
+// u16, and the smallest and largest candidate of every cell (kSubMM words).
+// Cells this narrow usually hold one value when the values are discrete (e.g.
+// ULP steps of 8-bit significands lie 8 or more groups apart): the final
+// read-off then takes the key from the cell bounds and reads no candidate.
+constexpr int kCellShift = 3;
+constexpr int kCells = 8192 >> kCellShift;
+constexpr int kSubTab = kCells + 2;
+constexpr int kSubMM = 2 * kCells;
 // fkey(+0.0f), the abs and rel diffs of identical pairs.  Select level 1
 // leaves these exact zeros out of its histograms and candidates.
 constexpr uint32_t kZeroKey = 0x80000000u;

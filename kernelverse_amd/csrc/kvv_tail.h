@@ -43,7 +43,7 @@ struct TailArgs {
   const float* arr[kArrays];
   uint32_t* slots;            // kArrays * kSlotWords words per large segment
   uint16_t* subtab;           // level-1 candidate tables: kSubTab per select round, per array
-  uint32_t* submm;            // per select round and array: min and max kept key of each of its 128 cells
+  uint32_t* submm;            // per select round and array: min and max kept key of each of its kCells cells
   int64_t total_sub;          // select rounds per array (total_chunks * rounds)
   const uint32_t* item_near;
   uint64_t* item_near_off;
@@ -950,11 +950,16 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
   // level 1: bins (rank, digit), the second rank's 4096 only when its prefix differs
   const int nwords = LEVEL == 0 ? 128 : (same ? 2048 : 4096);
   uint32_t* h = &L.h[0][0];
-  // level 1: each wave's kept keys of the round (at most its PER * 64 values)
+  // level 1: each wave's kept keys of the round (at most its PER * 64 values),
+  // then a spare word per lane; the round's cell bounds
   uint32_t* klist = nullptr;
+  uint32_t *cmin = nullptr, *cmax = nullptr;
   if constexpr (LEVEL == 1) {
-    __shared__ uint32_t kl[kWaves][PER * 64];
+    __shared__ uint32_t kl[kWaves][PER * 64 + 64];
+    __shared__ uint32_t cb[2][kCells];
     klist = kl[tid >> 6];
+    cmin = cb[0];
+    cmax = cb[1];
   }
   if (LEVEL == 0) {
     for (int i = tid; i < nwords; i += kBlock) h[i] = 0;
@@ -975,21 +980,22 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
       __syncthreads();
     }
     uint32_t keep = 0;
+    // position i of the thread lies inside the round when its offset in the round is below lim
+    const int lim = (int)(c1 - c0) - 4 * tid;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int64_t idx = c0 + (int64_t)(i >> 2) * (4 * kBlock) + 4 * tid + (i & 3);
-      const bool isn = __builtin_isnan(x[i]);
-      const bool ok = idx < c1 && !isn;
-      if (LEVEL == 0) nans += (idx < c1 && isn) ? 1u : 0u;
+      const bool in = (i >> 2) * (4 * kBlock) + (i & 3) < lim;
       const uint32_t key = fkey(x[i]);
-      const uint32_t dig = (key >> DS) & DM;
       if (LEVEL == 0) {
-        run0.add(h, dig, ok);
+        const bool isn = __builtin_isnan(x[i]);
+        nans += in && isn ? 1u : 0u;
+        run0.add(h, (key >> DS) & DM, in && !isn);
       } else {
-        // under a rank's prefix: key - lo < span (exact zeros left out of the +0 prefix)
-        const bool m0 = LEVEL == 1 ? ok && key - lo0 < span0 : false;
-        const bool m1 = LEVEL == 1 ? ok && !same && key - lo1 < span1 : false;
-        keep |= (m0 || m1 ? 1u : 0u) << i;
+        // under a rank's prefix: key - lo < span (exact zeros left out of the +0
+        // prefix); no NaN reaches level 1 (a NaN count returns above)
+        const bool m0 = key - lo0 < span0;
+        const bool m1 = !same && key - lo1 < span1;
+        keep |= (in && (m0 || m1) ? 1u : 0u) << i;
       }
     }
     uint32_t wkept = 0;
@@ -1000,10 +1006,15 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
       const uint32_t nk = (uint32_t)__popc(keep);
       const uint32_t incl = wave_incl_scan(nk);
       wkept = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+      // (branch-free: a value that is not kept goes to the lane's spare word)
+      const uint32_t spare = PER * 64 + (uint32_t)(tid & 63);
       uint32_t o = incl - nk;
 #pragma unroll
-      for (int i = 0; i < PER; ++i)
-        if ((keep >> i) & 1u) klist[o++] = fkey(x[i]);
+      for (int i = 0; i < PER; ++i) {
+        const uint32_t b = (keep >> i) & 1u;
+        klist[b ? o : spare] = fkey(x[i]);
+        o += b;
+      }
       __builtin_amdgcn_wave_barrier();
       for (uint32_t e = (uint32_t)(tid & 63); e < wkept; e += 64) {
         const uint32_t key = klist[e];
@@ -1022,16 +1033,14 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
       const uint32_t total = block_offsets16(h, nwords, L);
       const int64_t sub = (d.chunk_begin + c) * (int64_t)rounds + r;
       uint16_t* tab = a.subtab + ((size_t)arr * a.total_sub + (size_t)sub) * kSubTab;
-      if (tid < 129) {
-        const int bin = tid * 64;
-        tab[tid] = (uint16_t)(bin < 2 * nwords ? (h[bin >> 1] & 0xFFFFu) : total);
+      for (int i = tid; i <= kCells; i += kBlock) {
+        const int bin = i << kCellShift;
+        tab[i] = (uint16_t)(bin < 2 * nwords ? (h[bin >> 1] & 0xFFFFu) : total);
       }
-      // the smallest and largest kept key of each cell of 64 groups
-      uint32_t* cmin = reinterpret_cast<uint32_t*>(L.part);
-      uint32_t* cmax = cmin + 128;
-      if (tid < 128) {
-        cmin[tid] = 0xFFFFFFFFu;
-        cmax[tid] = 0u;
+      // the smallest and largest kept key of each cell
+      for (int i = tid; i < kCells; i += kBlock) {
+        cmin[i] = 0xFFFFFFFFu;
+        cmax[i] = 0u;
       }
       __syncthreads();  // (the offsets are read before the scatter advances them)
       uint32_t* out = reinterpret_cast<uint32_t*>(v + c0);
@@ -1041,15 +1050,12 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
         const uint32_t sh = (bin & 1u) << 4;
         const uint32_t old = atomicAdd(&h[bin >> 1], 1u << sh);
         out[(old >> sh) & 0xFFFFu] = key;
-        atomicMin(&cmin[bin >> 6], key);
-        atomicMax(&cmax[bin >> 6], key);
+        atomicMin(&cmin[bin >> kCellShift], key);
+        atomicMax(&cmax[bin >> kCellShift], key);
       }
       __syncthreads();
-      uint32_t* mm = a.submm + ((size_t)arr * a.total_sub + (size_t)sub) * 256;
-      if (tid < 128) {
-        mm[2 * tid] = cmin[tid];
-        mm[2 * tid + 1] = cmax[tid];
-      }
+      uint2* mm = reinterpret_cast<uint2*>(a.submm + ((size_t)arr * a.total_sub + (size_t)sub) * kSubMM);
+      for (int i = tid; i < kCells; i += kBlock) mm[i] = make_uint2(cmin[i], cmax[i]);
     }
   }
   if (LEVEL == 0) {
@@ -1070,7 +1076,9 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
 // The final read-off of a large group (one block): the 20-bit prefixes and
 // residual ranks from the group's two histograms, then the last 12 bits from
 // the kept keys of the target (rank, level-1 digit) groups only: each round's
-// table bounds the 64 groups around the target, a block prefix over the rounds
+// table bounds the cell of 8 groups around the target (when the cell holds a
+// single value over all rounds, that value is the key and nothing is read),
+// a block prefix over the rounds
 // spreads those keys over all threads, and the keys under the prefix are
 // counted in LDS (per-thread run merging: the target often holds one repeated
 // value).  Ranks under different prefixes take one pass each.
@@ -1098,12 +1106,13 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
       for (int i = tid; i < 4096; i += kBlock) H[i] = 0;
       const uint32_t pr = rr == 0 ? pfx[0] : pfx[1];
       const uint32_t group = (p0[0] != p0[1] && rr == 1 ? 4096u : 0u) | (pr & 4095u);
-      const int cell = (int)(group >> 6);
+      const int cell = (int)(group >> kCellShift);
       // one value throughout the target's cell (e.g. equal power-of-two steps): that is the key
-      const uint32_t* mm0 = a.submm + ((size_t)arr * a.total_sub + (size_t)d.chunk_begin * rounds) * 256;
+      const uint32_t* mm0 = a.submm + ((size_t)arr * a.total_sub + (size_t)d.chunk_begin * rounds) * kSubMM;
       uint32_t lo_key = 0xFFFFFFFFu, hi_key = 0u;
       for (int64_t k = tid; k < nsub; k += kBlock) {
-        const uint32_t a0 = mm0[(size_t)k * 256 + 2 * cell], a1 = mm0[(size_t)k * 256 + 2 * cell + 1];
+        const uint2 b = *reinterpret_cast<const uint2*>(mm0 + (size_t)k * kSubMM + 2 * cell);
+        const uint32_t a0 = b.x, a1 = b.y;
         lo_key = a0 < lo_key ? a0 : lo_key;
         hi_key = a1 > hi_key ? a1 : hi_key;
       }

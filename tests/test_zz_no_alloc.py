@@ -87,11 +87,11 @@ def test_noalloc_matches_workspace_entry_on_consecutive_calls(lib):
 
 def test_noalloc_rejects_a_verdict_beyond_its_scratch(lib):
     from kernelverse_amd import _lib, verdict
-    n = 5_000_000  # 5 M samples of abs and rel: 40 MB of sample arrays alone
+    n = 10_000_000  # 10 M samples of abs and rel: 80 MB of sample arrays alone
     g = torch.zeros(n, dtype=torch.bfloat16, device=DEV)
     job = verdict._Job(g, g, "output", None, None, n)
     gt, rt, _ = verdict._device_views(g, g)
     out = torch.empty(ctypes.sizeof(_lib.KvvResult), dtype=torch.uint8, pin_memory=True)
     rc = lib.kvv_verdict_noalloc(gt, rt, job.kpolicy, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
     assert rc == -2
-    assert b"no-alloc entry point holds 33554432" in lib.kvv_last_error()
+    assert f"no-alloc entry point holds {_lib.NOALLOC_SCRATCH_BYTES}".encode() in lib.kvv_last_error()
