@@ -1027,6 +1027,36 @@ __device__ __forceinline__ void phase_b(const SegDesc& d, uint32_t R0, uint32_t 
   }
 }
 
+// Phase B in place, for an item of 32- or 64-bit elements whose pairs are
+// mostly slow (e.g. every pair perturbed by noise): each lane finishes its own
+// slot p of the stage, p = 0 .. NE-1, one slow_elem call per slot, with no
+// queue (its writes, reads and the stage reads that depend on them).  Taken
+// when every lane has at least 3/4 of its slots slow, where the queue would
+// need nearly as many calls.  Returns whether it ran.  (Narrower elements keep
+// the queue: mostly-slow items are rare there, and the extra path in their
+// item loop cost more than it saved.)
+template <int DT, int MODE>
+__device__ __forceinline__ bool phase_b_dense(const SegDesc& d, uint32_t R0, uint64_t slow, StageP stage, Acc& acc,
+                                              uint32_t* wc) {
+  using IO = VecIO<DT>;
+  using T = typename IO::T;
+  constexpr int V = IO::V;
+  if constexpr (IO::NE > 16) {
+    return false;
+  }
+  if (__ballot((uint32_t)__popcll(slow) * 4u < 3u * (uint32_t)IO::NE)) return false;
+  const int lane = lane_id();
+#pragma unroll 1
+  for (int p = 0; p < IO::NE; ++p) {
+    int u, e;
+    slot_of<Elem<DT>::width>(p, u, e);
+    const T gc = stage_elem<T>(stage, (2 * u) * 64 + lane, e);
+    const T rc = stage_elem<T>(stage, (2 * u + 1) * 64 + lane, e);
+    slow_elem<DT, MODE>(gc, rc, ((slow >> p) & 1u) != 0, R0 + (uint32_t)((u * 64 + lane) * V + e), d, acc, wc);
+  }
+  return true;
+}
+
 // ------------------------------------------------------------ near-zero entries
 // The near-zero elements (|ref| <= near_zero_abs) of a lane's vectors of 16-bit
 // codes, found on the codes, as a mask in the slow-mask layout: bit dd of the
@@ -1875,7 +1905,9 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
         if constexpr (NZ) ni = near_item<DT>(d, stage, L0, L1, full_now);
         const uint64_t slow = phase_a_any<DT>(d, L0, R0, stage, full_now, acc, careful);
         if constexpr (NZ) near_entries<DT>(ni, slow, full_now, stage, sink);
-        if (__ballot(slow != 0)) {
+        if (__ballot(slow != 0) && phase_b_dense<DT, MODE>(d, R0, slow, stage, acc, wc)) {
+          // (an item of mostly slow pairs was finished in place)
+        } else if (__ballot(slow != 0)) {
           uint32_t nq = queue_all(slow, sm.queue[w]);
           // more than the queue holds: kQSlots slots of every lane at a time
           const bool split = nq > 64u * kQSlots;
