@@ -14,11 +14,13 @@
 // bits of every value's ordering key into the group's global histogram.  Level
 // 1 locates both ranks' level-0 bins, histograms bits 23..12 of the values
 // under those prefixes, and keeps those values' keys in the round's own span
-// of the sample array, grouped by (rank, level-1 digit), with a small table of
-// where every 64th group starts.  The final launch (one block per large group)
-// locates the 20-bit prefixes, reads only the kept keys of the target groups,
-// counts their last 12 bits in LDS, interpolates like torch.quantile and
-// writes the result.  The main pass cleared the histograms.
+// of the sample array, grouped by (rank, level-1 digit), with a table of where
+// every cell of 8 groups starts and each cell's smallest and largest key.  The
+// final launch (one block per large group) locates the 20-bit prefixes, takes
+// the key from the cell bounds when the target's cell holds one value, else
+// reads only the kept keys of the target groups and counts their last 12 bits
+// in LDS, then interpolates like torch.quantile and writes the result.  The
+// main pass (or a clearing launch) cleared the histograms.
 //
 // A launch with at least as many large groups as the device has CUs (a big
 // batch) needs no global histograms or level launches: a contiguous pair's
