@@ -444,7 +444,14 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
     x.level = level;
     x.arr_lo = arr_lo;
     x.narr = narr;
-    const int64_t grid = reduce_blocks + (total_chunks > 0 ? (int64_t)narr * total_chunks : 0) + extra;
+    int64_t chunks = total_chunks;
+    if (!batch && level == 2 && chunks > 0) {
+      // a single pair's final read-off runs on each array's first chunk only: one
+      // block per array instead of a grid of blocks that return at once
+      chunks = 1;
+      x.total_chunks = 1;
+    }
+    const int64_t grid = reduce_blocks + (chunks > 0 ? (int64_t)narr * chunks : 0) + extra;
     if (grid == 0) return KVV_OK;
     void (*fn)(TailArgs) = nullptr;
     switch (level) {
