@@ -810,16 +810,18 @@ __device__ inline void select_group_stream(const TailArgs& a, const SegDesc& d, 
 // of its histograms and candidates: the +0 bin's level-0 count minus the
 // level-1 counts under it.  They join digit 0 here, and the final read-off
 // adds them to the target group when that is the zeros' group.
+// h0pre: the thread's level-0 words (the histogram and its copies), when the
+// caller loaded them itself (ahead of its own loads, so they land first).
 template <int LEVEL>
 __device__ inline void group_state(const uint32_t* slot, const uint64_t rank64[2], uint32_t pfx[2], uint32_t resid[2],
                                    SelectLds& L, uint32_t zeros_add = 0, uint32_t* pfx0 = nullptr,
-                                   uint32_t* zeros = nullptr) {
+                                   uint32_t* zeros = nullptr, const uint32_t* h0pre = nullptr) {
   static_assert(LEVEL == 1 || LEVEL == 2, "prefixes after one or two digit levels");
   const int tid = threadIdx.x;
   uint32_t h1a[16], h1b[16];
-  uint32_t h0w = slot[kH0 + tid] + (tid == (int)(0x80000000u >> 24) ? zeros_add : 0u);
+  uint32_t h0w = (h0pre ? h0pre[0] : slot[kH0 + tid]) + (tid == (int)(0x80000000u >> 24) ? zeros_add : 0u);
 #pragma unroll
-  for (int r = 0; r < kH0Copies; ++r) h0w += slot[kH0R + r * 256 + tid];
+  for (int r = 0; r < kH0Copies; ++r) h0w += h0pre ? h0pre[r + 1] : slot[kH0R + r * 256 + tid];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     if (LEVEL >= 2) {
@@ -910,6 +912,20 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
   uint32_t* slot = a.slots + ((size_t)d.lslot * kArrays + arr) * kSlotWords;
   float* v = const_cast<float*>(a.arr[arr]) + d.sample_off;
   auto load_round = [&](float (&x)[PER], int64_t c0, int64_t c1) {
+    if (c1 - c0 == kSelChunk) {
+      // a full round (every round but a group's last): only 16-byte loads, all
+      // in flight together.  (With the partial form's element loads in the same
+      // code, each 16-byte load waited for the one before: their registers are shared.)
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const float4 q = *reinterpret_cast<const float4*>(v + c0 + (int64_t)k * (4 * kBlock) + 4 * tid);
+        x[4 * k] = q.x;
+        x[4 * k + 1] = q.y;
+        x[4 * k + 2] = q.z;
+        x[4 * k + 3] = q.w;
+      }
+      return;
+    }
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int64_t i0 = c0 + (int64_t)k * (4 * kBlock) + 4 * tid;
@@ -925,7 +941,19 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
       }
     }
   };
-  // the first round's values are in flight while the group's state is read
+  // level 1: the group's state words are loaded first, then the first round's
+  // values, so the state (its sums and block scans) is worked out while the
+  // values are still in flight
+  uint32_t h0v[kH0Copies + 1];
+  uint32_t nan_count = 0, zadd = 0;
+  if (LEVEL == 1) {
+    nan_count = slot[kMisc];
+    zadd = entry_zeros(d, arr, count, slot);
+    h0v[0] = slot[kH0 + tid];
+#pragma unroll
+    for (int r = 0; r < kH0Copies; ++r) h0v[r + 1] = slot[kH0R + r * 256 + tid];
+    asm volatile("" ::: "memory");  // (keeps the value loads below behind these)
+  }
   int64_t c0 = c * rounds * (int64_t)kSelChunk;
   int64_t c1 = c0 + kSelChunk < count ? c0 + kSelChunk : count;
   float x[PER];
@@ -933,12 +961,11 @@ __device__ inline void select_chunk(const TailArgs& a, const SegDesc& d, int arr
   uint32_t pfx[2] = {0u, 0u};
   bool same = true;
   if (LEVEL == 1) {
-    const uint32_t nan_count = slot[kMisc];  // (read with the group's state, in one round trip)
     uint64_t rank64[2];
     float wgt;
     q99_ranks(count, rank64, wgt);
     uint32_t resid[2];
-    group_state<1>(slot, rank64, pfx, resid, L, entry_zeros(d, arr, count, slot));
+    group_state<1>(slot, rank64, pfx, resid, L, zadd, nullptr, nullptr, h0v);
     // a NaN among the samples makes the quantile NaN: nothing to locate (the final read-off checks the same count)
     if (nan_count != 0) return;
     same = pfx[0] == pfx[1];
