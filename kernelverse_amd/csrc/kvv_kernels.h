@@ -1043,18 +1043,19 @@ __device__ __forceinline__ bool phase_b_dense(const SegDesc& d, uint32_t R0, uin
   constexpr int V = IO::V;
   if constexpr (IO::NE > 16) {
     return false;
-  }
-  if (__ballot((uint32_t)__popcll(slow) * 4u < 3u * (uint32_t)IO::NE)) return false;
-  const int lane = lane_id();
+  } else {
+    if (__ballot((uint32_t)__popcll(slow) * 4u < 3u * (uint32_t)IO::NE)) return false;
+    const int lane = lane_id();
 #pragma unroll 1
-  for (int p = 0; p < IO::NE; ++p) {
-    int u, e;
-    slot_of<Elem<DT>::width>(p, u, e);
-    const T gc = stage_elem<T>(stage, (2 * u) * 64 + lane, e);
-    const T rc = stage_elem<T>(stage, (2 * u + 1) * 64 + lane, e);
-    slow_elem<DT, MODE>(gc, rc, ((slow >> p) & 1u) != 0, R0 + (uint32_t)((u * 64 + lane) * V + e), d, acc, wc);
+    for (int p = 0; p < IO::NE; ++p) {
+      int u, e;
+      slot_of<Elem<DT>::width>(p, u, e);
+      const T gc = stage_elem<T>(stage, (2 * u) * 64 + lane, e);
+      const T rc = stage_elem<T>(stage, (2 * u + 1) * 64 + lane, e);
+      slow_elem<DT, MODE>(gc, rc, ((slow >> p) & 1u) != 0, R0 + (uint32_t)((u * 64 + lane) * V + e), d, acc, wc);
+    }
+    return true;
   }
-  return true;
 }
 
 // ------------------------------------------------------------ near-zero entries
