@@ -144,7 +144,8 @@ def cpu_baseline(pairs, policy=None, budget_s: float = 12.0):
 # HBM traffic of the main-pass kernel per launch, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (KiB per
 # dispatch) scaled by what the same counters read for a plain 512 MiB device copy on the same box (factors
 # below); the runs and commands are in profiles/scan_bf16_c1_traffic.md (c1) and
-# profiles/scan_traffic_c0_c2_c3fp8_c3int8_c1tolerant.md (the others).  Keyed by config, and by
+# profiles/scan_traffic_c0_c2_c3fp8_c3int8_c1tolerant.md (the others; c4's whole call in
+# profiles/verdict_c4_batch_traffic.md).  Keyed by config, and by
 # config/policy where the policy changes the main pass (tolerant: near-zero entries).
 _F2 = 524288.0 / 262156.5
 PMC_TRAFFIC = {
@@ -154,6 +155,8 @@ PMC_TRAFFIC = {
     "c2": {"fetch_kib": 262465.8, "write_kib": 9061.3, "fetch_factor": _F2, "write_factor": 1.0},
     "c3fp8": {"fetch_kib": 131273.0, "write_kib": 9060.4, "fetch_factor": _F2, "write_factor": 1.0},
     "c3int8": {"fetch_kib": 131256.1, "write_kib": 9063.4, "fetch_factor": _F2, "write_factor": 1.0},
+    # c4: the whole batch call (every kernel of one kvv_verdict_batch), profiles/verdict_c4_batch_traffic.md
+    "c4": {"fetch_kib": 5478772.4, "write_kib": 117720.7, "fetch_factor": 524288.0 / 262157.4, "write_factor": 1.0},
 }
 
 
@@ -264,6 +267,10 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time a plain 512 MiB device copy instead (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counts to bytes)")
+    ap.add_argument("--host-gen", action="store_true",
+                    help="c4: draw the workload on the host and copy it over (same model, other bytes), so no "
+                         "generator kernel runs on the GPU; for counter runs, under which the device draw crashed "
+                         "the profiler")
     ap.add_argument("--trial", action="store_true",
                     help="time the correctness trial's verdict stage (device) against the reference's host copies "
                          "plus CPU compare, on C1-shaped outputs")
@@ -287,7 +294,7 @@ def main():
     torch.cuda.set_device(dev)
     log(f"[bench] building workload {args.config}")
     if args.config == "c4":
-        pairs = synth.c4_batch(dev)
+        pairs = synth.c4_batch(dev, gen_device=torch.device("cpu") if args.host_gen else None)
         desc = ("4096 pairs, dtype alternating fp32/bf16, sizes log-uniform in [1024, 1048576] (seed 5), C0 noise "
                 "model; FP32 atol=rtol=1e-5, BF16 atol=1e-2 rtol=1.6e-2; one batched call (kvv_verdict_batch)")
         dlabel = "f32+bf16"

@@ -272,21 +272,24 @@ def c3_int8_pair(device, n: int = 134_217_728, changed: int = 1000, seed: int = 
     return g, r
 
 
-def c4_batch(device, count: int = 4096, seed: int = 5):
+def c4_batch(device, count: int = 4096, seed: int = 5, gen_device=None):
     """C4: `count` pairs, dtype alternating fp32 / bf16, sizes log-uniform in [1024, 2^20], the C0 noise model
     (ref ~ N(0,1); cand = ref + N(0,1e-6); 0.1% of positions + U(1e-3, 1e-1)); each pair is its own allocation.
-    Returns [(cand, ref, tolerance)]."""
+    `gen_device` (default `device`) draws the values there and moves them to `device` (same model, other
+    bytes: the host draw runs no generator kernels on the GPU).  Returns [(cand, ref, tolerance)]."""
     sizes = ragged_sizes(count, seed)
-    gen = torch.Generator(device=device)
+    gdev = device if gen_device is None else gen_device
+    gen = torch.Generator(device=gdev)
     gen.manual_seed(seed)
     out = []
     for i, n in enumerate(sizes):
-        ref = torch.randn(n, generator=gen, device=device)
-        cand = ref + 1e-6 * torch.randn(n, generator=gen, device=device)
-        hit = torch.rand(n, generator=gen, device=device) < 1e-3
-        cand = torch.where(hit, cand + (1e-3 + (1e-1 - 1e-3) * torch.rand(n, generator=gen, device=device)), cand)
+        ref = torch.randn(n, generator=gen, device=gdev)
+        cand = ref + 1e-6 * torch.randn(n, generator=gen, device=gdev)
+        hit = torch.rand(n, generator=gen, device=gdev) < 1e-3
+        cand = torch.where(hit, cand + (1e-3 + (1e-1 - 1e-3) * torch.rand(n, generator=gen, device=gdev)), cand)
         if i % 2:
-            out.append((cand.to(torch.bfloat16), ref.to(torch.bfloat16), {"BF16": {"rtol": 1.6e-2, "atol": 1e-2}}))
+            cand, ref, tol = cand.to(torch.bfloat16), ref.to(torch.bfloat16), {"BF16": {"rtol": 1.6e-2, "atol": 1e-2}}
         else:
-            out.append((cand, ref, {"FP32": {"rtol": 1e-5, "atol": 1e-5}}))
+            tol = {"FP32": {"rtol": 1e-5, "atol": 1e-5}}
+        out.append((cand.to(device), ref.to(device), tol))
     return out
