@@ -370,8 +370,18 @@ __device__ inline void reduce_near_prefix(const TailArgs& a, const SegDesc& d, R
   const int64_t per = (d.item_count + kBlock - 1) / kBlock;
   const int64_t k0 = tid * per < d.item_count ? tid * per : d.item_count;
   const int64_t k1 = k0 + per < d.item_count ? k0 + per : d.item_count;
+  // (8 counts per pass with their loads in flight together; one load per step,
+  // and in the second loop a store between them, made every step a round trip)
+  constexpr int kB = 8;
+  const uint32_t* cnt = a.item_near + d.item_begin;
   uint64_t mine = 0;
-  for (int64_t k = k0; k < k1; ++k) mine += a.item_near[d.item_begin + k];
+  for (int64_t k = k0; k < k1; k += kB) {
+    uint32_t v[kB];
+#pragma unroll
+    for (int q = 0; q < kB; ++q) v[q] = k + q < k1 ? cnt[k + q] : 0u;
+#pragma unroll
+    for (int q = 0; q < kB; ++q) mine += v[q];
+  }
   uint64_t incl = mine;
   for (int o = 1; o < 64; o <<= 1) {
     const uint64_t v = __shfl_up(incl, o);
@@ -382,9 +392,16 @@ __device__ inline void reduce_near_prefix(const TailArgs& a, const SegDesc& d, R
   uint64_t base = 0;
   for (int i = 0; i < w; ++i) base += L.wsum[i];
   uint64_t run = base + incl - mine;
-  for (int64_t k = k0; k < k1; ++k) {
-    a.item_near_off[d.item_begin + k] = run;
-    run += a.item_near[d.item_begin + k];
+  uint64_t* off = a.item_near_off + d.item_begin;
+  for (int64_t k = k0; k < k1; k += kB) {
+    uint32_t v[kB];
+#pragma unroll
+    for (int q = 0; q < kB; ++q) v[q] = k + q < k1 ? cnt[k + q] : 0u;
+#pragma unroll
+    for (int q = 0; q < kB; ++q) {
+      if (k + q < k1) off[k + q] = run;
+      run += v[q];
+    }
   }
 }
 
