@@ -15,10 +15,12 @@
  *   - Plain C: pointers, sizes and PODs; no C++ exceptions cross the ABI.
  *   - Every call returns 0 on success or a negative KVV_E* code; the message
  *     of the last failure on the calling thread is kvv_last_error().
- *   - Calls are stream-ordered and asynchronous: results land in DEVICE
- *     memory (kvv_result*) when the stream reaches them; the caller copies
- *     them out and synchronises.  No global mutable device state: concurrent
- *     calls on different streams with different workspaces are independent.
+ *   - Calls are stream-ordered and asynchronous: results land in the
+ *     kvv_result memory the caller passes -- device memory, or pinned host
+ *     memory (hipHostMalloc) that the kernels write over the bus -- when the
+ *     stream reaches them; the caller synchronises before reading them.  No
+ *     global mutable device state: concurrent calls on different streams with
+ *     different workspaces are independent.
  *   - Inputs are borrowed and never written.  Linear indices reported in
  *     kvv_result are LOGICAL row-major indices, not memory offsets.
  */
@@ -99,6 +101,8 @@ enum kvv_mode {
                                      select slots clear; with this flag the next one on the same workspace skips
                                      clearing them (one launch fewer) when its slots lie where the previous
                                      call's did.  Without the flag, or on any other workspace, they are cleared.
+                                     Ignored on a stream that is being captured into a graph (the graph always
+                                     clears), and a captured call leaves no record for the next call to trust.
                                      No counterpart in the reference (GCR:672-786 allocates per call). */
 
 /* kvv_result.status values. */
@@ -191,7 +195,10 @@ KVV_API int kvv_verdict_timed(const kvv_tensor* gen, const kvv_tensor* ref, cons
  * KVV_E_WORKSPACE and leaves the stream untouched.  Calls on one GPU share
  * that array: calls that overlap on one GPU (other streams, other threads)
  * race, so the caller orders them.  The kernels clear what must start at
- * zero; the array keeps the last call's contents. */
+ * zero; the array keeps the last call's contents.  The call may be captured
+ * into a HIP graph: it then clears its select slots in the graph, and once a
+ * graph holding a no-alloc verdict exists on a device, eager calls there clear
+ * theirs as well (the graph's replays write the array unseen). */
 KVV_API int kvv_verdict_noalloc(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_policy* policy,
                                 kvv_result* out, void* stream);
 

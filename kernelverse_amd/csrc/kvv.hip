@@ -70,20 +70,25 @@ int device_cus() {
 // this kernel (one round, no straggler round), each streaming a contiguous
 // range of items.
 int64_t blocks_target(ScanFn fn) {
-  static thread_local ScanFn cached_fn = nullptr;
-  static thread_local int cached_dev = -1, cached_nb = 0;
+  // resident blocks per CU of each kernel seen on this thread (a few dozen at most)
+  struct Occ {
+    ScanFn fn;
+    int dev, nb;
+  };
+  static thread_local Occ cache[64];
+  static thread_local int used = 0;
   int dev = 0;
   (void)hipGetDevice(&dev);
-  if (fn != cached_fn || dev != cached_dev) {
-    int nb = 0;
+  int nb = 0;
+  for (int i = 0; i < used; ++i)
+    if (cache[i].fn == fn && cache[i].dev == dev) nb = cache[i].nb;
+  if (nb == 0) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(fn), kBlock, 0) != hipSuccess ||
         nb <= 0)
       nb = 2;
-    cached_fn = fn;
-    cached_dev = dev;
-    cached_nb = nb;
+    cache[used < 64 ? used++ : 63] = Occ{fn, dev, nb};
   }
-  const int64_t b = (int64_t)device_cus() * cached_nb;
+  const int64_t b = (int64_t)device_cus() * nb;
   return b < 4096 ? b : 4096;
 }
 
@@ -659,8 +664,27 @@ void put_kept(const void* ws, size_t off, size_t len) {
   g_kept.push_back(KeptRange{dev, ws, off, len});
 }
 
+// Whether the launches on `st` are being recorded into a graph instead of run.
+// Host-side decisions taken now (skipping the clearing launch) would then be
+// frozen into a graph that replays later, on a workspace other calls may have
+// written in between.  The legacy default stream cannot be captured; a failed
+// query counts as capturing (the safe side: the clearing launch is kept).
+bool stream_capturing(hipStream_t st) {
+  if (st == nullptr) return false;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;
+  }
+  return cs != hipStreamCaptureStatusNone;
+}
+
 int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st, bool kept,
                hipEvent_t ev_begin = nullptr, hipEvent_t ev_end = nullptr) {
+  // under capture the slots are always cleared, and the record of this
+  // workspace is dropped (take_kept below) and not renewed: a replay runs later
+  const bool capturing = stream_capturing(st);
+  if (capturing) kept = false;
   SegDesc d = d0;
   d.item_begin = 0;
   d.sample_off = 0;
@@ -743,7 +767,7 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   std::vector<NearLaunch> nears{{near_fn(d.dtype, d.mode), 0, 1, 0, d.item_count}};
   rc = launch_tail(&d, nullptr, nullptr, 1, d.chunk_count, nslots, g.near, L, ws, out, st, nears);
   // the final read-off zeroes every slot it read: the next call may skip the clearing
-  if (rc == KVV_OK && main_hist && d.item_count > 0) put_kept(ws, L.slots, L.slot_bytes);
+  if (rc == KVV_OK && main_hist && d.item_count > 0 && !capturing) put_kept(ws, L.slots, L.slot_bytes);
   return rc;
 }
 
@@ -766,9 +790,15 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch[kMaxScratchDevices] = {};
+// a no-alloc verdict was captured into a graph on this device: its replays
+// write the scratch array at times the library does not see
+bool g_scratch_graphed[kMaxScratchDevices] = {};
 
-// The current device's scratch address, looked up once per device.
-int scratch_address(void** p) {
+// The current device's scratch address, looked up once per device.  `kept`:
+// whether only the library's own eager calls can have written the array since
+// the previous one (no no-alloc verdict on this device was ever captured;
+// `capturing` says this one is).
+int scratch_address(void** p, bool capturing, bool* kept) {
   int dev = 0;
   KVV_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= kMaxScratchDevices)
@@ -780,7 +810,9 @@ int scratch_address(void** p) {
     if (!q) return fail(KVV_E_HIP, "hipGetSymbolAddress(scratch) gave a null address");
     g_scratch[dev] = q;
   }
+  if (capturing) g_scratch_graphed[dev] = true;
   *p = g_scratch[dev];
+  *kept = !g_scratch_graphed[dev];
   return KVV_OK;
 }
 
@@ -1045,10 +1077,13 @@ int kvv_verdict_noalloc(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_
                                           std::to_string(kvv::kScratchBytes) +
                                           " (lower max_samples, or call kvv_verdict with a workspace)");
   void* ws = nullptr;
-  rc = kvv::scratch_address(&ws);
+  bool kept = false;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = kvv::scratch_address(&ws, kvv::stream_capturing(st), &kept);
   if (rc) return rc;
-  // the scratch array is the library's own: only its calls write it
-  return kvv::run_single(d, out, ws, kvv::kScratchBytes, static_cast<hipStream_t>(stream), true);
+  // the scratch array is the library's own: only its calls write it, eagerly,
+  // until a graph holding one of them exists on the device
+  return kvv::run_single(d, out, ws, kvv::kScratchBytes, st, kept);
 }
 
 int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs,

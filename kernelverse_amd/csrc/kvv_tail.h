@@ -1338,7 +1338,11 @@ __device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
   const uint64_t m = c < ms ? c : ms;
   const bool strided = c > ms;
   const uint64_t num = strided ? c - 1 : 1, den = strided ? m - 1 : 1;
-  const bool large = d.lslot >= 0;
+  // the near-zero sample's slot is used only when that sample itself is a large
+  // group: a group of at most kSmall values is selected by select_small straight
+  // from the array, and only select_final (large groups) clears the slot again,
+  // which a kept workspace relies on
+  const bool large = d.lslot >= 0 && m > (uint64_t)kSmall;
   uint32_t* slot = large ? a.slots + ((size_t)d.lslot * kArrays + 2) * kSlotWords : nullptr;
   float* sample = const_cast<float*>(a.arr[2]) + d.sample_off;
   double sum = 0.0;

@@ -149,3 +149,54 @@ def test_dropin_repeats_match_oracle(kv):
         probs = meta_problems(got[2], want[2], g, r)
         assert not probs, (k, probs)
         assert got[0] == want[0]
+
+
+def _near_pair(n, near_frac, seed):
+    """bf16 pair whose reference has about near_frac of its values at |x| <= 0.25 (the
+    tolerant policy's near-zero band) and the rest at 1 <= |x| <= 4; 30% of all
+    positions are moved by one code, so near-zero elements carry nonzero abs_diffs."""
+    from kernelverse_amd import synth
+    rng = np.random.default_rng(seed)
+    big = rng.uniform(1.0, 4.0, size=n) * rng.choice([-1.0, 1.0], size=n)
+    small = rng.uniform(-0.25, 0.25, size=n)
+    ref = torch.from_numpy(np.where(rng.random(n) < near_frac, small, big).astype(np.float32)).to(torch.bfloat16)
+    pos = np.sort(rng.choice(n, size=int(0.3 * n), replace=False))
+    gen = synth.step_codes(ref, pos, np.ones(pos.size, dtype=np.int64), rng)
+    return gen, ref
+
+
+def test_tolerant_small_then_large_near_zero_sample(kv):
+    """A tolerant verdict whose abs/rel sample is a large group but whose near-zero
+    sample is small (selected in one block, its select slot never used), then one of
+    the same shape whose near-zero sample is large, on one kept workspace: the second
+    must not read anything the first left in the near-zero slot."""
+    from kernelverse_amd import _lib
+    from oracle import torch_verdict as tv
+    from parity_util import meta_problems
+    pol = _policy("tolerant")
+    small = _near_pair(100_000, 0.05, 901)    # ~5k near-zero refs: <= 8192 samples
+    large = _near_pair(100_000, 0.40, 902)    # ~40k near-zero refs
+    seq = [("small", *small), ("large", *large), ("small again", *small), ("large again", *large)]
+    dev = {n: (g.to(DEV), r.to(DEV)) for n, g, r in seq}
+    near_counts = {}
+    shared = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
+    flags = 0
+    for n, g, r in seq:
+        _say("tolerant near-zero sample on a kept workspace:", n)
+        gd, rd = dev[n]
+        fresh = _call(kv, gd, rd, pol, None, 0)
+        got = _call(kv, gd, rd, pol, shared, flags)
+        flags = _lib.FLAG_WS_KEPT
+        assert got["status"] == 0 and fresh["status"] == 0
+        bad = _same(got, fresh)
+        assert not bad, (n, bad)
+        near_counts[n] = got["near_zero_count"]
+    assert near_counts["small"] <= 8192 < near_counts["large"], near_counts
+    # the drop-in keeps its workspace and passes the flag from its second call on
+    for n, g, r in seq:
+        _say("drop-in tolerant near-zero sample:", n)
+        gd, rd = dev[n]
+        want = tv.compare_tensors(g, r, "output", None, pol)
+        got = kv._compare_tensors(gd, rd, "output", None, pol)
+        probs = meta_problems(got[2], want[2], g, r)
+        assert not probs, (n, probs)

@@ -95,3 +95,65 @@ def test_noalloc_rejects_a_verdict_beyond_its_scratch(lib):
     rc = lib.kvv_verdict_noalloc(gt, rt, job.kpolicy, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
     assert rc == -2
     assert f"no-alloc entry point holds {_lib.NOALLOC_SCRATCH_BYTES}".encode() in lib.kvv_last_error()
+
+
+def test_noalloc_captured_graphs_alternate_with_eager_calls(lib):
+    """kvv_verdict_noalloc captured into HIP graphs (torch.cuda.graph) for two layouts;
+    the graphs are replayed alternately, with eager no-alloc calls of the other layout
+    and synchronisations in between, and every replay's record must equal kvv_verdict's
+    on a fresh workspace.  The eager calls and the other graph write the shared scratch
+    between replays, so a graph that skipped its slot clearing would read their leftovers."""
+    from kernelverse_amd import _lib, synth, verdict
+    from kernelverse_amd.correctness_policy import resolve_correctness_policy
+    tolerant = resolve_correctness_policy({"category": "gemm", "op_name": "x"})
+    cases = {
+        "A bf16 3M tolerant": (*synth.code_flip_pair(3_000_000, seed=71), {"BF16": {"rtol": 1e-3, "atol": 1e-4}},
+                               tolerant),
+        "B fp32 600k strict": (*synth.fp32_noise_pair(600_000, seed=72), {"FP32": {"rtol": 1e-5, "atol": 1e-5}},
+                               None),
+    }
+    rec_size = ctypes.sizeof(_lib.KvvResult)
+    views, want = {}, {}
+    for name, (g, r, tol, pol) in cases.items():
+        gd, rd = g.to(DEV), r.to(DEV)
+        job = verdict._Job(gd, rd, "output", tol, pol, verdict.MAX_SAMPLES, fp8_errors=False)
+        gt, rt, held = verdict._device_views(gd, rd)
+        views[name] = (gt, rt, job.kpolicy, held)
+        _say("noalloc graph: expected record of", name)
+        want[name], eager = _records(lib, gd, rd, tol, pol)
+        assert not _same(want[name], eager), name
+
+    def eager_noalloc(name):
+        gt, rt, pol, _ = views[name]
+        out = torch.zeros(rec_size, dtype=torch.uint8, pin_memory=True)
+        _lib.check(lib.kvv_verdict_noalloc(gt, rt, pol, out.data_ptr(), torch.cuda.current_stream().cuda_stream),
+                   "kvv_verdict_noalloc")
+        torch.cuda.current_stream().synchronize()
+        return _lib.KvvResult.from_buffer_copy(out.numpy().tobytes()).to_dict()
+
+    graphs, outs = {}, {}
+    for name in cases:
+        gt, rt, pol, _ = views[name]
+        outs[name] = torch.zeros(rec_size, dtype=torch.uint8, device=DEV)
+        graphs[name] = torch.cuda.CUDAGraph()
+        _say("noalloc graph: capture", name)
+        with torch.cuda.graph(graphs[name]):
+            rc = lib.kvv_verdict_noalloc(gt, rt, pol, outs[name].data_ptr(), torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "kvv_verdict_noalloc under capture")
+    torch.cuda.synchronize()
+    order = ["replay A", "eager B", "replay B", "eager A", "replay A", "replay B", "eager B", "replay A", "eager A",
+             "replay B"]
+    for step in order:
+        kind, key = step.split()
+        name = next(n for n in cases if n.startswith(key + " "))
+        _say("noalloc graph:", step)
+        if kind == "replay":
+            outs[name].zero_()
+            graphs[name].replay()
+            torch.cuda.synchronize()
+            got = _lib.KvvResult.from_buffer_copy(outs[name].cpu().numpy().tobytes()).to_dict()
+        else:
+            got = eager_noalloc(name)
+        bad = _same(want[name], got)
+        assert not bad, (step, bad)
+        assert got["status"] == 0 and got["numel"] == cases[name][0].numel()
