@@ -83,6 +83,25 @@ def make_workload(name: str, dev):
     raise SystemExit(f"unknown config {name}")
 
 
+def host_threads():
+    """(threads for the CPU baseline, CPUs this process may run on, logical CPUs of the host).
+
+    The baseline uses every CPU of the process's affinity mask, capped by OMP_NUM_THREADS when that is
+    set (the GPU box sets it to the CPU share of one GPU, 16, while the mask may show the whole host)."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    threads = usable
+    try:
+        omp = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        omp = 0
+    if omp > 0:
+        threads = min(threads, omp)
+    return threads, usable, os.cpu_count() or usable
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -99,7 +118,7 @@ def cpu_baseline(pairs, policy=None, budget_s: float = 12.0):
     the first 64 Mi elements of a single pair, or the leading pairs of a batch up to 64 Mi elements, repeated
     for about budget_s seconds of CPU work (at least 3 runs)."""
     from oracle import torch_verdict as tv
-    threads = min(os.cpu_count() or 1, 16)
+    threads, usable, host_cpus = host_threads()
     torch.set_num_threads(threads)
     cap = 1 << 26
     host, taken = [], 0
@@ -133,10 +152,14 @@ def cpu_baseline(pairs, policy=None, budget_s: float = 12.0):
         "value": round(bytes_read / t / 1e9, 4),
         "unit": "GB/s",
         "cores": threads,
+        "affinity_cpus": usable,
+        "host_logical_cpus": host_cpus,
         "kind": "port",
         "sample": (f"torch-CPU oracle compare_tensors (restatement of GCR:672-786) over {taken:,} elements "
                    f"({len(host)} pair(s)) of the same workload, median of {len(times)} runs, {t * 1e3:.1f} ms each; "
-                   f"{threads} threads of {_cpu_model()}; torch {torch.__version__}; the device-to-host copy the "
+                   f"{threads} threads (affinity mask {usable} CPUs, OMP_NUM_THREADS "
+                   f"{os.environ.get('OMP_NUM_THREADS', 'unset')}, host {host_cpus} logical CPUs) of "
+                   f"{_cpu_model()}; torch {torch.__version__}; the device-to-host copy the "
                    f"reference pays first took {d2h_s * 1e3:.1f} ms and is excluded"),
     }
 
@@ -228,7 +251,7 @@ def trial_measurement(args):
         ok, details, metas = trial._run_correctness_trial_once(**kw)
         times.append(time.perf_counter() - t0)
     dev_ms = 1e3 * statistics.median(times)
-    threads = min(os.cpu_count() or 1, 16)
+    threads, _, _ = host_threads()
     torch.set_num_threads(threads)
     log("[bench] reference-style stage: host copies, then the CPU oracle")
     t0 = time.perf_counter()
@@ -296,7 +319,8 @@ def main():
     if args.config == "c4":
         pairs = synth.c4_batch(dev, gen_device=torch.device("cpu") if args.host_gen else None)
         desc = ("4096 pairs, dtype alternating fp32/bf16, sizes log-uniform in [1024, 1048576] (seed 5), C0 noise "
-                "model; FP32 atol=rtol=1e-5, BF16 atol=1e-2 rtol=1.6e-2; one batched call (kvv_verdict_batch)")
+                "model; per-pair atol/rtol (each dtype cycles four tolerance sets: synth.C4_TOLERANCES); one "
+                "batched call (kvv_verdict_batch)")
         dlabel = "f32+bf16"
     else:
         g, r, tol, desc, dlabel = make_workload(args.config, dev)
@@ -351,18 +375,11 @@ def main():
     # Single-call measurements first, then the throughput steps.  The device reaches its full clocks only
     # after some 10 ms of sustained load: on one box back-to-back C1 verdicts took 233 us each for the first
     # 20 after 5 warm-ups and 206 us from the 50th on, and 234 us again after 0.5 s idle.  The latency and
-    # drop-in calls below (28 verdicts) therefore precede the W warm-up and K timed steps.
-    # latency of one verdict issued and waited for on its own (the reference's usage: one compare, then read)
-    lat = []
-    for _ in range(5):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        step()
-        stream.synchronize()
-        lat.append(time.perf_counter() - t0)
-    us_sync = 1e6 * statistics.median(lat)
-    # the drop-in (kernelverse_amd.verdict._compare_tensors, what the reference's callers invoke, GCR:672-786)
-    # end to end: job planning, workspace sizing, the launches, the synchronisation and the meta dict
+    # drop-in calls below (51 verdicts) therefore precede the W warm-up and K timed steps.
+    # latency of one verdict issued and waited for on its own (the reference's usage: one compare, then read),
+    # raw (kvv_verdict, then a stream synchronisation) and through the drop-in
+    # (kernelverse_amd.verdict._compare_tensors, what the reference's callers invoke, GCR:672-786: job planning,
+    # the launches, the synchronisation and the meta dict), interleaved call by call so both see the same clocks
     dropin = None
     g0, r0, tol0 = pairs[0]
     try:
@@ -371,18 +388,25 @@ def main():
     except NotImplementedError as e:
         # float8 e4m3fn: the reference's verdict raises (torch-CPU has no isfinite for it), and so does the drop-in
         dropin = {"raises": f"NotImplementedError: {e}"}
-    if n_pairs == 1 and dropin is None:
-        for _ in range(2):
-            verdict._compare_tensors(g0, r0, "output", tol0, policy)
-        dl = []
-        for _ in range(20):
+    with_dropin = n_pairs == 1 and dropin is None
+    lat, dl = [], []
+    for k in range(25):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step()
+        stream.synchronize()
+        lat.append(time.perf_counter() - t0)
+        if with_dropin:
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             verdict._compare_tensors(g0, r0, "output", tol0, policy)
             dl.append(time.perf_counter() - t0)
-        dropin = {"us_per_call_median": round(1e6 * statistics.median(dl), 1), "calls": len(dl),
+    us_sync = 1e6 * statistics.median(lat[5:])
+    if with_dropin:
+        dropin = {"us_per_call_median": round(1e6 * statistics.median(dl[5:]), 1), "calls": len(dl) - 5,
                   "call": "kernelverse_amd.verdict._compare_tensors(gen, ref, 'output', tolerance, policy)",
-                  "raw_us_per_verdict_synchronous": round(us_sync, 1)}
+                  "raw_us_per_verdict_synchronous": round(us_sync, 1),
+                  "timing": "median of 20 calls each after 5, raw and drop-in calls interleaved"}
     log(f"[bench] warmup {args.warmup}")
     for _ in range(args.warmup):
         step()

@@ -9,6 +9,7 @@
 #include <type_traits>
 
 #include "kvv.h"
+#include "kvv_bounds.h"
 
 namespace kvv {
 

@@ -1,5 +1,5 @@
 // Instantiates the scan, near-zero and input-select kernels of one element type.  The build
-// compiles this file once per dtype code (-DKVV_DT=<kvv_dtype>) so the twelve
+// compiles this file once per dtype code (-DKVV_DT=<kvv_dtype>) so the fifteen
 // dtypes compile in parallel; kvv.hip reaches the kernels through the
 // kvv_scan_fn_<n> / kvv_near_fn_<n> / kvv_isel_fn_<n> accessors defined here.
 #include <hip/hip_runtime.h>

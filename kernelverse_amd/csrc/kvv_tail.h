@@ -4,7 +4,7 @@
 //     order (bit-reproducible fp64 sums);
 //   * the exact order statistics of torch.quantile(q=0.99) over the strided
 //     sample arrays (abs_diff, rel_diff and, for the tolerant policy, the
-//     near-zero abs_diff), GCR:318-343 and GCR:525-548.
+//     near-zero abs_diff), GCR:396-402 (torch.quantile) and GCR:525-548.
 //
 // One kernel, tail_kernel, plays both roles: its first `reduce_blocks` blocks
 // fold run records (one segment each), the others select.  A (segment, array)
@@ -1192,13 +1192,10 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
         uint32_t lo = 0, len = 0;
         if (tid < nb) {
           const uint16_t* t = tab0 + (size_t)(s0 + tid) * kSubTab;
-          lo = t[cell];
-          len = (uint32_t)t[cell + 1] - lo;
           // the round's own span bounds every read below, whatever the table holds
-          const int64_t left = count - (int64_t)(s0 + tid) * kSelChunk;
-          const uint32_t rsz = left < kSelChunk ? (uint32_t)left : (uint32_t)kSelChunk;
-          lo = lo < rsz ? lo : rsz;
-          len = len <= rsz - lo ? len : rsz - lo;
+          const CellSpan cs = cell_span(t[cell], t[cell + 1], count, s0 + tid, kSelChunk);
+          lo = cs.lo;
+          len = cs.len;
         }
         const uint32_t incl = wave_incl_scan(len);
         __syncthreads();  // (pre/beg of the previous batch are read)

@@ -171,14 +171,15 @@ RAGGED_TOLERANCES = ({"rtol": 1e-5, "atol": 1e-5}, {"rtol": 1.6e-2, "atol": 1e-2
 
 
 def ragged_batch(count: int, seed: int, lo: int = 1024, hi: int = 1 << 20):
-    """List of (cand, ref, tolerance) with dtype alternating fp32 / bf16 and the fp32 noise model."""
+    """List of (cand, ref, tolerance) with dtype alternating fp32 / bf16 and the fp32 noise model; pair i takes
+    RAGGED_TOLERANCES[(i // 2) % 4], so each dtype cycles through all four."""
     sizes = ragged_sizes(count, seed, lo, hi)
     out = []
     for i, n in enumerate(sizes):
         cand, ref = fp32_noise_pair(n, seed * 100003 + i)
         if i % 2:
             cand, ref = cand.to(torch.bfloat16), ref.to(torch.bfloat16)
-        out.append((cand, ref, dict(RAGGED_TOLERANCES[i % len(RAGGED_TOLERANCES)])))
+        out.append((cand, ref, dict(RAGGED_TOLERANCES[(i // 2) % len(RAGGED_TOLERANCES)])))
     return out
 
 
@@ -272,11 +273,28 @@ def c3_int8_pair(device, n: int = 134_217_728, changed: int = 1000, seed: int = 
     return g, r
 
 
+# C4's per-pair tolerances: pair i takes entry (i // 2) % 4 of its dtype's list (fp32 pairs are the even
+# ones), so neighbouring pairs of one dtype in a batch never share a tolerance.
+C4_TOLERANCES = {
+    "FP32": ({"rtol": 1e-5, "atol": 1e-5}, {"rtol": 1.3e-6, "atol": 1e-5}, {"rtol": 5e-4, "atol": 5e-4},
+             {"rtol": 1e-4, "atol": 1e-6}),
+    "BF16": ({"rtol": 1.6e-2, "atol": 1e-2}, {"rtol": 1.6e-2, "atol": 1e-3}, {"rtol": 1e-2, "atol": 1e-2},
+             {"rtol": 5e-3, "atol": 1e-3}),
+}
+
+
+def c4_tolerance(i: int) -> dict:
+    """The tolerance table of C4's pair i: its dtype's entry (i // 2) % 4."""
+    name = "BF16" if i % 2 else "FP32"
+    return {name: dict(C4_TOLERANCES[name][(i // 2) % 4])}
+
+
 def c4_batch(device, count: int = 4096, seed: int = 5, gen_device=None):
     """C4: `count` pairs, dtype alternating fp32 / bf16, sizes log-uniform in [1024, 2^20], the C0 noise model
-    (ref ~ N(0,1); cand = ref + N(0,1e-6); 0.1% of positions + U(1e-3, 1e-1)); each pair is its own allocation.
-    `gen_device` (default `device`) draws the values there and moves them to `device` (same model, other
-    bytes: the host draw runs no generator kernels on the GPU).  Returns [(cand, ref, tolerance)]."""
+    (ref ~ N(0,1); cand = ref + N(0,1e-6); 0.1% of positions + U(1e-3, 1e-1)); each pair is its own allocation
+    with its own tolerances (``c4_tolerance``).  `gen_device` (default `device`) draws the values there and
+    moves them to `device` (same model, other bytes: the host draw runs no generator kernels on the GPU).
+    Returns [(cand, ref, tolerance)]."""
     sizes = ragged_sizes(count, seed)
     gdev = device if gen_device is None else gen_device
     gen = torch.Generator(device=gdev)
@@ -288,8 +306,6 @@ def c4_batch(device, count: int = 4096, seed: int = 5, gen_device=None):
         hit = torch.rand(n, generator=gen, device=gdev) < 1e-3
         cand = torch.where(hit, cand + (1e-3 + (1e-1 - 1e-3) * torch.rand(n, generator=gen, device=gdev)), cand)
         if i % 2:
-            cand, ref, tol = cand.to(torch.bfloat16), ref.to(torch.bfloat16), {"BF16": {"rtol": 1.6e-2, "atol": 1e-2}}
-        else:
-            tol = {"FP32": {"rtol": 1e-5, "atol": 1e-5}}
-        out.append((cand.to(device), ref.to(device), tol))
+            cand, ref = cand.to(torch.bfloat16), ref.to(torch.bfloat16)
+        out.append((cand.to(device), ref.to(device), c4_tolerance(i)))
     return out

@@ -28,6 +28,7 @@ from __future__ import annotations
 import ctypes
 import math
 import threading
+from collections import OrderedDict
 from typing import Any, Dict, List, Optional, Sequence, Tuple
 
 import torch
@@ -239,7 +240,7 @@ class _Job:
     """One tensor pair on its way to the device, with what the meta builder needs."""
 
     __slots__ = ("gen", "ref", "path", "policy", "tolerance", "near_thresholds", "correctness_policy", "kpolicy",
-                 "record")
+                 "record", "is_float", "active", "tol_text")
 
     def __init__(self, gen, ref, path, tolerance_policy, correctness_policy, max_samples, fp8_errors=None):
         self.gen, self.ref, self.path = gen, ref, path
@@ -273,6 +274,9 @@ class _Job:
             raise TypeError(f"verdict does not support dtype {ref.dtype}")
         self.kpolicy = kp
         self.record = None
+        self.tol_text = None
+        self.is_float = torch.is_floating_point(ref)
+        self.active = policy_name(correctness_policy)
 
 
 def _device_for(*tensors) -> torch.device:
@@ -358,30 +362,69 @@ class _Buffers:
 
     Every call synchronises its stream before it returns, so consecutive calls
     on one stream can reuse both; the lock serialises threads that share the
-    stream.  Each grows to the largest call seen (``release_buffers`` frees them).
+    stream.  Each grows to the largest call seen.  At most ``_MAX_STREAMS``
+    (device, stream) entries are kept: a new stream evicts the least recently
+    used idle one, and ``release_buffers`` frees them all.
     ``kept``: the workspace went through a previous call and nothing else writes
     it, so single-pair calls pass KVV_FLAG_WS_KEPT (the library then skips
-    clearing the select slots that call left clear)."""
+    clearing the select slots that call left clear).
+    ``plans``: per single-pair layout and policy, the C-ABI views (their data
+    pointers set per call) and the workspace size, so a repeated call plans nothing
+    on the host."""
 
-    __slots__ = ("lock", "ws", "out", "kept")
+    __slots__ = ("lock", "ws", "out", "kept", "stream", "handle", "plans", "ws_bytes", "ws_ptr", "out_ptr")
 
-    def __init__(self):
+    def __init__(self, stream):
         self.lock = threading.Lock()
         self.ws = None
         self.out = None
         self.kept = False
+        self.stream = stream
+        self.handle = stream.cuda_stream
+        self.plans: "OrderedDict[tuple, tuple]" = OrderedDict()
+        self.ws_bytes = self.ws_ptr = self.out_ptr = 0
 
 
-_BUFFERS: Dict[Tuple[int, int], _Buffers] = {}
+_MAX_STREAMS = 8
+_MAX_PLANS = 64
+_BUFFERS: "OrderedDict[Tuple[int, int], _Buffers]" = OrderedDict()
 _BUFFERS_LOCK = threading.Lock()
+_LAST = [None]  # the most recently used entry (its LRU position needs no update)
+# the current stream's raw handle without building a torch Stream object (falls back to the public call)
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
-def _buffers_for(dev: torch.device, stream: int) -> _Buffers:
-    key = (dev.index, stream)
+def _stream_buffers(dev: torch.device) -> _Buffers:
+    """The buffers of dev's current stream (created, and the LRU bound kept, on first use)."""
+    idx = dev.index
+    handle = _RAW_STREAM(idx) if _RAW_STREAM is not None else torch.cuda.current_stream(dev).cuda_stream
+    key = (idx, handle)
     b = _BUFFERS.get(key)
-    if b is None:
-        with _BUFFERS_LOCK:
-            b = _BUFFERS.setdefault(key, _Buffers())
+    if b is not None:
+        if b is not _LAST[0]:
+            with _BUFFERS_LOCK:
+                if key in _BUFFERS:
+                    _BUFFERS.move_to_end(key)
+                    _LAST[0] = b
+        return b
+    cur = torch.cuda.current_stream(dev)
+    with _BUFFERS_LOCK:
+        b = _BUFFERS.get(key)
+        if b is None:
+            b = _BUFFERS[key] = _Buffers(cur)
+            _LAST[0] = b
+            # evict the least recently used idle entries beyond the bound (their memory goes back to torch)
+            for old in list(_BUFFERS.keys())[:-1]:
+                if len(_BUFFERS) <= _MAX_STREAMS:
+                    break
+                ob = _BUFFERS[old]
+                if ob.lock.acquire(blocking=False):
+                    try:
+                        ob.ws = ob.out = None
+                        ob.plans.clear()
+                        del _BUFFERS[old]
+                    finally:
+                        ob.lock.release()
     return b
 
 
@@ -391,10 +434,104 @@ def release_buffers() -> None:
         for b in _BUFFERS.values():
             with b.lock:
                 b.ws = b.out = None
+                b.plans.clear()
         _BUFFERS.clear()
+        _LAST[0] = None
+
+
+def _ensure(buf: _Buffers, dev: torch.device, ws_bytes: int, records: int) -> None:
+    """Grows buf's workspace and pinned record buffer to this call's needs (under buf.lock)."""
+    rec_size = ctypes.sizeof(_lib.KvvResult)
+    if buf.ws is None or buf.ws.numel() < ws_bytes:
+        buf.ws = None
+        buf.kept = False
+        buf.ws = torch.empty(max(ws_bytes, 1 << 20), dtype=torch.uint8, device=dev)
+        buf.ws_bytes, buf.ws_ptr = buf.ws.numel(), buf.ws.data_ptr()
+    if buf.out is None or buf.out.numel() < rec_size * records:
+        # the records are written by the kernels straight into pinned host memory
+        buf.out = torch.empty(max(rec_size * records, 64 * rec_size), dtype=torch.uint8, pin_memory=True)
+        buf.out_ptr = buf.out.data_ptr()
+
+
+def _device_of(job: _Job) -> torch.device:
+    g, r = job.gen, job.ref
+    if r.device.type == "cuda":
+        return r.device
+    if g.device.type == "cuda":
+        return g.device
+    return _device_for(r, g)
+
+
+_REC_SIZE = ctypes.sizeof(_lib.KvvResult)
+_GET_DEVICE = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+_DEVICES: Dict[int, torch.device] = {}
+
+
+def _cuda_device(index: int) -> torch.device:
+    d = _DEVICES.get(index)
+    if d is None:
+        d = _DEVICES[index] = torch.device("cuda", index)
+    return d
+
+
+def _launch_single(job: _Job) -> None:
+    """One pair through kvv_verdict, with the views and workspace size cached per layout and policy."""
+    lib = _lib.load()
+    g, r = job.gen, job.ref
+    gi, ri = g.get_device(), r.get_device()
+    if ri < 0 or gi != ri:
+        dev = _device_of(job)
+        g = g if g.device == dev else g.to(dev)
+        r = r if r.device == dev else r.to(dev)
+        ri = dev.index
+    ctx = torch.cuda.device(ri) if ri != _GET_DEVICE() else None
+    if ctx is not None:
+        ctx.__enter__()
+    try:
+        buf = _stream_buffers(_cuda_device(ri))
+        kp = job.kpolicy
+        gp, rp = g.data_ptr(), r.data_ptr()
+        key = (g.dtype, g.shape, g.stride(), r.stride(), (gp & 15) == 0, (rp & 15) == 0, kp.mode, kp.flags, kp.rtol,
+               kp.atol, kp.max_abs_diff, kp.near_zero_abs, kp.near_zero_bad_abs, kp.max_samples)
+        with buf.lock:
+            plan = buf.plans.get(key)
+            if plan is None:
+                gt, rt, _ = _device_views(g, r)
+                size = ctypes.c_size_t()
+                _lib.check(lib.kvv_workspace_size(gt, rt, kp, ctypes.byref(size)), "kvv_workspace_size")
+                plan = (gt, rt, size.value)
+                buf.plans[key] = plan
+                if len(buf.plans) > _MAX_PLANS:
+                    buf.plans.popitem(last=False)
+            elif gp:
+                plan[0].data = gp
+                plan[1].data = rp
+            gt, rt, size = plan
+            if buf.ws is None or buf.ws_bytes < size or buf.out is None:
+                _ensure(buf, torch.device("cuda", ri), size, 1)
+            flags = kp.flags
+            if buf.kept:
+                kp.flags = flags | _lib.FLAG_WS_KEPT
+            buf.kept = False  # (until this call has gone through)
+            try:
+                rc = lib.kvv_verdict(gt, rt, kp, buf.out_ptr, buf.ws_ptr, size, buf.handle)
+            finally:
+                kp.flags = flags
+            _lib.check(rc, "kvv_verdict")
+            # host work that needs no record, done while the device runs
+            job.tol_text = f"{job.tolerance}"
+            buf.stream.synchronize()
+            buf.kept = True
+            job.record = _lib.KvvResult.from_buffer_copy(ctypes.string_at(buf.out_ptr, _REC_SIZE))
+    finally:
+        if ctx is not None:
+            ctx.__exit__(None, None, None)
 
 
 def _launch(jobs: List[_Job]) -> None:
+    if len(jobs) == 1 and jobs[0].gen.dtype not in _COMPLEX_REAL and jobs[0].gen.dim() <= _lib.MAX_DIMS:
+        _launch_single(jobs[0])
+        return
     lib = _lib.load()
     dev = _device_for(*[j.ref for j in jobs], *[j.gen for j in jobs])
     keep = []
@@ -413,8 +550,8 @@ def _launch(jobs: List[_Job]) -> None:
     if ctx is not None:
         ctx.__enter__()
     try:
-        cur = torch.cuda.current_stream(dev)
-        stream = cur.cuda_stream
+        buf = _stream_buffers(dev)
+        stream = buf.stream.cuda_stream
         size = ctypes.c_size_t()
         if n == 1:
             _lib.check(lib.kvv_workspace_size(gts[0], rts[0], jobs[0].kpolicy, ctypes.byref(size)), "kvv_workspace_size")
@@ -422,15 +559,8 @@ def _launch(jobs: List[_Job]) -> None:
             GA, PA = _lib.KvvTensor * n, _lib.KvvPolicy * n
             garr, rarr, parr = GA(*gts), GA(*rts), PA(*[j.kpolicy for j in jobs])
             _lib.check(lib.kvv_batch_workspace_size(n, garr, rarr, parr, ctypes.byref(size)), "kvv_batch_workspace_size")
-        buf = _buffers_for(dev, stream)
         with buf.lock:
-            if buf.ws is None or buf.ws.numel() < size.value:
-                buf.ws = None
-                buf.kept = False
-                buf.ws = torch.empty(max(size.value, 1 << 20), dtype=torch.uint8, device=dev)
-            if buf.out is None or buf.out.numel() < rec_size * n:
-                # the records are written by the kernels straight into pinned host memory
-                buf.out = torch.empty(max(rec_size * n, 64 * rec_size), dtype=torch.uint8, pin_memory=True)
+            _ensure(buf, dev, size.value, n)
             ws, out = buf.ws, buf.out
             if n == 1:
                 pol = _lib.KvvPolicy.from_buffer_copy(jobs[0].kpolicy)
@@ -443,7 +573,7 @@ def _launch(jobs: List[_Job]) -> None:
                 buf.kept = False
                 rc = lib.kvv_verdict_batch(n, garr, rarr, parr, out.data_ptr(), ws.data_ptr(), size.value, stream)
                 _lib.check(rc, "kvv_verdict_batch")
-            cur.synchronize()
+            buf.stream.synchronize()
             buf.kept = True
             host = ctypes.string_at(out.data_ptr(), rec_size * n)
     finally:
@@ -483,11 +613,10 @@ def _unravel(index: int, shape: Sequence[int]) -> Tuple[int, ...]:
 def _meta_from_record(job: _Job) -> Tuple[bool, List[str], Dict[str, Any]]:
     """Builds GCR:681-786's (ok, details, meta) from the device record."""
     rec = job.record
-    ref = job.ref
     path = job.path
-    numel = int(rec.numel)
-    is_float = torch.is_floating_point(ref)
-    active = policy_name(job.correctness_policy)
+    numel = rec.numel
+    is_float = job.is_float
+    active = job.active
     meta: Dict[str, Any] = {"path": path, "correctness_policy": active}
     if numel == 0 or not is_float:
         meta["cosine_similarity"] = None
@@ -495,52 +624,54 @@ def _meta_from_record(job: _Job) -> Tuple[bool, List[str], Dict[str, Any]]:
     else:
         meta["cosine_similarity"] = _rounded_or_convention(rec.sample_cosine, rec.sample_sum_gg, rec.sample_sum_rr)
         meta["norm_ratio"] = _norm_ratio_value(rec)
-    count = int(rec.mismatch_count)
+    count = rec.mismatch_count
     allclose = count == 0
     meta["mismatch_rate"] = round((count / numel) if numel else 0.0, 4)
-    meta["p99_abs"] = None if numel == 0 else float(rec.p99_abs)
-    meta["p99_rel"] = None if numel == 0 else float(rec.p99_rel)
+    meta["p99_abs"] = None if numel == 0 else rec.p99_abs
+    meta["p99_rel"] = None if numel == 0 else rec.p99_rel
     meta["allclose_pass"] = allclose
     meta["normal_metric_pass"] = False
     meta["cosine_metric_pass"] = False
     meta["norm_ratio_pass"] = False
     if is_float:
-        meta["finite_pass"] = int(rec.finite_violations) == 0
+        meta["finite_pass"] = rec.finite_violations == 0
         _near_zero_meta(job, meta, numel)
-    meta["metric_pass"] = False if allclose else _evaluate_tensor_policy(ref, meta, job.correctness_policy)
+    meta["metric_pass"] = False if allclose else _evaluate_tensor_policy(job.ref, meta, job.correctness_policy)
     meta["policy_pass"] = bool(allclose or meta["metric_pass"])
     if numel == 0 or count == 0:
         return True, [], meta
     if job.kpolicy.mode == _lib.MODE_MAX_ABS_DIFF:
         max_abs: Any = int(rec.mismatch_max_abs)
     else:
-        max_abs = float(rec.mismatch_max_abs)
-    max_rel = float(rec.mismatch_max_rel)
+        max_abs = rec.mismatch_max_abs
+    max_rel = rec.mismatch_max_rel
     meta["max_abs"] = float(max_abs)
     meta["max_rel"] = max_rel
-    first = "()" if ref.dim() == 0 else _unravel(int(rec.first_mismatch_index), ref.shape)
+    ref = job.ref
+    first = "()" if ref.dim() == 0 else _unravel(rec.first_mismatch_index, ref.shape)
     meta["first_mismatch_index"] = first
+    ok = bool(meta["policy_pass"])
+    if ok:
+        return True, [], meta
+    # (the policy failed, so policy_pass and metric_pass are False)
     detail = (
-        f"{path}: policy={active}, policy_pass={meta['policy_pass']}, "
-        f"allclose_pass={meta['allclose_pass']}, metric_pass={meta['metric_pass']}, "
-        f"normal_metric_pass={meta.get('normal_metric_pass')}, "
-        f"cosine_metric_pass={meta.get('cosine_metric_pass')}, "
-        f"near_zero_abs_pass={meta.get('near_zero_abs_pass')}, "
-        f"{count}/{numel} elements mismatched, "
+        f"{path}: policy={active}, policy_pass=False, allclose_pass=False, metric_pass=False, "
+        f"normal_metric_pass={meta['normal_metric_pass']}, cosine_metric_pass={meta['cosine_metric_pass']}, "
+        f"near_zero_abs_pass={meta.get('near_zero_abs_pass')}, {count}/{numel} elements mismatched, "
         f"max_abs={_format_number(max_abs)}, max_rel={_format_number(max_rel)}, "
         f"p99_abs={_format_number(meta['p99_abs'])}, p99_rel={_format_number(meta['p99_rel'])}, "
-        f"cosine_similarity={_format_number(meta.get('cosine_similarity'))}, "
-        f"norm_ratio={_format_number(meta.get('norm_ratio'))}, "
-        f"first_mismatch_index={first}, tolerance={job.tolerance}"
+        f"cosine_similarity={_format_number(meta['cosine_similarity'])}, "
+        f"norm_ratio={_format_number(meta['norm_ratio'])}, first_mismatch_index={first}, "
+        f"tolerance={job.tol_text if job.tol_text is not None else job.tolerance}"
     )
-    ok = bool(meta["policy_pass"])
-    return ok, ([] if ok else [detail]), meta
+    return False, [detail], meta
 
 
 def _rounded_or_convention(cos: float, gg: float, rr: float) -> float:
-    """GCR:364-372: exact 1.0 / 0.0 for zero norms, else round(cosine, 4)."""
-    g_zero = math.sqrt(gg) == 0.0
-    r_zero = math.sqrt(rr) == 0.0
+    """GCR:364-372: exact 1.0 / 0.0 for zero norms, else round(cosine, 4).  (A norm is the square root of
+    a sum of squares, which is >= 0, -0.0 or NaN: the norm is zero exactly when the sum is.)"""
+    g_zero = gg == 0.0
+    r_zero = rr == 0.0
     if g_zero and r_zero:
         return 1.0
     if g_zero or r_zero:
@@ -550,8 +681,8 @@ def _rounded_or_convention(cos: float, gg: float, rr: float) -> float:
 
 def _norm_ratio_value(rec) -> float:
     """GCR:383-393."""
-    g_zero = math.sqrt(rec.sample_sum_gg) == 0.0
-    r_zero = math.sqrt(rec.sample_sum_rr) == 0.0
+    g_zero = rec.sample_sum_gg == 0.0
+    r_zero = rec.sample_sum_rr == 0.0
     if g_zero and r_zero:
         return 1.0
     if g_zero:
@@ -568,9 +699,9 @@ def _near_zero_meta(job: _Job, meta: Dict[str, Any], numel: int) -> None:
     if th is None:
         return
     rec = job.record
-    near = int(rec.near_zero_count)
-    far = int(rec.far_count)
-    far_mm = int(rec.far_mismatch_count)
+    near = rec.near_zero_count
+    far = rec.far_count
+    far_mm = rec.far_mismatch_count
     meta["near_zero_abs"] = float(th["near_zero_abs"])
     meta["near_zero_rate"] = round((near / numel) if numel else 0.0, 4)
     meta["far_mismatch_rate"] = round((far_mm / far) if far else 0.0, 4)
@@ -579,9 +710,9 @@ def _near_zero_meta(job: _Job, meta: Dict[str, Any], numel: int) -> None:
         meta["near_zero_mean_abs"] = None
         meta["near_zero_bad_rate"] = 0.0
         return
-    meta["near_zero_p99_abs"] = float(rec.near_zero_p99_abs)
-    meta["near_zero_mean_abs"] = float(rec.near_zero_mean_abs)
-    meta["near_zero_bad_rate"] = round(int(rec.near_zero_bad_count) / near, 4)
+    meta["near_zero_p99_abs"] = rec.near_zero_p99_abs
+    meta["near_zero_mean_abs"] = rec.near_zero_mean_abs
+    meta["near_zero_bad_rate"] = round(rec.near_zero_bad_count / near, 4)
     meta["near_zero_abs_pass"] = bool(
         meta.get("finite_pass")
         and far_mm == 0
@@ -670,8 +801,13 @@ def verdict_record(generated: torch.Tensor, reference: torch.Tensor, tolerance_p
 
 
 def verdict_records(pairs, tolerance_policy=None, correctness_policy=None, max_samples: int = MAX_SAMPLES):
-    """Records of many (generated, reference) pairs from one batched device call."""
-    jobs = [_Job(g, r, f"output[{i}]", tolerance_policy, correctness_policy, max_samples, fp8_errors=False)
-            for i, (g, r) in enumerate(pairs)]
+    """Records of many pairs from one batched device call.  A pair is (generated, reference) or
+    (generated, reference, tolerance_policy): the third item, when given, is that pair's own
+    tolerance table in place of ``tolerance_policy``."""
+    jobs = []
+    for i, p in enumerate(pairs):
+        g, r = p[0], p[1]
+        tol = p[2] if len(p) > 2 and p[2] is not None else tolerance_policy
+        jobs.append(_Job(g, r, f"output[{i}]", tol, correctness_policy, max_samples, fp8_errors=False))
     _run_jobs(jobs)
     return [j.record.to_dict() for j in jobs]

@@ -11,8 +11,11 @@ from oracle import torch_verdict as tv
 
 # fp64 sums are accumulated in a different order on the device; the contract is 1e-6 relative
 SUM_RTOL = 1e-6
-# near_zero_mean_abs: torch sums float32 in its own cascade order; the device sums in fp64
-MEAN_RTOL = 1e-5
+# near_zero_mean_abs: torch sums float32 in its own cascade order; the device sums in fp64 and
+# rounds once.  Over 3,000 seeded near-zero samples (1 to 10^6 values: 1-ULP bf16 steps with
+# exact zeros, fp16 diffs, 30 binades of range, tiny values with rare large ones) the largest
+# relative gap between the two was 5.5e-7.
+MEAN_RTOL = 1e-6
 
 EXACT_FIELDS = ("ulp_hist", "nan_pairs", "equal_count", "max_abs_index", "max_rel_index", "finite_violations",
                 "first_finite_violation", "nan_gen", "nan_ref", "posinf_gen", "posinf_ref", "neginf_gen",

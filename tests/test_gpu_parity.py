@@ -221,12 +221,20 @@ def test_batch_matches_single_and_oracle(kv):
     gi, ri = synth.int8_pair(77_777, seed=10, changed=50)
     gm = torch.randn(33, 700)[:, :650]
     rm = gm + 1e-4
-    pairs = [(g, r) for g, r, _ in batch] + [(gi, ri), (gm, rm)]
-    recs = kv.verdict_records([(g.to(DEV), r.to(DEV)) for g, r in pairs],
-                              tolerance_policy={"FP32": {"rtol": 1e-5, "atol": 1e-5}})
-    for (g, r), rec in zip(pairs, recs):
-        probs = record_vs_oracle(rec, g, r, {"FP32": {"rtol": 1e-5, "atol": 1e-5}})
-        assert not probs, (tuple(g.shape), g.dtype, probs)
+    # each ragged member keeps its own tolerance (synth.RAGGED_TOLERANCES, four per dtype in turn)
+    name = {torch.float32: "FP32", torch.bfloat16: "BF16"}
+    pairs = [(g, r, {name[r.dtype]: t}) for g, r, t in batch]
+    pairs += [(gi, ri, None), (gm, rm, {"FP32": {"rtol": 1e-5, "atol": 1e-5}})]
+    assert len({(r.dtype, t[name[r.dtype]]["rtol"], t[name[r.dtype]]["atol"]) for _, r, t in pairs[:48]}) == 8
+    recs = kv.verdict_records([(g.to(DEV), r.to(DEV), t) for g, r, t in pairs])
+    for (g, r, t), rec in zip(pairs, recs):
+        probs = record_vs_oracle(rec, g, r, t)
+        mm = tv.mismatch_stats(g, r, t)
+        for k in ("mismatch_count", "first_mismatch_index"):
+            if rec[k] != mm[k]:
+                probs.append(f"{k}: device {rec[k]} != oracle {mm[k]} under {t}")
+        assert not probs, (tuple(g.shape), g.dtype, t, probs)
+    pairs = [(g, r) for g, r, _ in pairs]
     # nested outputs through the batched _compare_outputs
     gen = tuple(p[0].to(DEV) for p in pairs[:10])
     ref = tuple(p[1].to(DEV) for p in pairs[:10])
