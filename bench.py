@@ -23,7 +23,9 @@ reference's own torch-CPU verdict) on a bounded slice of the same workload.
 
 Configurations (BASELINE.json ``configs``): c0 fp32 1 Mi, c1 bf16 256 Mi
 (default, the headline), c2 fp16 4096x32768 strided, c3fp8 / c3int8 128 Mi,
-c4 ragged batch of 4096 fp32/bf16 pairs (events then bracket the whole call).
+c4 ragged batch of 4096 fp32/bf16 pairs (events then bracket the whole call);
+c1m50 is C1's shape with half of all elements moved by one code (for the
+tolerant policy on data that differs almost everywhere).
 
 ``--trial`` instead times the correctness trial's verdict stage on C1-shaped
 outputs: the device trial driver (kernelverse_amd/trial.py) against the
@@ -65,6 +67,11 @@ def make_workload(name: str, dev):
         return g, r, {"BF16": {"rtol": 1.6e-2, "atol": 1e-2}}, (
             "bf16 pair, 268,435,456 elements (1 GiB read); ref=bf16(N(0,2)); cand = ref with 1-ULP steps at 5% "
             "and 3-ULP steps at 0.01%; atol=1e-2 rtol=1.6e-2; full verdict + 16-bucket ULP histogram"), "bf16"
+    if name == "c1m50":
+        g, r = synth.c1_pair(dev, p1=0.5)
+        return g, r, {"BF16": {"rtol": 1.6e-2, "atol": 1e-2}}, (
+            "bf16 pair, 268,435,456 elements (1 GiB read); ref=bf16(N(0,2)); cand = ref with 1-ULP steps at 50% "
+            "and 3-ULP steps at 0.01% (C1's shape, half of all elements moved); atol=1e-2 rtol=1.6e-2"), "bf16"
     if name == "c0":
         g, r = synth.fp32_noise_pair(1 << 20, seed=0)
         return g.to(dev), r.to(dev), {"FP32": {"rtol": 1e-5, "atol": 1e-5}}, (

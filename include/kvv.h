@@ -92,8 +92,7 @@ enum kvv_mode {
 #define KVV_FLAG_NEAR_ZERO 0x1u   /* tolerant-policy near-zero diagnostics (generated_correctness_runner.py:481-548);
                                      honoured for fp16/bf16 pairs, the only dtypes the reference computes them for */
 #define KVV_FLAG_NEAR_EXACT 0x2u  /* with KVV_FLAG_NEAR_ZERO: take the near-zero sample in a second pass over the
-                                     inputs instead of from entries recorded in the main pass (see
-                                     KVV_STATUS_NEAR_RETRY) */
+                                     inputs instead of from entries recorded in the main pass */
 
 #define KVV_FLAG_WS_KEPT 0x4u    /* the workspace is the one the previous single-pair verdict on this device was
                                      given, and nothing has written it since (a caller that keeps one workspace
@@ -105,10 +104,10 @@ enum kvv_mode {
                                      clears), and a captured call leaves no record for the next call to trust.
                                      No counterpart in the reference (GCR:672-786 allocates per call). */
 
-/* kvv_result.status values. */
-#define KVV_STATUS_NEAR_RETRY 1   /* a single fp16/bf16 pair's near-zero elements with a nonzero abs_diff did not fit
-                                     the workspace's entry pool: the near-zero fields are not valid (the others
-                                     are); call again with KVV_FLAG_NEAR_EXACT */
+/* kvv_result.status values.  kvv_verdict and kvv_verdict_noalloc return status 0: near-zero
+ * entries that outgrow the workspace's pool are taken by reading that part of the pair again inside
+ * the same call.  KVV_STATUS_NEAR_RETRY keeps its value for callers built against ABI version 1. */
+#define KVV_STATUS_NEAR_RETRY 1   /* (no longer returned) the near-zero fields needed KVV_FLAG_NEAR_EXACT */
 
 typedef struct kvv_policy {
   int32_t mode;                /* enum kvv_mode */

@@ -24,7 +24,7 @@ MODE_ISCLOSE, MODE_MAX_ABS_DIFF = 0, 1
 FLAG_NEAR_ZERO = 0x1
 FLAG_NEAR_EXACT = 0x2
 FLAG_WS_KEPT = 0x4
-# kvv_result.status: the near-zero fields need the exact path (KVV_STATUS_NEAR_RETRY)
+# kvv_result.status value of ABI version 1 that kvv_verdict no longer returns (KVV_STATUS_NEAR_RETRY)
 STATUS_NEAR_RETRY = 1
 
 STATUS_NAMES = {0: "OK", -1: "INVALID", -2: "WORKSPACE", -3: "HIP", -4: "UNSUPPORTED"}

@@ -296,15 +296,21 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
 struct WsLayout {
   int64_t run_stride;
   size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample,
-      near_cm, ent, near_wave, ent_fill, near_psum, table, chunk_seg, isel_state, isel_seg, isel_chunk, isel_sums, subtab,
+      near_cm, ent, near_wave, ent_fill, wave_range, near_psum, table, chunk_seg, isel_state, isel_seg, isel_chunk,
+      isel_sums, subtab,
       submm, total;
 };
 
-// Near-zero entries of a single fp16/bf16 pair (kFlagNearEntries): at most
-// kEntPool 8-byte entries in all, split evenly over the main pass's waves;
-// kScatterMax blocks of the first tail launch place them.
+// Near-zero entries of a single fp16/bf16 pair (kFlagNearEntries), 8 bytes each,
+// split evenly over the main pass's waves.  A wave's share is an eighth of its
+// element range when the workspace holds that (the size kvv_workspace_size
+// asks for), else kEntPool entries in all (the least workspace such a verdict
+// runs with); never more than the wave's elements.  A wave whose entries do
+// not fit is read again by the first tail launch.  Up to kScatterMax blocks of
+// that launch place the entries, each for an equal run of consecutive waves.
 constexpr int64_t kEntPool = int64_t(1) << 21;
-constexpr int kScatterMax = 256;
+constexpr int64_t kEntFrac = 8;
+constexpr int kScatterMax = 2048;
 
 // How a single pair's near-zero diagnostics are taken: none, entries recorded
 // in the main pass, or the near-zero pass over the inputs after it.
@@ -357,6 +363,7 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
     L.ent = take((size_t)near.ent_total * 8);
     L.near_wave = take((size_t)near.waves * 4);
     L.ent_fill = take((size_t)near.waves * 4);
+    L.wave_range = take((size_t)near.waves * 8);
     L.near_psum = take((size_t)kScatterMax * 8);
   }
   if (nslots > 0) {
@@ -434,6 +441,7 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
     t.ent = at<uint2>(ws, L.ent);
     t.near_wave = at<uint32_t>(ws, L.near_wave);
     t.ent_fill = at<uint32_t>(ws, L.ent_fill);
+    t.wave_range = at<uint2>(ws, L.wave_range);
     t.nwaves = (int32_t)nm.waves;
     t.ent_quota = (uint32_t)(nm.ent_total / nm.waves);
     scatter = nm.waves < kScatterMax ? (int)nm.waves : kScatterMax;
@@ -443,7 +451,7 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   t.isel_sums = at<double>(ws, L.isel_sums);
   t.near_cm = near ? at<uint64_t>(ws, L.near_cm) : nullptr;
   const bool batch = dtable != nullptr;
-  auto launch = [&](int reduce_blocks, int level, int arr_lo, int narr, int extra = 0) -> int {
+  auto launch = [&](int reduce_blocks, int level, int arr_lo, int narr) -> int {
     TailArgs x = t;
     x.reduce_blocks = reduce_blocks;
     x.level = level;
@@ -456,7 +464,7 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
       chunks = 1;
       x.total_chunks = 1;
     }
-    const int64_t grid = reduce_blocks + (chunks > 0 ? (int64_t)narr * chunks : 0) + extra;
+    const int64_t grid = reduce_blocks + (chunks > 0 ? (int64_t)narr * chunks : 0);
     if (grid == 0) return KVV_OK;
     void (*fn)(TailArgs) = nullptr;
     switch (level) {
@@ -470,18 +478,18 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
     KVV_HIP(hipGetLastError());
     return KVV_OK;
   };
-  // (with near-zero entries the first launch's trailing blocks build the near-zero sample)
+  // near-zero entries: their own launch builds the near-zero sample and its level-0
+  // histogram, so the first tail launch selects it like abs and rel
+  if (scatter > 0) {
+    hipLaunchKernelGGL(near_scatter_kernel, dim3((unsigned)scatter), dim3(kBlock), 0, st, t);
+    KVV_HIP(hipGetLastError());
+  }
   // a single pair whose main pass did select level 0 of abs/rel starts at level 1 there
   const bool main_hist = seg0 && (seg0->flags & kFlagMainHist);
-  int rc = launch(nseg * t.reduce_roles, main_hist ? 3 : 0, 0, 2, scatter);
+  int rc = launch(nseg * t.reduce_roles, main_hist ? 3 : 0, 0, nm.entries ? 3 : 2);
   if (rc) return rc;
   if (stream_groups) {
     rc = launch(0, 4, 0, 2);
-    if (rc) return rc;
-  }
-  if (nm.entries && nslots == 0) {
-    // a small near-zero sample is selected once the first launch has placed the entries
-    rc = launch(0, 1, 2, 1);
     if (rc) return rc;
   }
   if (nm.exact) {
@@ -513,7 +521,7 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   if (nslots > 0) {
     const int narr = near ? 3 : 2;
     if (!main_hist) rc = launch(0, 1, 0, narr);
-    else if (near) rc = launch(0, 1, 2, 1);  // abs/rel took level 1 in the first launch
+    else if (nm.exact) rc = launch(0, 1, 2, 1);  // abs/rel (and an entries-built near-zero sample) took level 1 first
     if (rc) return rc;
     rc = launch(0, 2, 0, narr);
     if (rc) return rc;
@@ -586,7 +594,8 @@ struct SingleGeom {
   uint32_t ent_quota = 0;
 };
 
-int single_geom(const SegDesc& d, SingleGeom& g) {
+// full: the entry share of the size kvv_workspace_size asks for; else the least.
+int single_geom(const SegDesc& d, SingleGeom& g, bool full = true) {
   const bool nz = (d.flags & kFlagNearEntries) != 0;
   g.scan = scan_fn(d.dtype, d.mode, scan_kind(d), false, nz);
   if (!g.scan) return fail(KVV_E_INVALID, "no kernel for dtype");
@@ -606,9 +615,9 @@ int single_geom(const SegDesc& d, SingleGeom& g) {
   if (nz) {
     // an even share of the pool, but never more than a wave's elements
     g.near.waves = g.grid * kWaves > 0 ? g.grid * kWaves : kWaves;
-    // a scatter block places the entries of at most 64 waves
-    if (g.near.waves > (int64_t)kScatterMax * 64) return fail(KVV_E_UNSUPPORTED, "main-pass grid too large for the near-zero scatter");
-    const int64_t share = kEntPool / g.near.waves, range = max_ipw * (int64_t)d.item_elems;
+    const int64_t range = max_ipw * (int64_t)d.item_elems;
+    int64_t share = kEntPool / g.near.waves;
+    if (full && range / kEntFrac > share) share = range / kEntFrac;
     g.ent_quota = (uint32_t)(share < range ? share : range);
     g.near.ent_total = (int64_t)g.ent_quota * g.near.waves;
   }
@@ -696,7 +705,13 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   SingleGeom g;
   int rc = single_geom(d, g);
   if (rc) return rc;
-  const WsLayout L = single_layout(d, g);
+  WsLayout L = single_layout(d, g);
+  if (g.near.entries && ws_bytes < L.total) {
+    // a smaller workspace: the least entry pool (waves whose entries overflow it are read again)
+    rc = single_geom(d, g, false);
+    if (rc) return rc;
+    L = single_layout(d, g);
+  }
   rc = check_ws(L, ws, ws_bytes, out);
   if (rc) return rc;
   // A large group of a vector layout: the main pass's blocks histogram select
@@ -748,6 +763,7 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
       a.ent = at<uint2>(ws, L.ent);
       a.near_wave = at<uint32_t>(ws, L.near_wave);
       a.ent_fill = at<uint32_t>(ws, L.ent_fill);
+      a.wave_range = at<uint2>(ws, L.wave_range);
       a.ent_quota = g.ent_quota;
       // the near-zero sample starts at zero: entries fill in its nonzero values
       a.zero2_ptr = at<uint4>(ws, L.near_sample);
@@ -771,9 +787,11 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   return rc;
 }
 
-int single_workspace_bytes(const SegDesc& d, size_t* bytes) {
+// full: the workspace with the full entry share (what kvv_workspace_size reports);
+// else the least one a verdict runs with.
+int single_workspace_bytes(const SegDesc& d, size_t* bytes, bool full = true) {
   SingleGeom g;
-  const int rc = single_geom(d, g);
+  const int rc = single_geom(d, g, full);
   if (rc) return rc;
   *bytes = single_layout(d, g).total;
   return KVV_OK;
@@ -1069,7 +1087,7 @@ int kvv_verdict_noalloc(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_
   int rc = kvv::plan_single(gen, ref, policy, d);
   if (rc) return rc;
   size_t need = 0;
-  rc = kvv::single_workspace_bytes(d, &need);
+  rc = kvv::single_workspace_bytes(d, &need, false);
   if (rc) return rc;
   if (need > kvv::kScratchBytes)
     return kvv::fail(KVV_E_WORKSPACE, "this verdict needs " + std::to_string(need) +

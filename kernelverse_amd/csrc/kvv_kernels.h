@@ -167,6 +167,8 @@ struct ScanArgs {
   uint2* ent;              // (rank among the wave's near-zero elements, abs_diff bits)
   uint32_t* near_wave;
   uint32_t* ent_fill;
+  uint2* wave_range;       // the wave's items [x, y), relative to the segment's first item (a wave whose
+                           // entries did not fit is re-read from them by the first tail launch)
   uint32_t ent_quota;
   uint32_t pad_ent;
   uint32_t* slots;         // kFlagMainHist: the select slots (abs, rel) the blocks' level-0 histograms join
@@ -1834,6 +1836,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
       if (lane == 0) {
         a.near_wave[wave_id] = 0;
         a.ent_fill[wave_id] = 0;
+        a.wave_range[wave_id] = make_uint2(0u, 0u);
       }
     }
     // a single-segment launch folds one record per block: an empty wave still
@@ -1942,6 +1945,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
         if (lane == 0) {
           a.near_wave[wave_id] = sink.run_near;
           a.ent_fill[wave_id] = sink.over ? kNone32 : sink.n;
+          a.wave_range[wave_id] = make_uint2((uint32_t)(i0 - a.item_lo), (uint32_t)(i1 - a.item_lo));
         }
       }
       block_record_part(a, sm, acc, wc, w, base);

@@ -57,6 +57,7 @@ struct TailArgs {
   const uint2* ent;
   const uint32_t* near_wave;
   const uint32_t* ent_fill;
+  const uint2* wave_range;    // each wave's items (relative to the segment), for waves whose entries did not fit
   uint32_t ent_quota;
   int32_t nwaves;
   int32_t scatter_blocks;
@@ -212,11 +213,6 @@ __device__ inline void reduce_counts(const TailArgs& a, const SegDesc& d, int se
   } else if (F0 == LC_HIST0) {  // ULP histogram
     if (tid < kBuckets) o.ulp_hist[tid] = cnt(LC_HIST0 + tid);
   } else {  // mismatches, and the fields of no column
-    // a wave whose near-zero entries did not fit: the near-zero fields must come from the exact path
-    bool over = false;
-    if ((d.flags & kFlagNearEntries) && a.ent_fill)
-      for (int w = tid; w < a.nwaves; w += kBlock) over = over || a.ent_fill[w] == kNone32;
-    over = __syncthreads_or(over);
     if (tid != 0) return;
     const bool imode = d.mode == KVV_MODE_MAX_ABS_DIFF;
     o.numel = d.n;
@@ -228,7 +224,7 @@ __device__ inline void reduce_counts(const TailArgs& a, const SegDesc& d, int se
     o.sample_count = d.m;
     // an empty sample has no selection to write its quantiles
     if (d.m == 0) o.p99_abs = o.p99_rel = qnan;
-    o.status = over ? KVV_STATUS_NEAR_RETRY : 0;
+    o.status = 0;  // (a wave whose near-zero entries did not fit is re-read by the first tail launch)
     o.reserved = 0;
   }
 }
@@ -1265,110 +1261,23 @@ __device__ inline void select_final(const TailArgs& a, const SegDesc& d, int arr
 }
 
 // ------------------------------------------------------------ near-zero entries
-// Scatter block b of the first tail launch (a single pair with
-// kFlagNearEntries).  The entries of waves [w0, w1) get their rank in the
-// compacted near-zero array (GCR:525-529: abs_diff over |ref| <= near_zero_abs,
-// row-major): the near-zero elements before wave w0 plus the entry's rank
-// within its wave.  A sampled rank j (every rank when c <= max_samples, else
-// j = i*(c-1)//(m-1) for some i, GCR:346-347) puts its value at position i of
-// the near-zero sample, which the main pass zeroed: the near-zero elements
-// without an entry are its zeros.  The block adds its sampled values to the
-// array's level-0 histogram (the zeros join when the next level reads it),
-// counts them and their NaNs, and leaves their fp64 sum for the mean.
-__device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
-  constexpr int kMaxW = 64;  // waves per scatter block (kScatterMax blocks cover 16384 waves)
-  const SegDesc& d = a.seg0;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int nw = a.nwaves;
-  const int per = (nw + a.scatter_blocks - 1) / a.scatter_blocks;
-  const int w0 = b * per < nw ? b * per : nw;
-  const int w1 = w0 + per < nw ? w0 + per : nw;
-  // the near-zero count c, and the near-zero elements of the waves before w0
-  uint64_t tot = 0, before = 0;
-  for (int w = tid; w < nw; w += kBlock) {
-    const uint64_t x = a.near_wave[w];
-    tot += x;
-    before += w < w0 ? x : 0u;
-  }
-  tot = wave_sum(tot);
-  before = wave_sum(before);
-  uint64_t* red = reinterpret_cast<uint64_t*>(L.part);
-  uint32_t* woff = &L.h[1][0];        // entry offset of each of the block's waves (+ the total)
-  uint64_t* wbase = red + 2 * kWaves;  // rank base of each of the block's waves
-  if (lane == 0) {
-    red[wv] = tot;
-    red[kWaves + wv] = before;
-  }
-  for (int i = tid; i < 256; i += kBlock) L.h[0][i] = 0;
-  // the block's waves: entry counts (a wave whose entries did not fit has none
-  // here; the fold marks the call for the exact path) and near-zero counts
-  uint32_t fill = 0, nnear = 0;
-  if (tid < w1 - w0) {
-    fill = a.ent_fill[w0 + tid];
-    fill = fill == kNone32 ? 0u : fill;
-    nnear = a.near_wave[w0 + tid];
-  }
-  __syncthreads();
-  uint64_t c = 0, base = 0;
-  for (int i = 0; i < kWaves; ++i) {
-    c += red[i];
-    base += red[kWaves + i];
-  }
-  // exclusive prefixes over the block's waves (at most kMaxW = 64, which the
-  // host's scatter block count guarantees): the first wave scans them
-  if (tid < kMaxW) {
-    const uint32_t fi = wave_incl_scan(fill);
-    const uint64_t ni = nnear;
-    uint64_t incl = ni;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t v = __shfl_up(incl, o);
-      if (lane >= o) incl += v;
-    }
-    woff[tid] = fi - fill;
-    wbase[tid] = base + incl - ni;
-    if (tid == 63) woff[kMaxW] = fi;
-  }
-  __syncthreads();
-  const uint32_t total = woff[kMaxW];
-  const uint64_t ms = (uint64_t)d.max_samples;
-  const uint64_t m = c < ms ? c : ms;
-  const bool strided = c > ms;
-  const uint64_t num = strided ? c - 1 : 1, den = strided ? m - 1 : 1;
-  // the near-zero sample's slot is used only when that sample itself is a large
-  // group: a group of at most kSmall values is selected by select_small straight
-  // from the array, and only select_final (large groups) clears the slot again,
-  // which a kept workspace relies on
-  const bool large = d.lslot >= 0 && m > (uint64_t)kSmall;
-  uint32_t* slot = large ? a.slots + ((size_t)d.lslot * kArrays + 2) * kSlotWords : nullptr;
-  float* sample = const_cast<float*>(a.arr[2]) + d.sample_off;
-  double sum = 0.0;
-  uint32_t cnt = 0, nan = 0;
-  // the block's entries, wave after wave, all threads at once, 8 per thread per
-  // pass with their loads in flight together (k grows, so the wave index wi only
-  // moves forward)
-  constexpr int kEnt = 8;
-  int wi = 0;
-#pragma unroll 1
-  for (uint32_t k0 = tid; k0 < total; k0 += kEnt * kBlock) {
-    uint2 xs[kEnt];
-    uint64_t jb[kEnt];
-#pragma unroll
-    for (int u = 0; u < kEnt; ++u) {
-      const uint32_t k = k0 + (uint32_t)u * kBlock;
-      xs[u] = make_uint2(0u, 0u);
-      jb[u] = ~0ull;
-      if (k < total) {
-        while (wi + 1 < w1 - w0 && woff[wi + 1] <= k) ++wi;
-        xs[u] = a.ent[(size_t)(w0 + wi) * a.ent_quota + (k - woff[wi])];
-        jb[u] = wbase[wi];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kEnt; ++u) {
-    if (jb[u] == ~0ull) continue;
-    const uint2 x = xs[u];
-    const uint64_t j = jb[u] + x.x;
+// Where a sampled near-zero value goes: the near-zero sample (GCR:525-529 samples
+// the compacted array abs_diff[|ref| <= near_zero_abs] with the stride
+// i*(c-1)//(m-1) of GCR:346-347, or takes every rank when c <= max_samples).
+// The main pass zeroed the sample, so only nonzero values (NaN included) are
+// placed: the near-zero elements without one are its zeros.  Each placed value
+// joins the block's level-0 histogram (an LDS 256-bin histogram), its count,
+// NaN count and fp64 sum.
+struct NearPlace {
+  uint64_t c, m, num, den;
+  bool strided;
+  float* sample;
+  uint32_t* hist;  // LDS, 256 bins; null when the near-zero sample is a small group
+  double sum;
+  uint32_t cnt, nan;
+
+  // Rank j (0-based, in the compacted array) holding value v.
+  __device__ __forceinline__ void put(uint64_t j, float v) {
     uint64_t i = j;
     bool take = j < c;
     if (strided) {
@@ -1383,19 +1292,191 @@ __device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
       take = i < m && i * num < t + den;
     }
     if (take) {
-      const float v = __uint_as_float(x.y);
       sample[i] = v;
       sum += (double)v;
       ++cnt;
       if (v != v) ++nan;
-      else if (large) atomicAdd(&L.h[0][fkey(v) >> 24], 1u);
-    }
+      else if (hist) atomicAdd(&hist[fkey(v) >> 24], 1u);
     }
   }
-  sum = wave_sum(sum);
-  cnt = wave_sum(cnt);
-  nan = wave_sum(nan);
-  __syncthreads();  // (the rank bases in L.part are read above)
+};
+
+// A wave whose entries did not fit its share of the pool: its items are read
+// again (one item per block iteration, thread t taking the 8 consecutive
+// elements 8t..8t+7 of the item, so thread order is row-major order) and every
+// near-zero element at a sampled rank with a nonzero abs_diff is placed.
+// `base` is the number of near-zero elements before the wave.  Called by all
+// threads of the block; fp16/bf16 single pairs of a vector layout only.
+__device__ inline void near_refill(const TailArgs& a, const SegDesc& d, int w, uint64_t base, NearPlace& np,
+                                   SelectLds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint2 wr = a.wave_range[w];
+  const bool bf = d.dtype == KVV_BF16;
+  auto f32 = [bf](uint32_t code) -> float {
+    return bf ? __uint_as_float(code << 16) : Elem<KVV_F16>::f32((uint16_t)code);
+  };
+#pragma unroll 1
+  for (uint32_t it = wr.x; it < wr.y; ++it) {
+    const int64_t L0 = (int64_t)it * d.item_elems;
+    const int64_t L1 = L0 + d.item_elems < d.n ? L0 + d.item_elems : d.n;
+    const int64_t e0 = L0 + 8 * (int64_t)tid;
+    const int ne = e0 >= L1 ? 0 : (L1 - e0 >= 8 ? 8 : (int)(L1 - e0));
+    uint32_t gq[4] = {0u, 0u, 0u, 0u}, rq[4] = {0u, 0u, 0u, 0u};
+    if (ne > 0) {
+      int64_t og, orr;
+      elem_offsets(d, e0, og, orr);  // a vector layout: 8 consecutive elements never cross a row
+      const uint16_t* gp = reinterpret_cast<const uint16_t*>(d.g) + og;
+      const uint16_t* rp = reinterpret_cast<const uint16_t*>(d.r) + orr;
+      if (ne == 8) {
+        const uint4 x = nt_load16(gp), y = nt_load16(rp);
+        gq[0] = x.x; gq[1] = x.y; gq[2] = x.z; gq[3] = x.w;
+        rq[0] = y.x; rq[1] = y.y; rq[2] = y.z; rq[3] = y.w;
+      } else {
+        for (int k = 0; k < ne; ++k) {
+          gq[k >> 1] |= (uint32_t)gp[k] << ((k & 1) * 16);
+          rq[k >> 1] |= (uint32_t)rp[k] << ((k & 1) * 16);
+        }
+      }
+    }
+    uint32_t mask = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float rf = f32((rq[k >> 1] >> ((k & 1) * 16)) & 0xFFFFu);
+      mask |= (k < ne && fabsf(rf) <= d.nz_abs ? 1u : 0u) << k;
+    }
+    // exclusive block prefix of the threads' near-zero counts (row-major ranks)
+    const uint32_t cntt = (uint32_t)__popc(mask);
+    const uint32_t incl = wave_incl_scan(cntt);
+    __syncthreads();  // (the previous item's totals are read)
+    if (lane == 63) L.misc[wv] = incl;
+    __syncthreads();
+    uint32_t before = incl - cntt;
+    for (int q = 0; q < wv; ++q) before += L.misc[q];
+    const uint32_t total = L.misc[0] + L.misc[1] + L.misc[2] + L.misc[3];
+    uint64_t j = base + before;
+    while (mask) {
+      const int k = __builtin_ctz(mask);
+      mask &= mask - 1;
+      const float gf = f32((gq[k >> 1] >> ((k & 1) * 16)) & 0xFFFFu);
+      const float rf = f32((rq[k >> 1] >> ((k & 1) * 16)) & 0xFFFFu);
+      const float adf = fabsf(gf - rf);
+      if (!(adf == 0.0f)) np.put(j, adf);
+      ++j;
+    }
+    base += total;
+  }
+}
+
+// Scatter block b of the first tail launch (a single pair with
+// kFlagNearEntries) handles waves [w0, w1): the entries of each wave get their
+// rank in the compacted near-zero array (GCR:525-529: abs_diff over |ref| <=
+// near_zero_abs, row-major) -- the near-zero elements before the wave plus the
+// entry's rank within it -- and are placed (NearPlace); a wave whose entries did
+// not fit is read again (near_refill).  The block adds its placed values'
+// histogram to copy b mod 16 of the near-zero sample's level-0 histogram (the
+// zeros join when the next level reads it), their count and NaN count to the
+// slot, and leaves their fp64 sum for the mean.
+__device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
+  const SegDesc& d = a.seg0;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int nw = a.nwaves;
+  const int per = (nw + a.scatter_blocks - 1) / a.scatter_blocks;
+  const int w0 = b * per < nw ? b * per : nw;
+  const int w1 = w0 + per < nw ? w0 + per : nw;
+  // the near-zero count c, and the near-zero elements of the waves before w0: the
+  // per-wave counts in 16-byte loads, all of a thread's in flight at once (the
+  // array holds 256-byte aligned words; a partial last vector is read by element)
+  uint64_t tot = 0, before = 0;
+  {
+    constexpr int kQ = 4;  // 16-byte loads per thread and pass: 4 x 256 x 4 = 4096 waves
+    const uint4* q = reinterpret_cast<const uint4*>(a.near_wave);
+    const int nq = nw >> 2;
+#pragma unroll 1
+    for (int v0 = tid; v0 < nq; v0 += kQ * kBlock) {
+      uint4 x[kQ];
+#pragma unroll
+      for (int k = 0; k < kQ; ++k) x[k] = v0 + k * kBlock < nq ? q[v0 + k * kBlock] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int k = 0; k < kQ; ++k) {
+        const int w = 4 * (v0 + k * kBlock);
+        const uint32_t e[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          tot += e[j];
+          before += w + j < w0 ? e[j] : 0u;
+        }
+      }
+    }
+    for (int w = 4 * nq + tid; w < nw; w += kBlock) {
+      const uint64_t x = a.near_wave[w];
+      tot += x;
+      before += w < w0 ? x : 0u;
+    }
+  }
+  tot = wave_sum(tot);
+  before = wave_sum(before);
+  uint64_t* red = reinterpret_cast<uint64_t*>(L.part);
+  if (lane == 0) {
+    red[wv] = tot;
+    red[kWaves + wv] = before;
+  }
+  for (int i = tid; i < 256; i += kBlock) L.h[0][i] = 0;
+  __syncthreads();
+  uint64_t c = 0, base = 0;
+  for (int i = 0; i < kWaves; ++i) {
+    c += red[i];
+    base += red[kWaves + i];
+  }
+  const uint64_t ms = (uint64_t)d.max_samples;
+  const uint64_t m = c < ms ? c : ms;
+  if (b == 0 && tid == 0) {
+    // the near-zero count and sample count, for the selection's launches
+    a.near_cm[0] = c;
+    a.near_cm[1] = m;
+  }
+  NearPlace np;
+  np.c = c;
+  np.m = m;
+  np.strided = c > ms;
+  np.num = np.strided ? c - 1 : 1;
+  np.den = np.strided ? m - 1 : 1;
+  np.sample = const_cast<float*>(a.arr[2]) + d.sample_off;
+  // the near-zero sample's slot is used only when that sample itself is a large
+  // group: a group of at most kSmall values is selected by select_small straight
+  // from the array, and only select_final (large groups) clears the slot again,
+  // which a kept workspace relies on
+  const bool large = d.lslot >= 0 && m > (uint64_t)kSmall;
+  uint32_t* slot = large ? a.slots + ((size_t)d.lslot * kArrays + 2) * kSlotWords : nullptr;
+  np.hist = large ? &L.h[0][0] : nullptr;
+  np.sum = 0.0;
+  np.cnt = np.nan = 0;
+#pragma unroll 1
+  for (int w = w0; w < w1; ++w) {
+    const uint32_t fill = a.ent_fill[w];
+    if (fill == kNone32) {
+      near_refill(a, d, w, base, np, L);
+    } else {
+      // the wave's entries, 8 per thread per pass with their loads in flight together
+      const uint2* ent = a.ent + (size_t)w * a.ent_quota;
+      constexpr int kEnt = 8;
+#pragma unroll 1
+      for (uint32_t k0 = tid; k0 < fill; k0 += kEnt * kBlock) {
+        uint2 xs[kEnt];
+#pragma unroll
+        for (int u = 0; u < kEnt; ++u) {
+          const uint32_t k = k0 + (uint32_t)u * kBlock;
+          xs[u] = k < fill ? ent[k] : make_uint2(0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < kEnt; ++u)
+          if (k0 + (uint32_t)u * kBlock < fill) np.put(base + xs[u].x, __uint_as_float(xs[u].y));
+      }
+    }
+    base += a.near_wave[w];
+  }
+  const double sum = wave_sum(np.sum);
+  const uint32_t cnt = wave_sum(np.cnt), nan = wave_sum(np.nan);
+  __syncthreads();  // (the rank bases in L.part and the refill's L.misc are read)
   if (lane == 0) {
     L.part[wv] = sum;
     L.sh[wv] = cnt;
@@ -1403,9 +1484,9 @@ __device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
   }
   __syncthreads();
   if (tid == 0) {
-    double s = 0.0;
-    for (int i = 0; i < kWaves; ++i) s += L.part[i];
-    a.near_psum[b] = s;
+    double t = 0.0;
+    for (int i = 0; i < kWaves; ++i) t += L.part[i];
+    a.near_psum[b] = t;
     uint32_t tc = 0, tn = 0;
     for (int i = 0; i < kWaves; ++i) {
       tc += L.sh[i];
@@ -1415,8 +1496,10 @@ __device__ inline void near_scatter(const TailArgs& a, int b, SelectLds& L) {
     if (large && tn) atomicAdd(&slot[kMisc], tn);
   }
   if (large) {
+    // copy b mod 16: thousands of scatter blocks would otherwise serialise on the busiest bins
+    uint32_t* h0 = slot + kH0R + (b % kH0Copies) * 256;
     for (int i = tid; i < 256; i += kBlock)
-      if (L.h[0][i]) atomicAdd(&slot[kH0 + i], L.h[0][i]);
+      if (L.h[0][i]) atomicAdd(&h0[i], L.h[0][i]);
   }
 }
 
@@ -1428,11 +1511,20 @@ __global__ __launch_bounds__(kBlock) void fill_zero_kernel(uint4* p, int64_t n4)
     p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-// LEVEL 0: the first launch: leading blocks fold run records, trailing blocks
-// place near-zero entries, the others run select level 0 and select small
-// groups.  LEVEL 3: the first launch of a single pair whose main pass did
-// level 0 of its abs/rel samples (kFlagMainHist): as LEVEL 0, with select
-// level 1 for those arrays.  LEVEL 1: select level 1.  LEVEL 2: the final
+// The near-zero entries of a single pair (kFlagNearEntries), placed by their own
+// launch between the main pass and the first tail launch: block b handles its
+// run of waves (near_scatter); block 0 also leaves the near-zero count and
+// sample count for the selection that follows (the fold writes the same values).
+// Its few registers let many blocks share a CU: the work is latency-bound loads.
+__global__ __launch_bounds__(kBlock) void near_scatter_kernel(TailArgs a) {
+  __shared__ SelectLds lds;
+  near_scatter(a, (int)blockIdx.x, lds);
+}
+
+// LEVEL 0: the first launch: leading blocks fold run records, the others run
+// select level 0 and select small groups.  LEVEL 3: the first launch of a
+// single pair whose main pass did level 0 of its abs/rel samples
+// (kFlagMainHist): as LEVEL 0, with select level 1 for its large groups.  LEVEL 1: select level 1.  LEVEL 2: the final
 // read-off, by the first chunk block of each large group.
 // "Level" 4 selects the large groups of a many-group launch (select_group_stream).
 // BATCH: the segments come from the device table; otherwise the single pair's
@@ -1447,11 +1539,6 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
     return;
   }
   const int64_t sb = b - a.reduce_blocks;
-  if (kFirst && !BATCH && sb >= (int64_t)a.narr * a.total_chunks) {
-    // the trailing blocks of a single pair's first launch place its near-zero entries
-    near_scatter(a, (int)(sb - (int64_t)a.narr * a.total_chunks), lds.s);
-    return;
-  }
   const int arr = a.arr_lo + (int)(sb / a.total_chunks);
   const int64_t chunk = sb - (int64_t)(arr - a.arr_lo) * a.total_chunks;
   const int s = BATCH ? (int)a.chunk_seg[chunk] : 0;
@@ -1467,12 +1554,12 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
     return;
   }
   if (count <= kSmall || d.lslot < 0) {
-    // a near-zero sample built from entries is complete only after the first launch
-    const int small_level = arr == 2 && (d.flags & kFlagNearEntries) ? 1 : 0;
-    if ((kFirst ? 0 : LEVEL) == small_level && c == 0 && count <= kSmall) select_small(a, d, arr, count, lds.s);
+    if (kFirst && c == 0 && count <= kSmall) select_small(a, d, arr, count, lds.s);
     return;
   }
   if constexpr (LEVEL == 0) {
+    // (a near-zero sample built from entries had its level 0 from near_scatter_kernel)
+    if (arr == 2 && (d.flags & kFlagNearEntries)) return;
     if (c * d.sel_rounds * (int64_t)kSelChunk >= count) return;
     select_chunk<0>(a, d, arr, count, c, lds.s);
   } else if constexpr (LEVEL == 1 || LEVEL == 3) {

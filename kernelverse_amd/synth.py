@@ -212,9 +212,11 @@ def code_flip_pair_device(n: int, seed: int, device, dtype=torch.bfloat16, std: 
 # ------------------------------------------------------------ benchmark configurations
 # The five workloads of the verdict benchmark, generated on the device from fixed seeds.
 
-def c1_pair(device):
-    """C1: bf16, 268,435,456 elements; ref = bf16(N(0,2)); cand = ref with 1-ULP steps at 5% and 3-ULP at 0.01%."""
-    return code_flip_pair_device(268_435_456, seed=1, device=device, dtype=torch.bfloat16, std=2.0, p1=0.05, p3=1e-4)
+def c1_pair(device, p1: float = 0.05):
+    """C1: bf16, 268,435,456 elements; ref = bf16(N(0,2)); cand = ref with 1-ULP steps at 5% (or `p1`) and 3-ULP
+    at 0.01%.  p1 = 0.5 is the C1 shape with half of all elements moved (outputs of GEMM-like operators differ
+    almost everywhere, so under the tolerant policy most near-zero elements carry a nonzero abs_diff)."""
+    return code_flip_pair_device(268_435_456, seed=1, device=device, dtype=torch.bfloat16, std=2.0, p1=p1, p3=1e-4)
 
 
 # The 17 finite-pattern breaks of C2, by kind: (reference class, candidate value).

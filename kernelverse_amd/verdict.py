@@ -342,16 +342,12 @@ def _run_jobs(jobs: List[_Job]) -> None:
     """Runs every job's pair through libkvv (one call for one pair, a batch call otherwise).
 
     A single fp16/bf16 pair under the tolerant policy takes its near-zero
-    diagnostics from entries recorded in the main pass; when they do not fit
-    the workspace's pool the record says so (KVV_STATUS_NEAR_RETRY) and the
-    pair is run again with the near-zero pass over the inputs."""
+    diagnostics from entries recorded in the main pass; a part of the pair whose
+    entries outgrow the workspace's pool is read again inside the same call, so
+    every record comes back complete (status 0)."""
     if not jobs:
         return
     _launch(jobs)
-    retry = [j for j in jobs if j.record.status == _lib.STATUS_NEAR_RETRY]
-    for j in retry:
-        j.kpolicy.flags |= _lib.FLAG_NEAR_EXACT
-        _launch([j])
     for j in jobs:
         if j.record.status != 0:
             raise _lib.KvvLibraryError(f"the device verdict of {j.path} reported status {j.record.status}")
