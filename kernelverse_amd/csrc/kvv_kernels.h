@@ -801,6 +801,18 @@ __device__ __forceinline__ PhaseA phase_a(const SegDesc& d, StageP stage, uint32
         const double x = E::f64(c);
         if (e) s1 = fma(x, x, s1); else s0 = fma(x, x, s0);
       }
+    } else if constexpr (W == 32 && !NEAR) {
+      // one element per dword: the squares only where the wave has a fast pair
+      uint32_t f[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f[j] = dword_flags<DT>(gw[j], rw[j]);
+        m0 |= f[j] << (u * 4 + j);
+      }
+      if (__ballot((f[0] & f[1] & f[2] & f[3]) == 0u)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dword_fast_sums<DT, false>(gw[j] & ~flag_mask<W>(f[j]), nz_abs, s0, s1, nnear);
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -971,17 +983,30 @@ __device__ __forceinline__ PhaseA phase_a_dot(const SegDesc& d, StageP stage, ui
   return o;
 }
 
-// The wave's queue holds 64 * kQSlots entries (entry = (lane << 6) | slot, in
-// lane order).  queue_all appends every slow element of the lanes when they
-// fit and returns their number, else returns it without writing anything;
-// queue_part then appends the slots [p0, p0 + kQSlots) of every lane.
+// The wave's queue holds 64 * slots entries (entry = (lane << 6) | slot, in
+// lane order): kQSlots for 8- and 16-bit elements; 32- and 64-bit elements
+// (16 or 8 per lane and item) keep half of it, and the other half holds their
+// replicated ULP-bucket counters (QueueGeom).  queue_all appends every slow
+// element of the lanes when they fit and returns their number, else returns it
+// without writing anything; queue_part then appends the slots [p0, p0 + slots)
+// of every lane.
 constexpr int kQSlots = 16;
+constexpr int kRep = 16;  // copies of each ULP bucket counter of the dense path
+template <int DT>
+struct QueueGeom {
+  static constexpr bool wide = VecIO<DT>::NE <= 16;
+  static constexpr int slots = wide ? kQSlots / 2 : kQSlots;
+  static constexpr int rep_words = wide ? kBuckets * kRep : 1;
+  static_assert(!wide || 64 * slots * 2 >= kBuckets * kRep * 4, "the counters take the queue's other half");
+};
+
+template <int SLOTS>
 __device__ __forceinline__ uint32_t queue_all(uint64_t slow, uint16_t* queue) {
   const int lane = lane_id();
   const uint32_t cnt = (uint32_t)__popcll(slow);
   const uint32_t incl = wave_incl_scan(cnt);
   const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-  if (total > 64u * kQSlots) return total;
+  if (total > 64u * SLOTS) return total;
   uint32_t at = incl - cnt;
   while (slow) {
     queue[at++] = (uint16_t)((lane << 6) | __builtin_ctzll(slow));
@@ -990,9 +1015,10 @@ __device__ __forceinline__ uint32_t queue_all(uint64_t slow, uint16_t* queue) {
   return total;
 }
 
+template <int SLOTS>
 __device__ __forceinline__ uint32_t queue_part(uint32_t part, int p0, uint16_t* queue) {
   const int lane = lane_id();
-  part &= (1u << kQSlots) - 1;
+  part &= (1u << SLOTS) - 1;
   const uint32_t cnt = (uint32_t)__popc(part);
   const uint32_t incl = wave_incl_scan(cnt);
   const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
@@ -1058,6 +1084,101 @@ __device__ __forceinline__ bool phase_b_dense(const SegDesc& d, uint32_t R0, uin
     }
     return true;
   }
+}
+
+// Phase B in place for an fp32 item of mostly slow pairs under the isclose test
+// without near-zero diagnostics (e.g. every pair perturbed by noise): each lane
+// walks its own slots once and finishes every slow pair whose only outputs are
+// common ones, which are the abs key (argmax), the ULP bucket and the fp64
+// sums.  Such a pair is within tolerance, has a finite abs_diff, has values of
+// one sign, and has a rel_diff below the wave's rel-argmax bound.  For it,
+// slow_elem would change nothing else.  Its ULP bucket goes to copy lane % kRep
+// of the wave's replicated counters `rep` (no ballots, and at most four
+// increments of one element step meet at an address).
+//
+// The other slow pairs are mismatches, non-finite values, opposite signs and
+// rel-argmax candidates.  They are returned as a mask for the queue and
+// slow_elem.  The lean pairs of a lane come in ascending index order and
+// precede the item's queued pairs, so a strict key comparison keeps the lowest
+// index of a tie.  The bound only rises, so a pair below it now stays below it.
+// Taken when every lane has at least 3/4 of its slots slow.  Otherwise `slow`
+// comes back unchanged.
+template <int DT, int MODE>
+__device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, uint64_t slow, StageP stage,
+                                                 Acc& acc, KVV_LDS uint32_t* rep) {
+  constexpr int V = VecIO<DT>::V;
+  if constexpr (DT != KVV_F32 || MODE != KVV_MODE_ISCLOSE) {
+    return slow;
+  } else {
+    if (__ballot((uint32_t)__popcll(slow) * 4u < 3u * (uint32_t)VecIO<DT>::NE)) return slow;
+    const int lane = lane_id();
+    // close == (g == r) under a zero tolerance: an allowed bound of -inf
+    const bool zt = d.zero_tol != 0;
+    const float atol = zt ? -__builtin_inff() : d.atol;
+    const float rtol = zt ? 0.0f : d.rtol;
+    const float thr = acc.rel_thr;
+    KVV_LDS uint32_t* const mine = rep + (lane & (kRep - 1));
+    uint64_t rare = 0;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (__ballot(((slow >> (u * V)) & 0xFu) != 0) == 0) continue;
+      const uint4 gq = stage_vec(stage, (2 * u) * 64 + lane);
+      const uint4 rq = stage_vec(stage, (2 * u + 1) * 64 + lane);
+      const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w};
+      const uint32_t rw[4] = {rq.x, rq.y, rq.z, rq.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int p = u * 4 + e;
+        const bool act = ((slow >> p) & 1u) != 0;
+        const float g = __uint_as_float(gw[e]), r = __uint_as_float(rw[e]);
+        const float ad = fabsf(g - r);
+        const float allowed = atol + fabsf(rtol * g);
+        const bool close = g == r || ad <= allowed;
+        const float den = fabsf(r) + 1e-12f;
+        const bool lean = close && __builtin_isfinite(ad) && (int32_t)(gw[e] ^ rw[e]) >= 0 && ad < thr * den;
+        rare |= (uint64_t)(act && !lean) << p;
+        if (act && lean) {
+          const uint32_t key = __float_as_uint(ad) | 0x80000000u;
+          if (key > acc.gabs_k) {
+            acc.gabs_k = key;
+            acc.gabs_i = R0 + (uint32_t)((u * 64 + lane) * V + e);
+          }
+          // one sign: the ULP distance is the distance of the codes
+          const uint32_t a = gw[e] - rw[e], b = rw[e] - gw[e];
+          const int bl = 32 - __clz(a < b ? a : b);
+          atomicAdd((uint32_t*)(mine + (bl < kBuckets - 1 ? bl : kBuckets - 1) * kRep), 1u);
+          const double g64 = (double)g, r64 = (double)r;
+          const double d64 = g64 - r64;
+          acc.s[0] = fma(g64, g64, acc.s[0]);
+          acc.s[1] = fma(r64, r64, acc.s[1]);
+          acc.s[2] = fma(g64, r64, acc.s[2]);
+          acc.s[3] = fma(d64, d64, acc.s[3]);
+        }
+      }
+    }
+    return rare;
+  }
+}
+
+// Adds the wave's replicated ULP-bucket counters into its LDS counters and
+// clears them (before the wave's counters are read for a record).
+__device__ __forceinline__ void fold_rep(KVV_LDS uint32_t* rep, uint32_t* wc) {
+  const int lane = lane_id();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < kBuckets) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int c = 0; c < kRep; ++c) {
+      t += rep[lane * kRep + c];
+      rep[lane * kRep + c] = 0;
+    }
+    wc[LC_HIST0 + lane] += t;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // ------------------------------------------------------------ near-zero entries
@@ -1657,14 +1778,16 @@ __device__ inline void fold_block_record(const LdsRecord* rec, const RunCols& ou
 
 // ------------------------------------------------------------ scan kernel
 // LDS of one scan block: per wave, its item's vectors (SW uint4: kUnroll
-// vectors of each tensor per lane), its queue of stage positions (NQ = 64 lanes
-// x kQSlots), its sample buffer (SBW words for each of its consecutive sample
+// vectors of each tensor per lane), its queue of stage positions (NQ entries:
+// 64 lanes x the dtype's queue slots), its replicated ULP-bucket counters (RW
+// words), its sample buffer (SBW words for each of its consecutive sample
 // positions) and its counters.  Waves never touch each other's part.
-template <int SW, int NQ, int SBW>
+template <int SW, int NQ, int RW, int SBW>
 struct ScanShared {
   uint32_t done;  // waves of the block that have left their record (single-segment launches)
   uint4 stage[kWaves][SW];
   uint16_t queue[kWaves][NQ];
+  uint32_t rep[kWaves][RW];
   uint32_t sbuf[kWaves][SBW][SBW == 1 ? 384 : 320];
   uint32_t wcnt[kWaves][WC_COUNT];
   // kFlagMainHist: the block's level-0 histograms (2 x 128 words) and NaN counts (2)
@@ -1674,9 +1797,10 @@ struct ScanShared {
 template <int DT, int KIND>
 struct ScanLds {
   static constexpr bool vec = KIND != K_SCALAR;
+  using QG = QueueGeom<DT>;
   // (the scalar kind stages nothing, but its waves leave their run records there)
-  using type = ScanShared<vec ? 2 * kUnroll * 64 : (kColU32 * 4 + kColU64 * 8 + 15) / 16, vec ? 64 * kQSlots : 2,
-                         SampleWords<DT>::words>;
+  using type = ScanShared<vec ? 2 * kUnroll * 64 : (kColU32 * 4 + kColU64 * 8 + 15) / 16, vec ? 64 * QG::slots : 2,
+                          vec ? QG::rep_words : 1, SampleWords<DT>::words>;
 };
 
 // Per-item near-zero count of the wave (feeds the compacted-rank prefix of near_kernel).
@@ -1779,6 +1903,12 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
   const int tid = threadIdx.x, w = (int)uniform((uint32_t)(tid >> 6)), lane = tid & 63;
   uint32_t* wc = sm.wcnt[w];
   if (lane < WC_COUNT) wc[lane] = 0;
+  // the dense path's replicated ULP-bucket counters (fp32 isclose, vector kinds)
+  constexpr bool kLean = DT == KVV_F32 && MODE == KVV_MODE_ISCLOSE && KIND != K_SCALAR;
+  KVV_LDS uint32_t* const rep = (KVV_LDS uint32_t*)sm.rep[w];
+  if constexpr (kLean) {
+    for (int i = lane; i < kBuckets * kRep; i += 64) rep[i] = 0;
+  }
   if constexpr (!BATCH) {
     if (tid == 0) sm.done = 0;
   }
@@ -1909,17 +2039,22 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
         if constexpr (NZ) ni = near_item<DT>(d, stage, L0, L1, full_now);
         const uint64_t slow = phase_a_any<DT>(d, L0, R0, stage, full_now, acc, careful);
         if constexpr (NZ) near_entries<DT>(ni, slow, full_now, stage, sink);
-        if (__ballot(slow != 0) && phase_b_dense<DT, MODE>(d, R0, slow, stage, acc, wc)) {
-          // (an item of mostly slow pairs was finished in place)
-        } else if (__ballot(slow != 0)) {
-          uint32_t nq = queue_all(slow, sm.queue[w]);
-          // more than the queue holds: kQSlots slots of every lane at a time
-          const bool split = nq > 64u * kQSlots;
+        // what is left for the queue after an in-place pass over an item of mostly slow pairs
+        uint64_t left = slow;
+        if (__ballot(slow != 0)) {
+          if (kLean && !(d.flags & kFlagNearAny)) left = phase_b_lean<DT, MODE>(d, R0, slow, stage, acc, rep);
+          else if (phase_b_dense<DT, MODE>(d, R0, slow, stage, acc, wc)) left = 0;
+        }
+        if (__ballot(left != 0)) {
+          constexpr int QS = QueueGeom<DT>::slots;
+          uint32_t nq = queue_all<QS>(left, sm.queue[w]);
+          // more than the queue holds: QS slots of every lane at a time
+          const bool split = nq > 64u * QS;
 #pragma unroll 1
-          for (int p0 = 0;; p0 += kQSlots) {
-            if (split) nq = queue_part((uint32_t)(slow >> p0), p0, sm.queue[w]);
+          for (int p0 = 0;; p0 += QS) {
+            if (split) nq = queue_part<QS>((uint32_t)(left >> p0), p0, sm.queue[w]);
             if (nq) phase_b<DT, MODE>(d, R0, nq, stage, sm.queue[w], acc, wc);
-            if (!split || p0 + kQSlots >= VecIO<DT>::NE) break;
+            if (!split || p0 + QS >= VecIO<DT>::NE) break;
           }
         }
         if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, R0, full_now, stage, acc, wc);
@@ -1935,6 +2070,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
     }
     // the run's buffered samples join its record
     if constexpr (KIND != K_SCALAR) sbuf_store<DT, MODE>(d, sb, ba, br, a.sample_abs, a.sample_rel, acc, mh);
+    if constexpr (kLean) fold_rep(rep, wc);
     if constexpr (BATCH) {
       flush_run(acc, wc, ColSink{&a.runs, run_slot(d, run_start)}, base);
       if (it >= i1) break;
