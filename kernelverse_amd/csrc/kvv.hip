@@ -111,9 +111,9 @@ ScanFn scan_fn(int dt, int mode, int kind, bool batch, bool nz = false) {
   }
 }
 
-IselFn isel_fn(int dt, bool gather) {
+IselFn isel_fn(int dt, int which) {
   switch (dt) {
-#define KVV_CASE(X) case X: return KVV_ISEL_FN(X)(gather);
+#define KVV_CASE(X) case X: return KVV_ISEL_FN(X)(which);
     KVV_CASE(0) KVV_CASE(1) KVV_CASE(2) KVV_CASE(3) KVV_CASE(4) KVV_CASE(5)
     KVV_CASE(6) KVV_CASE(7) KVV_CASE(8) KVV_CASE(9) KVV_CASE(10) KVV_CASE(11)
     KVV_CASE(12) KVV_CASE(13) KVV_CASE(14)
@@ -297,9 +297,13 @@ struct WsLayout {
   int64_t run_stride;
   size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample,
       near_cm, ent, near_wave, ent_fill, wave_range, near_psum, table, chunk_seg, isel_state, isel_seg, isel_chunk,
-      isel_sums, subtab,
+      isel_sums, fb_segs, fb_counts, cap_runs, cap_chunks, subtab,
       submm, total;
 };
+
+// Work-list counts: the input-select passes' chunk lists (one per scan group),
+// their segment list, then the capture pass's chunk lists (one per scan group).
+constexpr int kMaxGroups = 15 * 2 * 3;
 
 // Near-zero entries of a single fp16/bf16 pair (kFlagNearEntries), 8 bytes each,
 // split evenly over the main pass's waves.  A wave's share is an eighth of its
@@ -375,8 +379,12 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
     L.table = take((size_t)nseg * sizeof(SegDesc));
     L.chunk_seg = take((size_t)chunks * 8);
     L.isel_seg = take((size_t)nisel * 4);
-    L.isel_chunk = take((size_t)isel_chunks * 8);
+    L.isel_chunk = take((size_t)isel_chunks * 8);  // the input-select passes' chunk work lists
     L.isel_sums = take((size_t)isel_chunks * 3 * 8);
+    L.fb_segs = take((size_t)nisel * 4);           // ... and their segment work list
+    L.fb_counts = take((size_t)(2 * kMaxGroups + 1) * 4);
+    L.cap_runs = take((size_t)run_slots * 16);
+    L.cap_chunks = take((size_t)isel_chunks * 8);  // the capture pass's chunk work lists
   }
   L.total = off + 256;
   return L;
@@ -843,6 +851,7 @@ struct BatchPlan {
     int seg_lo, seg_hi;
     int64_t item_lo, items, ipb;
     int64_t ick_lo, ick_n;  // this group's input-select chunks in isel_chunk
+    int64_t isel_lo, isel_n;  // this group's input-select segments in isel_seg
   };
   std::vector<int32_t> isel_seg;      // input-select segments
   std::vector<int32_t> isel_chunk;    // (segment, chunk of the segment) pairs, grouped like the scans
@@ -851,6 +860,9 @@ struct BatchPlan {
   int rounds = 1;              // select rounds per chunk block (every segment of the batch)
   int64_t items = 0, samples = 0, chunks = 0, nslots = 0, run_slots = 0;
   bool near = false;
+  // run-time work lists of the input-select and capture passes (host copies, filled by run_batch)
+  std::vector<int32_t> work_chunks, work_segs, cap_work;
+  std::vector<uint32_t> work_counts;
 };
 
 int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, const kvv_policy* pols, BatchPlan& bp) {
@@ -887,9 +899,13 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     SegDesc& d = segs[i];
     d.sel_rounds = group_mode ? 1 : rounds;
     d.chunk_count = group_mode ? (d.m > 0 ? 1 : 0) : select_chunks(d.m, rounds);
-    // a large contiguous group: the p99 of abs/rel is selected from the inputs,
-    // and the main pass neither walks nor writes its samples
-    if (group_mode && d.m > kSmall && kinds[i] == K_CONTIG) d.flags |= kFlagInputSelect;
+    // a large contiguous group: the p99 of abs/rel is selected from the inputs:
+    // the main pass captures its sampled values above pivot thresholds (and the
+    // input-select passes select it if that misses)
+    if (group_mode && d.m > kSmall && kinds[i] == K_CONTIG) {
+      d.flags |= kFlagInputSelect | kFlagCapture;
+      if (d.m == d.n) d.flags |= kFlagCaptureElems;
+    }
   }
   auto key = [&](int i) { return (segs[i].dtype * 2 + segs[i].mode) * 3 + kinds[i]; };
   std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return key(a) < key(b); });
@@ -909,16 +925,19 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     sample += (d.m + 63) & ~int64_t(63);  // each segment's samples start on a 256-byte line
     chunk += d.chunk_count;
     bp.near = bp.near || (d.flags & KVV_FLAG_NEAR_ZERO);
-    if (d.flags & kFlagInputSelect) {
-      d.isel_slot = (int32_t)bp.isel_seg.size();
-      bp.isel_seg.push_back(s);
-    }
     if (bp.groups.empty() || bp.groups.back().dt != d.dtype || bp.groups.back().mode != d.mode ||
         bp.groups.back().kind != kinds[i]) {
-      bp.groups.push_back({d.dtype, d.mode, kinds[i], s, s + 1, d.item_begin, d.item_count, 1, 0, 0});
+      bp.groups.push_back({d.dtype, d.mode, kinds[i], s, s + 1, d.item_begin, d.item_count, 1, 0, 0,
+                           (int64_t)bp.isel_seg.size(), 0});
     } else {
       bp.groups.back().seg_hi = s + 1;
       bp.groups.back().items += d.item_count;
+    }
+    if (d.flags & kFlagInputSelect) {
+      d.isel_slot = (int32_t)bp.isel_seg.size();
+      d.isel_group = (int32_t)bp.groups.size() - 1;
+      bp.isel_seg.push_back(s);
+      ++bp.groups.back().isel_n;
     }
     bp.table.push_back(d);
   }
@@ -937,8 +956,10 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   bp.chunks = chunk;
   // the input-select chunk launches follow the scan groups (one kernel per
   // dtype); strided-sample chunks (element loads, slower) are dispatched first
+  if (bp.groups.size() > (size_t)kMaxGroups) return fail(KVV_E_INVALID, "too many scan groups");
   for (auto& gr : bp.groups) {
     gr.ick_lo = (int64_t)bp.isel_chunk.size() / 2;
+    for (int s = gr.seg_lo; s < gr.seg_hi; ++s) bp.table[s].isel_gchunk0 = (int32_t)gr.ick_lo;
     for (int pass = 0; pass < 2; ++pass) {
       for (int s = gr.seg_lo; s < gr.seg_hi; ++s) {
         const SegDesc& d = bp.table[s];
@@ -979,13 +1000,88 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   if (rc) return rc;
   SegDesc* dtable = at<SegDesc>(ws, L.table);
   int64_t* dchunk = at<int64_t>(ws, L.chunk_seg);
+  uint32_t* istate = at<uint32_t>(ws, L.isel_state);
+  for (SegDesc& d : bp.table) {
+    if (!(d.flags & kFlagCapture)) continue;
+    // the capture buffers are the segment's sample region; the thresholds come from the pivot launch
+    d.cap_buf[0] = at<float>(ws, L.sample_abs) + d.sample_off;
+    d.cap_buf[1] = at<float>(ws, L.sample_rel) + d.sample_off;
+    d.cap_state = istate + (size_t)d.isel_slot * kIselStateWords;
+  }
   KVV_HIP(hipMemcpyAsync(dtable, bp.table.data(), nseg * sizeof(SegDesc), hipMemcpyHostToDevice, st));
   if (bp.chunks) KVV_HIP(hipMemcpyAsync(dchunk, bp.chunk_seg.data(), bp.chunks * 8, hipMemcpyHostToDevice, st));
   int32_t* disel = at<int32_t>(ws, L.isel_seg);
   int2* dichunk = at<int2>(ws, L.isel_chunk);
+  int32_t* dfbseg = at<int32_t>(ws, L.fb_segs);
+  uint32_t* dcounts = at<uint32_t>(ws, L.fb_counts);
+  int2* dcapchunk = at<int2>(ws, L.cap_chunks);
+  const int ngroups = (int)bp.groups.size();
   if (nisel) {
+    // work lists: the input-select passes' start with the segments that do not
+    // capture (none at present), to which the capture final adds those that
+    // fall back; the capture pass's hold the chunks of the capture segments
+    // with strided samples
+    bp.work_chunks.assign((size_t)isel_chunks * 2, 0);
+    bp.cap_work.assign((size_t)isel_chunks * 2, 0);
+    bp.work_segs.clear();
+    bp.work_counts.assign((size_t)2 * ngroups + 1, 0u);
+    for (int g = 0; g < ngroups; ++g) {
+      const auto& gr = bp.groups[g];
+      for (int64_t k = gr.ick_lo; k < gr.ick_lo + gr.ick_n; ++k) {
+        const int32_t s = bp.isel_chunk[2 * k];
+        const uint32_t f = bp.table[s].flags;
+        std::vector<int32_t>& list = (f & kFlagCapture) ? bp.cap_work : bp.work_chunks;
+        uint32_t& cnt = bp.work_counts[(f & kFlagCapture) ? ngroups + 1 + g : g];
+        if ((f & kFlagCapture) && (f & kFlagCaptureElems)) continue;  // captured by the main pass
+        const int64_t at_k = gr.ick_lo + cnt++;
+        list[2 * at_k] = s;
+        list[2 * at_k + 1] = bp.isel_chunk[2 * k + 1];
+      }
+    }
+    for (int32_t s : bp.isel_seg)
+      if (!(bp.table[s].flags & kFlagCapture)) bp.work_segs.push_back(s);
+    bp.work_counts[ngroups] = (uint32_t)bp.work_segs.size();
     KVV_HIP(hipMemcpyAsync(disel, bp.isel_seg.data(), nisel * 4, hipMemcpyHostToDevice, st));
-    KVV_HIP(hipMemcpyAsync(dichunk, bp.isel_chunk.data(), isel_chunks * 8, hipMemcpyHostToDevice, st));
+    KVV_HIP(hipMemcpyAsync(dichunk, bp.work_chunks.data(), isel_chunks * 8, hipMemcpyHostToDevice, st));
+    KVV_HIP(hipMemcpyAsync(dcapchunk, bp.cap_work.data(), isel_chunks * 8, hipMemcpyHostToDevice, st));
+    if (!bp.work_segs.empty())
+      KVV_HIP(hipMemcpyAsync(dfbseg, bp.work_segs.data(), bp.work_segs.size() * 4, hipMemcpyHostToDevice, st));
+    KVV_HIP(hipMemcpyAsync(dcounts, bp.work_counts.data(), (2 * ngroups + 1) * 4, hipMemcpyHostToDevice, st));
+  }
+  IselArgs ia{};
+  ia.table = dtable;
+  ia.segs = disel;
+  ia.state = istate;
+  ia.sums = at<double>(ws, L.isel_sums);
+  ia.buf[0] = at<float>(ws, L.sample_abs);
+  ia.buf[1] = at<float>(ws, L.sample_rel);
+  ia.res = out;
+  ia.cap_runs = at<uint4>(ws, L.cap_runs);
+  ia.fb_chunks = dichunk;
+  ia.fb_ccount = dcounts;
+  ia.fb_segs = dfbseg;
+  ia.fb_scount = dcounts + ngroups;
+  // input-select segments: their state is cleared, and the capture thresholds
+  // estimated, before the main pass (one block per segment, per dtype)
+  for (int g = 0; g < ngroups; ++g) {
+    const auto& gr = bp.groups[g];
+    if (gr.isel_n == 0) continue;
+    IselFn fn = isel_fn(gr.dt, 2);
+    if (!fn) return fail(KVV_E_INVALID, "no input-select kernel for dtype");
+    IselArgs x = ia;
+    x.segs = disel + gr.isel_lo;
+    hipLaunchKernelGGL(fn, dim3((unsigned)gr.isel_n), dim3(kBlock), 0, st, x);
+    KVV_HIP(hipGetLastError());
+    // then the capture pass over the strided samples of the group's capture segments
+    const int64_t ncap = bp.work_counts[ngroups + 1 + g];
+    if (ncap > 0) {
+      IselFn cf = isel_fn(gr.dt, 3);
+      IselArgs c = ia;
+      c.chunks = dcapchunk + gr.ick_lo;
+      c.nchunks = dcounts + ngroups + 1 + g;
+      hipLaunchKernelGGL(cf, dim3((unsigned)(ncap < kIselWorkBlocks ? ncap : kIselWorkBlocks)), dim3(kBlock), 0, st, c);
+      KVV_HIP(hipGetLastError());
+    }
   }
   std::vector<NearLaunch> nears;
   bool zeroed = false;
@@ -1004,10 +1100,12 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     a.sample_abs = at<float>(ws, L.sample_abs);
     a.sample_rel = at<float>(ws, L.sample_rel);
     a.item_near = bp.near ? at<uint32_t>(ws, L.item_near) : nullptr;
+    a.cap_runs = at<uint4>(ws, L.cap_runs);
     if (!zeroed) {
       // the first main-pass launch clears the select slots of the whole batch
+      // (the input-select states after them were cleared by the pivot launch)
       a.zero_ptr = at<uint4>(ws, L.slots);
-      a.zero_n4 = (int64_t)(L.slot_bytes / 16);
+      a.zero_n4 = (int64_t)((L.isel_state - L.slots) / 16);
       zeroed = true;
     }
     const int64_t grid = (gr.items + gr.ipb * kWaves - 1) / (gr.ipb * kWaves);
@@ -1015,28 +1113,31 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     KVV_HIP(hipGetLastError());
   }
   if (nisel) {
-    // p99 of the input-select segments: histograms, target bins, gather, final select
-    IselArgs ia{};
-    ia.table = dtable;
-    ia.segs = disel;
-    ia.state = at<uint32_t>(ws, L.isel_state);
-    ia.sums = at<double>(ws, L.isel_sums);
-    ia.buf[0] = at<float>(ws, L.sample_abs);
-    ia.buf[1] = at<float>(ws, L.sample_rel);
-    ia.res = out;
+    // p99 of the input-select segments: the capture segments' selection among
+    // their captured values; then, for the other input-select segments and for
+    // capture segments that missed, histograms, target bins, gather, final select
+    hipLaunchKernelGGL(isel_cap_final_kernel, dim3((unsigned)nisel), dim3(kBlock), 0, st, ia);
+    KVV_HIP(hipGetLastError());
+    // (the passes loop over their work lists, which may be short: at most kIselWorkBlocks blocks)
+    IselArgs wl = ia;
+    wl.segs = dfbseg;
+    wl.nsegs = dcounts + ngroups;
     for (int pass = 0; pass < 2; ++pass) {
-      for (const auto& gr : bp.groups) {
+      for (int g = 0; g < ngroups; ++g) {
+        const auto& gr = bp.groups[g];
         if (gr.ick_n == 0) continue;
-        IselFn fn = isel_fn(gr.dt, pass == 1);
+        IselFn fn = isel_fn(gr.dt, pass);
         if (!fn) return fail(KVV_E_INVALID, "no input-select kernel for dtype");
-        IselArgs x = ia;
+        IselArgs x = wl;
         x.chunks = dichunk + gr.ick_lo;
-        x.chunk_lo = gr.ick_lo;
-        hipLaunchKernelGGL(fn, dim3((unsigned)gr.ick_n), dim3(kBlock), 0, st, x);
+        x.nchunks = dcounts + g;
+        const int64_t grid = gr.ick_n < kIselWorkBlocks ? gr.ick_n : kIselWorkBlocks;
+        hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
         KVV_HIP(hipGetLastError());
       }
-      if (pass == 0) hipLaunchKernelGGL(isel_find_kernel, dim3((unsigned)nisel), dim3(kBlock), 0, st, ia);
-      else hipLaunchKernelGGL(isel_final_kernel, dim3((unsigned)nisel), dim3(kBlock), 0, st, ia);
+      const int64_t sgrid = nisel < kIselWorkBlocks ? nisel : kIselWorkBlocks;
+      if (pass == 0) hipLaunchKernelGGL(isel_find_kernel, dim3((unsigned)sgrid), dim3(kBlock), 0, st, wl);
+      else hipLaunchKernelGGL(isel_final_kernel, dim3((unsigned)sgrid), dim3(kBlock), 0, st, wl);
       KVV_HIP(hipGetLastError());
     }
   }

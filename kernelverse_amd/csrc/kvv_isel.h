@@ -34,27 +34,23 @@
 
 constexpr int kIselStage = 512;          // per-wave LDS stage of the gather, values per array
 
-// Per-segment state (u32 words), cleared by the main pass.
-enum IselWord {
-  IS_HIST = 0,                 // [2][2048] top-digit histograms of abs_diff, rel_diff (zeros aside)
-  IS_ZEROS = 2 * 2048,         // exact zeros (abs_diff == rel_diff == +0)
-  IS_FILL,                     // [2] values appended per array
-  IS_NAN = IS_FILL + 2,        // [2] the array holds a NaN
-  IS_PFX = IS_NAN + 2,         // [2][2] bin of each order statistic
-  IS_BASE = IS_PFX + 4,        // [2][2] values below each of those bins
-  kIselStateWords = 4160       // 16,640 bytes: a multiple of 256
-};
-static_assert(IS_BASE + 4 <= kIselStateWords && (kIselStateWords * 4) % 256 == 0, "input-select state");
-
 struct IselArgs {
-  const SegDesc* table;
-  const int2* chunks;      // chunk launches: (segment, chunk of the segment) per block
-  int64_t chunk_lo;        // chunk launches: batch-wide number of the launch's first chunk
-  double* sums;            // sampled sums per chunk (3 each)
-  const int32_t* segs;     // segment launches: segment per block
+  SegDesc* table;          // (the pivot launch writes the capture thresholds of its segments)
+  const int2* chunks;      // chunk launches: work list of (segment, chunk of the segment), one per block,
+  const uint32_t* nchunks; // ... of this length (the blocks past it have no work)
+  double* sums;            // sampled sums per chunk (3 each, at the segment's isel_chunk0 + chunk)
+  const int32_t* segs;     // segment launches: segment per block,
+  const uint32_t* nsegs;   // ... this many (null: one for every block)
   uint32_t* state;         // kIselStateWords per input-select segment (SegDesc::isel_slot)
   float* buf[2];           // the sample arrays: space for the appended abs_diff, rel_diff
   kvv_result* res;
+  const uint4* cap_runs;   // capture final: the run records of the main pass
+  // capture final: the work lists of the input-select passes, to which it adds the segments that fall back
+  // (chunks: a region per dtype group from SegDesc::isel_gchunk0, counted in fb_ccount[isel_group])
+  int2* fb_chunks;
+  uint32_t* fb_ccount;
+  int32_t* fb_segs;
+  uint32_t* fb_scount;
 };
 
 // abs_diff and the rel_diff denominator of one pair, as elem_test / sample_pair
@@ -192,12 +188,154 @@ __device__ __forceinline__ void unit_pass(const SegDesc& d, int64_t e0, int64_t 
   else sample_pass<DT, MODE>(d, e0, e1, f);
 }
 
-__device__ __forceinline__ void chunk_range(const IselArgs& a, const SegDesc*& d, int64_t& e0, int64_t& e1) {
-  const int2 ck = a.chunks[blockIdx.x];
+// Entry b of a chunk work list: its segment and element range.
+__device__ __forceinline__ void chunk_range(const IselArgs& a, uint32_t b, const SegDesc*& d, int64_t& e0,
+                                            int64_t& e1, int64_t& gchunk) {
+  const int2 ck = a.chunks[b];
   d = &a.table[ck.x];
   const int64_t len = isel_chunk_len(*d);
   e0 = (int64_t)ck.y * len;
   e1 = e0 + len < d->m ? e0 + len : d->m;
+  gchunk = d->isel_chunk0 + ck.y;
+}
+
+// The input-select passes take their work lists in block-strided loops: a
+// launch sized for every chunk (or segment) costs little when the lists are
+// short, which they are when every capture succeeds.
+constexpr int kIselWorkBlocks = 1024;
+
+// ------------------------------------------------------------ capture path
+// An input-select segment (kFlagCapture) is selected in one read of its
+// inputs (its samples are its elements, or strided positions among them):
+//
+//   isel_pivot_kernel      one block per segment, before the main pass: the
+//                          abs/rel keys of kPivotSamples values (kPivotRuns
+//                          runs of kPivotRun consecutive samples, spread over
+//                          the segment), and a lower bound of their order
+//                          statistic at kPivotRank from two histogram levels
+//                          (11 key bits each), which becomes the capture
+//                          threshold (cap_key);
+//   main pass              every nonzero sampled value whose key reaches its
+//                          threshold is written, compacted, into its run's
+//                          part of the segment's sample region (from the run's
+//                          first sample on); the others
+//                          are counted (IS_BELOW); each run leaves a record;
+//   isel_cap_final_kernel  one block per segment: the runs' captured values
+//                          are moved together, then an order statistic of
+//                          rank t lies among the zeros (t < zeros), the values
+//                          below the thresholds (missed) or the captured ones
+//                          (rank t - zeros - below there).  If either array
+//                          misses one, the segment is added to the work lists
+//                          of the input-select passes, which select it from
+//                          its inputs.
+//
+// The threshold rank leaves 88 of the 4096 pivot values above it: 1 % of them
+// (41) plus six standard deviations of that count (6.4 each) and a margin, so
+// the p99 ranks lie above the thresholds unless the pivot runs misrepresent
+// the segment, and about 2 % of the values are captured.
+constexpr int kPivotRuns = 64, kPivotRun = 64, kPivotSamples = kPivotRuns * kPivotRun;
+constexpr uint32_t kPivotRank = kPivotSamples - 88;
+static_assert(kPivotSamples == 16 * kBlock && kPivotRun == 64 && kSmall < kIselChunk,
+              "pivot values: 16 per thread, one run per wave and step, fewer than a capture segment's");
+
+// Capture thresholds.  A NaN among the pivot values (the p99 is then NaN)
+// captures the NaNs only.  cap_rel_lo bounds where rel_diff = abs_diff / den
+// can reach cap_key[1] without the division: a pair with abs_diff <
+// fl(cap_rel_lo * den) has fl(abs_diff / den) below the threshold value v,
+// since cap_rel_lo <= v * (1 - 2^-20) and every product stays a normal float
+// (v >= 2^-80, den >= 1e-12; larger v are capped at 2^127, past which only the
+// division tells).
+__device__ inline void set_thresholds(SegDesc& d, uint32_t ka, bool nan_a, uint32_t kr, bool nan_r) {
+  const uint32_t k0 = nan_a ? 0xFFFFFFFFu : ka, k1 = nan_r ? 0xFFFFFFFFu : kr;
+  d.cap_key[0] = k0 > kZeroKey ? k0 : kZeroKey + 1u;
+  d.cap_key[1] = k1 > kZeroKey ? k1 : kZeroKey + 1u;
+  const float v = fkey_value(d.cap_key[1]);
+  float lo;
+  if (d.cap_key[1] == 0xFFFFFFFFu) lo = __builtin_inff();
+  else if (v < 0x1p-80f) lo = 0.0f;
+  else lo = fminf(v * (1.0f - 0x1p-20f), 0x1p127f);
+  d.cap_rel_lo = lo;
+}
+
+// Counts of bins [tid * 8, tid * 8 + 8) of both block histograms.
+__device__ __forceinline__ void hist_bins8(const SelectLds& L, uint32_t cA[8], uint32_t cB[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    cA[i] = L.h[0][threadIdx.x * 8 + i];
+    cB[i] = L.h[1][threadIdx.x * 8 + i];
+  }
+}
+
+template <int DT, int MODE>
+__global__ __launch_bounds__(kBlock) void isel_pivot_kernel(IselArgs a) {
+  __shared__ SelectLds L;
+  const int tid = threadIdx.x;
+  SegDesc& d = a.table[a.segs[blockIdx.x]];
+  uint32_t* st = a.state + (size_t)d.isel_slot * kIselStateWords;
+  if (!(d.flags & kFlagCapture)) {
+    // the input-select passes accumulate into the whole state
+    for (int i = tid; i < kIselStateWords; i += kBlock) st[i] = 0;
+    return;
+  }
+  // the capture counters (the histograms are cleared if the segment falls back)
+  for (int i = IS_ZEROS + tid; i < kIselStateWords; i += kBlock) st[i] = 0;
+  // pivot value i = k * kBlock + tid is element i % 64 of run i / 64, which starts
+  // at floor(run * (m - kPivotRun) / (kPivotRuns - 1)): a wave reads one run per step
+  using T = typename Elem<DT>::T;
+  const uint64_t span = (uint64_t)(d.m - kPivotRun);
+  const double inv_den = 1.0 / (double)(d.m - 1);
+  uint32_t key[2][16];
+  uint32_t low[2] = {0u, 0u}, nan[2] = {0u, 0u};
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int i = k * kBlock + tid;
+    // (sample positions: the element of sample j is j itself when every element is a sample)
+    const int64_t j = (int64_t)((uint64_t)(i / kPivotRun) * span / (uint64_t)(kPivotRuns - 1)) + i % kPivotRun;
+    const int64_t e = d.m == d.n ? j : sample_index(d, j, inv_den);
+    const T gc = load_elem<DT>(d.g, e), rc = load_elem<DT>(d.r, e);
+    float adf, den;
+    diff_parts<DT, MODE>(gc, rc, adf, den);
+    key[0][k] = fkey(adf);
+    key[1][k] = fkey(adf / den);
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      low[x] += key[x][k] <= kZeroKey ? 1u : 0u;
+      nan[x] += key[x][k] == 0xFFFFFFFFu ? 1u : 0u;
+    }
+  }
+  // counts over the block: values at or below zero (their keys go first), NaNs
+  uint32_t lo_a = block_sum_nan(low[0], L), lo_r = block_sum_nan(low[1], L);
+  const bool na = block_sum_nan(nan[0], L) != 0, nr = block_sum_nan(nan[1], L) != 0;
+  // the order statistic at kPivotRank among the values above zero, by two 11-bit levels
+  uint32_t resid[2] = {kPivotRank >= lo_a ? kPivotRank - lo_a : 0u, kPivotRank >= lo_r ? kPivotRank - lo_r : 0u};
+  const bool zero_a = kPivotRank < lo_a, zero_r = kPivotRank < lo_r;
+  uint32_t pfx[2] = {0u, 0u};
+#pragma unroll 1
+  for (int lev = 0; lev < 2; ++lev) {
+    const int shift = lev == 0 ? 21 : 10;
+    for (int i = tid; i < 2 * 2048; i += kBlock) (&L.h[0][0])[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const uint32_t kk = key[x][k];
+        const bool in = kk > kZeroKey && (lev == 0 || (kk >> 21) == pfx[x]);
+        if (in) atomicAdd(&L.h[x][(kk >> shift) & 2047u], 1u);
+      }
+    }
+    __syncthreads();
+    uint32_t cA[8], cB[8], bin[2], below[2];
+    hist_bins8(L, cA, cB);
+    block_find2<8>(cA, cB, false, resid, bin, below, L.sh);
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      pfx[x] = lev == 0 ? bin[x] : ((pfx[x] << 21) | (bin[x] << 10));
+      resid[x] -= below[x];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) set_thresholds(d, zero_a ? kZeroKey : pfx[0], na, zero_r ? kZeroKey : pfx[1], nr);
 }
 
 template <int DT, int MODE>
@@ -207,9 +345,13 @@ __global__ __launch_bounds__(kBlock) void isel_hist_kernel(IselArgs a) {
   __shared__ uint32_t zs[kWaves];
   __shared__ double ss[kWaves][3];
   const int tid = threadIdx.x, lane = tid & 63;
+  const uint32_t nwork = *a.nchunks;
+#pragma unroll 1
+  for (uint32_t b = blockIdx.x; b < nwork; b += gridDim.x) {
   const SegDesc* d;
-  int64_t e0, e1;
-  chunk_range(a, d, e0, e1);
+  int64_t e0, e1, gchunk;
+  chunk_range(a, b, d, e0, e1, gchunk);
+  uint32_t* st = a.state + (size_t)d->isel_slot * kIselStateWords;
   for (int i = tid; i < 2 * (2048 + 64); i += kBlock) (&h[0][0])[i] = 0;
   __syncthreads();
   using E = Elem<DT>;
@@ -244,9 +386,8 @@ __global__ __launch_bounds__(kBlock) void isel_hist_kernel(IselArgs a) {
   if (tid < 3) {
     double t = 0.0;
     for (int w = 0; w < kWaves; ++w) t += ss[w][tid];
-    a.sums[(size_t)(a.chunk_lo + blockIdx.x) * 3 + tid] = t;
+    a.sums[(size_t)gchunk * 3 + tid] = t;
   }
-  uint32_t* st = a.state + (size_t)d->isel_slot * kIselStateWords;
   for (int i = tid; i < 2 * 2048; i += kBlock) {
     const uint32_t c = h[i >> 11][i & 2047];
     if (c) atomicAdd(&st[IS_HIST + i], c);
@@ -255,6 +396,8 @@ __global__ __launch_bounds__(kBlock) void isel_hist_kernel(IselArgs a) {
     uint32_t t = 0;
     for (int w = 0; w < kWaves; ++w) t += zs[w];
     if (t) atomicAdd(&st[IS_ZEROS], t);
+  }
+  __syncthreads();
   }
 }
 
@@ -285,12 +428,16 @@ template <int DT, int MODE>
 __global__ __launch_bounds__(kBlock) void isel_gather_kernel(IselArgs a) {
   __shared__ float stage[kWaves][2][kIselStage];
   const int w = threadIdx.x >> 6;
+  const uint32_t nwork = *a.nchunks;
+#pragma unroll 1
+  for (uint32_t b = blockIdx.x; b < nwork; b += gridDim.x) {
+  // (each wave's stage is its own and written out at the end of the chunk: no barrier between chunks)
   const SegDesc* d;
-  int64_t e0, e1;
-  chunk_range(a, d, e0, e1);
+  int64_t e0, e1, gchunk;
+  chunk_range(a, b, d, e0, e1, gchunk);
   uint32_t* st = a.state + (size_t)d->isel_slot * kIselStateWords;
   const bool nan0 = st[IS_NAN] != 0, nan1 = st[IS_NAN + 1] != 0;
-  if (nan0 && nan1) return;
+  if (nan0 && nan1) continue;
   const uint32_t p00 = st[IS_PFX], p01 = st[IS_PFX + 1], p10 = st[IS_PFX + 2], p11 = st[IS_PFX + 3];
   float* ba = a.buf[0] + d->sample_off;
   float* br = a.buf[1] + d->sample_off;
@@ -305,13 +452,206 @@ __global__ __launch_bounds__(kBlock) void isel_gather_kernel(IselArgs a) {
   });
   if (fa) stage_flush(stage[w][0], fa, &st[IS_FILL], ba);
   if (fr) stage_flush(stage[w][1], fr, &st[IS_FILL + 1], br);
+  }
+}
+
+// The capture pass of the capture segments with strided samples, one block
+// per chunk of their samples: the sampled values at or above the pivot
+// thresholds are appended (through per-wave LDS stages) to the segment's
+// sample region, counted in IS_FILL; the nonzero ones below are counted in
+// IS_BELOW; and the chunk's sampled sums are left as isel_hist_kernel leaves
+// them.  (Dense capture segments are captured by the main pass.)
+template <int DT, int MODE>
+__global__ __launch_bounds__(kBlock) void isel_capture_kernel(IselArgs a) {
+  __shared__ float stage[kWaves][2][kIselStage];
+  __shared__ uint32_t nb[kWaves][2];
+  __shared__ double ss[kWaves][3];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint32_t nwork = *a.nchunks;
+#pragma unroll 1
+  for (uint32_t b = blockIdx.x; b < nwork; b += gridDim.x) {
+    const SegDesc* d;
+    int64_t e0, e1, gchunk;
+    chunk_range(a, b, d, e0, e1, gchunk);
+    uint32_t* st = a.state + (size_t)d->isel_slot * kIselStateWords;
+    float* ba = a.buf[0] + d->sample_off;
+    float* br = a.buf[1] + d->sample_off;
+    const uint32_t k0 = d->cap_key[0], k1 = d->cap_key[1];
+    uint32_t fa = 0, fr = 0, b0 = 0, b1 = 0;
+    bool nan0 = false, nan1 = false, neg = false;
+    double sg = 0.0, sr = 0.0, sx = 0.0;
+    using E = Elem<DT>;
+    unit_pass<DT, MODE>(*d, e0, e1, [&](float adf, float den, bool act, typename E::T gc, typename E::T rc) {
+      const float rel = adf / den;
+      const bool nz = act && !(adf == 0.0f);
+      const bool ca = nz && fkey(adf) >= k0, cr = nz && fkey(rel) >= k1;
+      b0 += nz && !ca ? 1u : 0u;
+      b1 += nz && !cr ? 1u : 0u;
+      nan0 = nan0 || (ca && adf != adf);
+      nan1 = nan1 || (cr && rel != rel);
+      neg = neg || (act && adf < 0.0f);
+      stage_append(stage[w][0], fa, ca, adf, &st[IS_FILL], ba);
+      stage_append(stage[w][1], fr, cr, rel, &st[IS_FILL + 1], br);
+      // inactive lanes hold zero codes, which add 0
+      const double g64 = E::f64(gc), r64 = E::f64(rc);
+      sg = fma(g64, g64, sg);
+      sr = fma(r64, r64, sr);
+      sx = fma(g64, r64, sx);
+    });
+    if (fa) stage_flush(stage[w][0], fa, &st[IS_FILL], ba);
+    if (fr) stage_flush(stage[w][1], fr, &st[IS_FILL + 1], br);
+    if (__ballot(nan0) && lane == 0) st[IS_CNAN] = 1u;
+    if (__ballot(nan1) && lane == 0) st[IS_CNAN + 1] = 1u;
+    if (__ballot(neg) && lane == 0) st[IS_CNEG] = 1u;
+    b0 = wave_sum(b0);
+    b1 = wave_sum(b1);
+    // the chunk's sampled sums, in a fixed order (bit-reproducible)
+    sg = wave_sum(sg);
+    sr = wave_sum(sr);
+    sx = wave_sum(sx);
+    if (lane == 0) {
+      nb[w][0] = b0;
+      nb[w][1] = b1;
+      ss[w][0] = sg;
+      ss[w][1] = sr;
+      ss[w][2] = sx;
+    }
+    __syncthreads();
+    if (tid < 3) {
+      double t = 0.0;
+      for (int v = 0; v < kWaves; ++v) t += ss[v][tid];
+      a.sums[(size_t)gchunk * 3 + tid] = t;
+    } else if (tid < 5) {
+      uint32_t t = 0;
+      for (int v = 0; v < kWaves; ++v) t += nb[v][tid - 3];
+      if (t) atomicAdd(&st[IS_BELOW + tid - 3], t);
+    }
+    __syncthreads();
+  }
 }
 
 #ifdef KVV_COMMON_KERNELS
+// Where the order statistics of capture array x lie: rank t among the zeros
+// (the smallest values: need = false), among the values below the threshold
+// (a miss) or among the `cap` captured ones (need, at rank rk there).
+struct CapRanks {
+  bool miss, need[2];
+  uint32_t rk[2];
+};
+__device__ __forceinline__ CapRanks cap_ranks(const SegDesc& d, uint32_t cap, uint32_t below, bool nan,
+                                              const uint64_t rank[2]) {
+  CapRanks c;
+  // (more counted than the segment holds cannot happen; it would fall back)
+  c.miss = (uint64_t)cap + below > (uint64_t)d.m;
+  const uint64_t zeros = c.miss ? 0 : (uint64_t)d.m - cap - below;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    c.need[t] = !nan && !c.miss && rank[t] >= zeros + below;
+    c.rk[t] = c.need[t] ? (uint32_t)(rank[t] - zeros - below) : 0u;
+    c.miss = c.miss || (!nan && rank[t] >= zeros && rank[t] < zeros + below);
+  }
+  return c;
+}
+
+// Moves the runs' captured values of array x (each at its run's first element)
+// together at the start of the region, run after run (a run's values only move
+// down, over values already moved); within a run, a step of the block reads
+// all its values before it writes them.
+__device__ inline void cap_compact(const IselArgs& a, const SegDesc& d, int64_t nruns, int x) {
+  const int tid = threadIdx.x;
+  float* v = a.buf[x] + d.sample_off;
+  uint32_t pos = 0;
+  for (int64_t k = 0; k < nruns; ++k) {
+    const uint4 rec = a.cap_runs[d.run_slot0 + k];
+    const uint32_t c = x == 0 ? rec.y : rec.z;
+    if (rec.x != pos) {
+      constexpr int PER = 8;
+      for (uint32_t o = 0; o < c; o += PER * kBlock) {
+        float t[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const uint32_t j = o + i * kBlock + tid;
+          t[i] = j < c ? v[rec.x + j] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const uint32_t j = o + i * kBlock + tid;
+          if (j < c) v[pos + j] = t[i];
+        }
+        __threadfence_block();
+        __syncthreads();
+      }
+    }
+    pos += c;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void isel_cap_final_kernel(IselArgs a) {
+  __shared__ SelectLds L;
+  const int tid = threadIdx.x;
+  const int seg = a.segs[blockIdx.x];
+  const SegDesc& d = a.table[seg];
+  if (!(d.flags & kFlagCapture)) return;
+  uint32_t* st = a.state + (size_t)d.isel_slot * kIselStateWords;
+  uint64_t rank64[2];
+  float wgt;
+  q99_ranks(d.m, rank64, wgt);
+  // the captured totals: the main pass's runs' counts, or the capture pass's (already compact)
+  const bool elems = (d.flags & kFlagCaptureElems) != 0;
+  const int64_t nruns = elems ? segment_runs(d) : 0;
+  uint32_t t0 = 0, t1 = 0;
+  for (int64_t k = tid; k < nruns; k += kBlock) {
+    const uint4 rec = a.cap_runs[d.run_slot0 + k];
+    t0 += rec.y;
+    t1 += rec.z;
+  }
+  uint32_t cap[2] = {block_sum_nan(t0, L), block_sum_nan(t1, L)};
+  if (!elems) {
+    cap[0] = st[IS_FILL];
+    cap[1] = st[IS_FILL + 1];
+  }
+  const bool nan[2] = {st[IS_CNAN] != 0, st[IS_CNAN + 1] != 0};
+  const CapRanks c0 = cap_ranks(d, cap[0], st[IS_BELOW], nan[0], rank64);
+  const CapRanks c1 = cap_ranks(d, cap[1], st[IS_BELOW + 1], nan[1], rank64);
+  if (st[IS_CNEG] != 0 || c0.miss || c1.miss) {
+    // the input-select passes take the segment over, from cleared histograms and counts
+    __syncthreads();
+    for (int i = tid; i <= IS_BASE + 3; i += kBlock) st[i] = 0;
+    if (tid == 0) {
+      a.fb_segs[atomicAdd(a.fb_scount, 1u)] = seg;
+      const uint32_t nck = (uint32_t)((d.m + isel_chunk_len(d) - 1) / isel_chunk_len(d));
+      const uint32_t at = atomicAdd(&a.fb_ccount[d.isel_group], nck);
+      for (uint32_t ck = 0; ck < nck; ++ck) a.fb_chunks[d.isel_gchunk0 + at + ck] = make_int2(seg, (int)ck);
+    }
+    return;
+  }
+#pragma unroll 1
+  for (int x = 0; x < 2; ++x) {
+    const bool need0 = x == 0 ? c0.need[0] : c1.need[0], need1 = x == 0 ? c0.need[1] : c1.need[1];
+    const uint32_t rk0 = x == 0 ? c0.rk[0] : c1.rk[0], rk1 = x == 0 ? c0.rk[1] : c1.rk[1];
+    const uint32_t cx = x == 0 ? cap[0] : cap[1];
+    uint32_t key[2] = {kZeroKey, kZeroKey};
+    if (need0 || need1) {
+      if (elems) cap_compact(a, d, nruns, x);
+      const uint32_t r2[2] = {need0 ? rk0 : rk1, need1 ? rk1 : rk0};
+      uint32_t k[2];
+      range_keys(a.buf[x] + d.sample_off, cx, r2, k, L);
+      if (need0) key[0] = k[0];
+      if (need1) key[1] = k[1];
+    }
+    if (tid == 0) store_p99(a.res[d.out_index], x, key, wgt, x == 0 ? nan[0] : nan[1]);
+    __syncthreads();
+  }
+}
+
 __global__ __launch_bounds__(kBlock) void isel_find_kernel(IselArgs a) {
   __shared__ SelectLds L;
   const int tid = threadIdx.x;
-  const SegDesc& d = a.table[a.segs[blockIdx.x]];
+  const uint32_t nwork = *a.nsegs;
+#pragma unroll 1
+  for (uint32_t wi = blockIdx.x; wi < nwork; wi += gridDim.x) {
+  const SegDesc& d = a.table[a.segs[wi]];
   uint32_t* st = a.state + (size_t)d.isel_slot * kIselStateWords;
   uint64_t rank64[2];
   float wgt;
@@ -337,12 +677,16 @@ __global__ __launch_bounds__(kBlock) void isel_find_kernel(IselArgs a) {
     }
     __syncthreads();
   }
+  }
 }
 
 __global__ __launch_bounds__(kBlock) void isel_final_kernel(IselArgs a) {
   __shared__ SelectLds L;
   const int tid = threadIdx.x;
-  const SegDesc& d = a.table[a.segs[blockIdx.x]];
+  const uint32_t nwork = *a.nsegs;
+#pragma unroll 1
+  for (uint32_t wi = blockIdx.x; wi < nwork; wi += gridDim.x) {
+  const SegDesc& d = a.table[a.segs[wi]];
   const uint32_t* st = a.state + (size_t)d.isel_slot * kIselStateWords;
   uint64_t rank64[2];
   float wgt;
@@ -387,6 +731,7 @@ __global__ __launch_bounds__(kBlock) void isel_final_kernel(IselArgs a) {
     }
     if (tid == 0) store_p99(a.res[d.out_index], x, key, wgt, nan);
     __syncthreads();
+  }
   }
 }
 #endif  // KVV_COMMON_KERNELS

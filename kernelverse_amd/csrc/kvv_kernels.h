@@ -44,6 +44,31 @@ constexpr uint32_t kFlagNearAny = KVV_FLAG_NEAR_ZERO | kFlagNearEntries;
 // SegDesc.flags: a single pair whose main pass also histograms the top 8 key bits of its abs/rel
 // samples (select level 0) into the select slots, which a launch before it cleared
 constexpr uint32_t kFlagMainHist = 0x20000000u;
+// SegDesc.flags: an input-select segment whose sampled abs/rel values at or above the thresholds a
+// pivot launch estimated (cap_key) are captured and the nonzero ones below them counted; the p99
+// order statistics are then selected among the captured values.  With kFlagCaptureElems every
+// element is a sample (m == n) and the main pass captures; otherwise a capture pass over the
+// strided samples does.
+constexpr uint32_t kFlagCapture = 0x10000000u;
+constexpr uint32_t kFlagCaptureElems = 0x08000000u;
+// Per-segment input-select state (u32 words), cleared by the pivot launch
+// (IS_HIST .. IS_BASE: the input-select passes; the rest: the capture path).
+enum IselWord {
+  IS_HIST = 0,                 // [2][2048] top-digit histograms of abs_diff, rel_diff (zeros aside)
+  IS_ZEROS = 2 * 2048,         // exact zeros (abs_diff == rel_diff == +0)
+  IS_FILL,                     // [2] values appended (input-select gather) or captured, per array
+  IS_NAN = IS_FILL + 2,        // [2] the array holds a NaN
+  IS_PFX = IS_NAN + 2,         // [2][2] bin of each order statistic
+  IS_BASE = IS_PFX + 4,        // [2][2] values below each of those bins
+  IS_BELOW = IS_BASE + 4,      // [2] kFlagCapture: nonzero values below the capture thresholds
+  IS_CNAN = IS_BELOW + 2,      // [2] kFlagCapture: a captured value is NaN
+  IS_CNEG = IS_CNAN + 2,       // kFlagCapture: a negative abs_diff (an int32 difference of INT_MIN) sits
+                               // below the zeros, which the counts do not place: the segment falls back
+  IS_FALLBACK,                 // kFlagCapture: an order statistic lies below the thresholds, so the
+                               // input-select passes select this segment instead
+  kIselStateWords = 4160       // 16,640 bytes: a multiple of 256
+};
+static_assert(IS_FALLBACK < kIselStateWords && (kIselStateWords * 4) % 256 == 0, "input-select state");
 constexpr int64_t kIselChunk = 1 << 17;        // elements per input-select chunk (every element a sample)
 constexpr int64_t kIselChunkSampled = 1 << 15;  // samples per chunk at strided positions (element loads)
 // Per (large segment, array) slot: level-0 histogram (256), its kH0Copies
@@ -73,7 +98,12 @@ enum Layout { L_CONTIG = 0, L_ROWS = 1, L_GENERIC = 2 };
 enum ScanKind { K_CONTIG = 0, K_ROWS = 1, K_SCALAR = 2 };
 
 // Wave-level counters kept in LDS (one row per wave): the LdsCounter set.
-constexpr int WC_COUNT = LC_COUNT;
+// The wave's LDS counters: the run columns' counts, then (kFlagCapture) the
+// run's nonzero abs / rel values below the capture thresholds (added to the
+// segment's input-select state at the end of the run), its captured abs / rel
+// values so far, and the run's first element (where its captures go).
+constexpr int WC_BELOW = LC_COUNT, WC_CFILL = LC_COUNT + 2, WC_CBASE = LC_COUNT + 4;
+constexpr int WC_COUNT = LC_COUNT + 5;
 
 struct Dims {
   int32_t ndim;
@@ -120,6 +150,14 @@ struct SegDesc {
   int64_t run_slot0;      // first run slot of this segment (a multiple of 4)
   int64_t row_len;        // L_ROWS: contiguous inner length
   Dims dims;              // L_ROWS: outer dims; L_GENERIC: all dims
+  // kFlagCapture (the thresholds are written by the pivot launch, on the device):
+  float* cap_buf[2];      // where the captured abs / rel values go (the segment's sample region)
+  uint32_t* cap_state;    // the segment's input-select state words
+  uint32_t cap_key[2];    // capture the nonzero values whose key is at least these (abs, rel)
+  float cap_rel_lo;       // rel_diff can reach cap_key[1] only where abs_diff >= cap_rel_lo * den
+  int32_t isel_group;     // input-select: the segment's dtype group (its chunk work list and count)
+  int32_t isel_gchunk0;   // input-select: the start of that group's region of the chunk work list
+  int32_t isel_pad;
 };
 
 // Samples per input-select chunk of segment d.
@@ -172,6 +210,7 @@ struct ScanArgs {
   uint32_t ent_quota;
   uint32_t pad_ent;
   uint32_t* slots;         // kFlagMainHist: the select slots (abs, rel) the blocks' level-0 histograms join
+  uint4* cap_runs;         // batch, kFlagCapture: per run slot (first element, captured abs, captured rel, 0)
 };
 
 // Per-lane accumulators.  Counts live in the per-wave LDS counters instead.
@@ -311,6 +350,71 @@ __device__ __forceinline__ float wave_max_f32(float v) {
   return v;
 }
 
+// ------------------------------------------------------------ capture (kFlagCapture)
+// A run of items (one wave's, within one segment) writes its captured values
+// compacted into its own elements' part of the segment's sample region: from
+// the run's first element (WC_CBASE) on, WC_CFILL values per array.  A run
+// never captures more values than it has elements, so no space is reserved
+// and no atomic is taken; the run's counts go to a run record at its end.
+
+// Whether this lane is the lowest active lane of the wave (the one that
+// updates a wave-uniform LDS word).
+__device__ __forceinline__ bool first_active() {
+  return lane_id() == __ffsll((long long)__ballot(true)) - 1;
+}
+
+// Appends v for the lanes with p to the run's captures of array x.  Every
+// active lane of the wave calls it.
+__device__ __forceinline__ void cap_put(const SegDesc& d, uint32_t* wc, int x, bool p, float v) {
+  const uint64_t b = __ballot(p);
+  if (!b) return;
+  const uint32_t fill = wc[WC_CFILL + x], base = wc[WC_CBASE];
+  const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+  if (p) d.cap_buf[x][base + fill + below] = v;
+  if (first_active()) wc[WC_CFILL + x] = fill + (uint32_t)__popcll(b);
+}
+
+// Marks a capture array as holding a NaN when a lane with p captured one.
+__device__ __forceinline__ void cap_nan(const SegDesc& d, int x, bool p) {
+  const uint64_t b = __ballot(p);
+  if (b && lane_id() == __ffsll((long long)b) - 1) d.cap_state[IS_CNAN + x] = 1u;
+}
+
+// A capture segment's abs/rel values of the lanes with nz (nonzero abs_diff),
+// captured as ca / cr say, the others counted below the thresholds.
+__device__ __forceinline__ void capture_put(const SegDesc& d, uint32_t* wc, bool nz, bool ca, bool cr, float adf,
+                                            float rel) {
+  wave_add(wc, WC_BELOW, nz && !ca);
+  wave_add(wc, WC_BELOW + 1, nz && !cr);
+  if (__ballot(ca || cr)) {
+    cap_put(d, wc, 0, ca, adf);
+    cap_put(d, wc, 1, cr, rel);
+    cap_nan(d, 0, ca && adf != adf);
+    cap_nan(d, 1, cr && rel != rel);
+  }
+}
+
+// One element of a capture segment whose elements are all samples, for the
+// lanes with `act` (every active lane calls it).  A nonzero abs_diff (NaN
+// included) is captured when its key reaches cap_key[0], else counted below
+// the threshold; rel_diff likewise, divided out only where abs_diff can reach
+// its threshold.  Zeros are neither: they are what the counts leave of the
+// segment's m values.  A negative abs_diff (max_abs_diff mode: an int32
+// difference of INT_MIN) would sit below the zeros: it is flagged, and the
+// segment falls back.
+__device__ __forceinline__ void capture_elem(const SegDesc& d, float adf, float den, bool act, uint32_t* wc) {
+  const bool nz = act && !(adf == 0.0f);
+  if (__ballot(act && adf < 0.0f) && first_active()) d.cap_state[IS_CNEG] = 1u;
+  const bool ca = nz && fkey(adf) >= d.cap_key[0];
+  float rel = 0.0f;
+  bool cr = false;
+  if (nz && !(adf < d.cap_rel_lo * den)) {
+    rel = adf / den;
+    cr = fkey(rel) >= d.cap_key[1];
+  }
+  capture_put(d, wc, nz, ca, cr, adf, rel);
+}
+
 // Full treatment of one element for the lanes with `act` set.  Every lane of
 // the wave calls it (it uses ballots); counts go to the wave's LDS row `wc`.
 template <int DT, int MODE>
@@ -322,6 +426,7 @@ __device__ __forceinline__ void slow_elem(typename Elem<DT>::T gc, typename Elem
   bool mm;
   elem_test<DT, MODE>(gc, rc, d, adf, abs_key, mm, rf);
   const float den = fabsf(rf) + 1e-12f;
+  if (d.flags & kFlagCaptureElems) capture_elem(d, adf, den, act, wc);
   mm = mm && act;
   acc.nmm += mm ? 1u : 0u;
   if (mm) {
@@ -1105,7 +1210,7 @@ __device__ __forceinline__ bool phase_b_dense(const SegDesc& d, uint32_t R0, uin
 // comes back unchanged.
 template <int DT, int MODE>
 __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, uint64_t slow, StageP stage,
-                                                 Acc& acc, KVV_LDS uint32_t* rep) {
+                                                 Acc& acc, KVV_LDS uint32_t* rep, uint32_t* wc) {
   constexpr int V = VecIO<DT>::V;
   if constexpr (DT != KVV_F32 || MODE != KVV_MODE_ISCLOSE) {
     return slow;
@@ -1116,9 +1221,24 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
     const bool zt = d.zero_tol != 0;
     const float atol = zt ? -__builtin_inff() : d.atol;
     const float rtol = zt ? 0.0f : d.rtol;
-    const float thr = acc.rel_thr;
+    float thr = acc.rel_thr;
+    if (__ballot(!(thr > -__builtin_inff()))) {
+      // no bound yet (the run's first pairs): the largest finite rel_diff of the
+      // wave's slot-0 pairs gives one.  The pairs that reach it are queued, so
+      // every pair skipped below it has a strictly smaller rel_diff than a
+      // pair slow_elem will see.
+      const float g = stage_elem<float>(stage, lane, 0), r = stage_elem<float>(stage, 64 + lane, 0);
+      const float rel = fabsf(g - r) / (fabsf(r) + 1e-12f);
+      const float m = wave_max_f32((slow & 1u) && __builtin_isfinite(rel) ? rel : -__builtin_inff());
+      if (m > -__builtin_inff()) {
+        const float t = rel_threshold(m);
+        thr = t > thr ? t : thr;
+      }
+    }
     KVV_LDS uint32_t* const mine = rep + (lane & (kRep - 1));
     uint64_t rare = 0;
+    const bool capseg = (d.flags & kFlagCaptureElems) != 0;
+    uint32_t cm[2] = {0u, 0u};  // capture segment: the lean slots whose abs / rel value is captured
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (__ballot(((slow >> (u * V)) & 0xFu) != 0) == 0) continue;
@@ -1153,6 +1273,46 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
           acc.s[1] = fma(r64, r64, acc.s[1]);
           acc.s[2] = fma(g64, r64, acc.s[2]);
           acc.s[3] = fma(d64, d64, acc.s[3]);
+          if (capseg) {
+            // (a lean abs_diff is finite and nonzero)
+            const bool ca = key >= d.cap_key[0];
+            bool cr = false;
+            if (!(ad < d.cap_rel_lo * den)) cr = fkey(ad / den) >= d.cap_key[1];
+            cm[0] |= (ca ? 1u : 0u) << p;
+            cm[1] |= (cr ? 1u : 0u) << p;
+          }
+        }
+      }
+    }
+    if (capseg) {
+      // the captured values of the lean pairs, lane by lane in slot order, from
+      // the stage, after the run's captures so far; the lean pairs not captured
+      // are nonzero values below the threshold
+      const uint32_t nl = (uint32_t)__popcll(slow & ~rare);
+      const uint32_t c0 = (uint32_t)__popc(cm[0]), c1 = (uint32_t)__popc(cm[1]);
+      const uint32_t pk = c0 | (c1 << 16);  // (a wave adds at most 1024 to each half)
+      const uint32_t incl = wave_incl_scan(pk);
+      const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+      const uint32_t nb = wave_sum((nl - c0) | ((nl - c1) << 16));
+      if (tot | nb) {
+        const uint32_t base = wc[WC_CBASE], f0 = wc[WC_CFILL], f1 = wc[WC_CFILL + 1];
+        const uint32_t ex = incl - pk;
+        uint32_t at[2] = {base + f0 + (ex & 0xFFFFu), base + f1 + (ex >> 16)};
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          for (uint32_t mk = cm[x]; mk; mk &= mk - 1) {
+            const int p = __builtin_ctz(mk), u = p >> 2, e = p & 3;
+            const float g = stage_elem<float>(stage, (2 * u) * 64 + lane, e);
+            const float r = stage_elem<float>(stage, (2 * u + 1) * 64 + lane, e);
+            const float ad = fabsf(g - r);
+            d.cap_buf[x][at[x]++] = x == 0 ? ad : ad / (fabsf(r) + 1e-12f);
+          }
+        }
+        if (lane == 0) {
+          wc[WC_CFILL] = f0 + (tot & 0xFFFFu);
+          wc[WC_CFILL + 1] = f1 + (tot >> 16);
+          wc[WC_BELOW] += nb & 0xFFFFu;
+          wc[WC_BELOW + 1] += nb >> 16;
         }
       }
     }
@@ -1836,7 +1996,10 @@ __device__ __forceinline__ uint64_t phase_a_any(const SegDesc& d, int64_t L0, ui
     o = phase_a<DT, true>(d, stage, full);
   } else if constexpr (DotForm<DT>::on) {
     bool redone = false;
-    if (__ballot(full != (1u << kUnroll) - 1) != 0) {
+    if (d.flags & kFlagCaptureElems) {
+      // the sampled sums of such a segment are its full sums: exact squares
+      o = phase_a<DT, false>(d, stage, full);
+    } else if (__ballot(full != (1u << kUnroll) - 1) != 0) {
       // a partial last vector (its elements are left to vec_tail): per-vector form
       o = phase_a<DT, false>(d, stage, full);
     } else if (careful) {
@@ -2002,8 +2165,10 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
     const int64_t run_end = i1 < seg_end ? i1 : seg_end;
     const int64_t base = (run_start - d.item_begin) * (int64_t)d.item_elems;  // the run's first element
     const bool dense = d.m == d.n;
-    uint32_t near_prev = 0;
     SampleCursor cur = cursor_at(d, base);
+    // the run's first element, where its captures start (such a segment has at most 2^24 elements)
+    if ((d.flags & kFlagCaptureElems) && lane == 0) wc[WC_CBASE] = (uint32_t)base;
+    uint32_t near_prev = 0;
     uint4 gv[kUnroll], rv[kUnroll];
     uint32_t full = 0;
     RowCursor rcur = row_cursor_at(d, run_start - d.item_begin);
@@ -2042,7 +2207,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
         // what is left for the queue after an in-place pass over an item of mostly slow pairs
         uint64_t left = slow;
         if (__ballot(slow != 0)) {
-          if (kLean && !(d.flags & kFlagNearAny)) left = phase_b_lean<DT, MODE>(d, R0, slow, stage, acc, rep);
+          if (kLean && !(d.flags & kFlagNearAny)) left = phase_b_lean<DT, MODE>(d, R0, slow, stage, acc, rep, wc);
           else if (phase_b_dense<DT, MODE>(d, R0, slow, stage, acc, wc)) left = 0;
         }
         if (__ballot(left != 0)) {
@@ -2057,7 +2222,8 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
             if (!split || p0 + QS >= VecIO<DT>::NE) break;
           }
         }
-        if (full_now != (1u << kUnroll) - 1) vec_tail<DT, MODE>(d, L0, L1, R0, full_now, stage, acc, wc);
+        // (every lane enters: slow_elem's wave-wide steps then see the whole wave)
+        if (__ballot(full_now != (1u << kUnroll) - 1)) vec_tail<DT, MODE>(d, L0, L1, R0, full_now, stage, acc, wc);
         if constexpr (NZ) {
           // every near-zero element of the item joins the run's count
           if (lane == 0) acc.nnear_fast += ni.total;
@@ -2071,6 +2237,22 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
     // the run's buffered samples join its record
     if constexpr (KIND != K_SCALAR) sbuf_store<DT, MODE>(d, sb, ba, br, a.sample_abs, a.sample_rel, acc, mh);
     if constexpr (kLean) fold_rep(rep, wc);
+    if (BATCH && (d.flags & kFlagCaptureElems)) {
+      // the run's record (its first element and captured counts) and its values below the thresholds
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint32_t f0 = wc[WC_CFILL], f1 = wc[WC_CFILL + 1];
+      if (lane < 2) {
+        const uint32_t b = wc[WC_BELOW + lane];
+        if (b) atomicAdd(d.cap_state + IS_BELOW + lane, b);
+      }
+      if (lane == 0) a.cap_runs[run_slot(d, run_start)] = make_uint4(wc[WC_CBASE], f0, f1, 0u);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (lane < 4) wc[WC_BELOW + lane] = 0;
+    }
     if constexpr (BATCH) {
       flush_run(acc, wc, ColSink{&a.runs, run_slot(d, run_start)}, base);
       if (it >= i1) break;

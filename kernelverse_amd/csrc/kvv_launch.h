@@ -18,7 +18,7 @@ using IselFn = void (*)(IselArgs);
 #define KVV_DECLARE(dt)                          \
   ScanFn KVV_SCAN_FN(dt)(int mode, int kind, bool batch, bool nz); \
   NearFn KVV_NEAR_FN(dt)(int mode);                      \
-  IselFn KVV_ISEL_FN(dt)(bool gather);
+  IselFn KVV_ISEL_FN(dt)(int which);
 
 KVV_DECLARE(0)
 KVV_DECLARE(1)

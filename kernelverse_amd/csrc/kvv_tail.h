@@ -332,7 +332,12 @@ __device__ inline void reduce_sums(const TailArgs& a, const SegDesc& d, int64_t 
   if (tid == 0) {
     // the sampled sums; an input-select segment's are its chunks', in chunk order
     double sg = sum(4), sr = sum(5), sx = sum(6);
-    if (d.flags & kFlagInputSelect) {
+    if (d.flags & kFlagCaptureElems) {
+      // every element is a sample: the sampled sums are the full ones (exact fp64 squares)
+      sg = sum(0);
+      sr = sum(1);
+      sx = sum(2);
+    } else if (d.flags & kFlagInputSelect) {
       sg = sr = sx = 0.0;
       const int64_t nck = (d.m + isel_chunk_len(d) - 1) / isel_chunk_len(d);
       for (int64_t c = 0; c < nck; ++c) {
@@ -798,6 +803,115 @@ __device__ inline bool stream_keys(const float* v, int64_t count, const uint32_t
     group_pass_ranks<10>(same, key, resid, L);
   }
   return has_nan;
+}
+
+// The keys of the order statistics of ranks rank[0] <= rank[1] among `count`
+// values, by radix passes over the values' own key range: the first pass
+// bins [min key, max key] into 2048 bins (shifting off the low bits the range
+// needs beyond 11), each later pass bins the key range of the rank's bin, down
+// to a single key (at most three passes for 32-bit keys).  Values that share a
+// narrow range (e.g. the top few percent of a distribution, whose leading key
+// bits agree) thus spread over the bins instead of meeting in a few LDS words.
+// Values stay in registers when there are at most kSmall of them, else every
+// pass reads them again.  Returns whether a value is NaN (the keys are then
+// not searched).  Called by all threads of the block.
+__device__ inline bool range_keys(const float* v, uint32_t count, const uint32_t rank[2], uint32_t key[2],
+                                  SelectLds& L) {
+  constexpr int PER = kSmall / kBlock;
+  const int tid = threadIdx.x;
+  const bool regs = count <= (uint32_t)kSmall;
+  uint32_t k[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t idx = (uint32_t)(i * kBlock + tid);
+    k[i] = regs && idx < count ? fkey(v[idx]) : 0u;
+  }
+  // f(key) for every value of this thread
+  auto visit = [&](auto&& f) {
+    if (regs) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        if ((uint32_t)(i * kBlock + tid) < count) f(k[i]);
+    } else {
+      // eight loads in flight per thread
+      for (uint32_t i0 = 0; i0 < count; i0 += 8 * kBlock) {
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t idx = i0 + (uint32_t)(i * kBlock + tid);
+          t[i] = idx < count ? v[idx] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (i0 + (uint32_t)(i * kBlock + tid) < count) f(fkey(t[i]));
+      }
+    }
+  };
+  uint32_t mn = 0xFFFFFFFFu, mx = 0u, nans = 0u;
+  visit([&](uint32_t kk) {
+    mn = kk < mn ? kk : mn;
+    mx = kk > mx ? kk : mx;
+    nans += kk == 0xFFFFFFFFu ? 1u : 0u;
+  });
+  key[0] = key[1] = 0u;
+  if (block_sum_nan(nans, L) != 0) return true;
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) {
+    L.misc[tid >> 6] = mn;
+    L.sh[tid >> 6] = mx;
+  }
+  __syncthreads();
+  mn = L.misc[0];
+  mx = L.sh[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    mn = L.misc[w] < mn ? L.misc[w] : mn;
+    mx = L.sh[w] > mx ? L.sh[w] : mx;
+  }
+  __syncthreads();
+  uint32_t lo[2] = {mn, mn}, hi[2] = {mx, mx}, resid[2] = {rank[0], rank[1]};
+#pragma unroll 1
+  for (int pass = 0; pass < 4; ++pass) {
+    if (lo[0] == hi[0] && lo[1] == hi[1]) break;
+    const bool same = lo[0] == lo[1] && hi[0] == hi[1];
+    int shift[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int bits = 32 - __clz(hi[t] - lo[t]);
+      shift[t] = bits > 11 ? bits - 11 : 0;
+    }
+    for (int i = tid; i < 2 * 2048; i += kBlock) (&L.h[0][0])[i] = 0;
+    __syncthreads();
+    visit([&](uint32_t kk) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if ((t == 0 || !same) && lo[t] != hi[t] && kk >= lo[t] && kk <= hi[t])
+          atomicAdd(&L.h[t][(kk - lo[t]) >> shift[t]], 1u);
+      }
+    });
+    __syncthreads();
+    uint32_t cA[8], cB[8], bin[2], below[2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      cA[i] = L.h[0][tid * 8 + i];
+      cB[i] = L.h[1][tid * 8 + i];
+    }
+    block_find2<8>(cA, cB, same, resid, bin, below, L.sh);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (lo[t] == hi[t]) continue;
+      const uint64_t nlo = (uint64_t)lo[t] + ((uint64_t)bin[t] << shift[t]);
+      const uint64_t nhi = nlo + ((uint64_t)1 << shift[t]) - 1;
+      lo[t] = (uint32_t)nlo;
+      hi[t] = nhi < hi[t] ? (uint32_t)nhi : hi[t];
+      resid[t] -= below[t];
+    }
+    __syncthreads();
+  }
+  key[0] = lo[0];
+  key[1] = lo[1];
+  return false;
 }
 
 // A whole large group selected by one block (stream_keys).  Used when a launch

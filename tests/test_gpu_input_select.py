@@ -230,3 +230,62 @@ def test_input_select_long_strided_pair(kv):
     for (g2, r2), rec2 in zip(pairs[1:40], recs[1:40]):
         a2, _, _, _ = tv.mismatch_parts(g2, r2, TOL)
         assert same_value(float(rec2["p99_abs"]), float(tv.p99_meta(a2)))
+
+
+def _pivot_positions(m):
+    """The elements the capture pivot reads: 64 runs of 64, run j from (j * (m - 64)) // 63."""
+    return np.concatenate([np.arange(s, s + 64) for s in ((j * (m - 64)) // 63 for j in range(64))])
+
+
+def test_capture_thresholds_miss_and_edges(kv):
+    """Dense members (every element a sample) have their values at or above pivot
+    thresholds captured by the main pass.  Here the pivot runs misrepresent some
+    pairs on purpose: thresholds above the p99 (the pair falls back to the
+    input-select passes), thresholds far below it (most values captured, more
+    than 8192: streamed); plus NaN and Inf away from the pivot runs, in fp32 and
+    bf16, and captured values in a segment's partial last vector, between 270
+    ordinary members."""
+    rng = np.random.default_rng(404)
+    pairs = [_fp32_noise(int(rng.integers(8_300, 20_000)), rng) for _ in range(270)]
+    special = []
+    for n, dt in ((200_000, torch.float32), (120_001, torch.bfloat16)):
+        pos = _pivot_positions(n)
+        r = rng.standard_normal(n).astype(np.float32)
+        # the pivot sees only large differences: thresholds above the p99
+        g = r + (1e-4 * rng.standard_normal(n)).astype(np.float32)
+        g[pos] = r[pos] + np.float32(1.0) + rng.uniform(0, 1, pos.size).astype(np.float32)
+        special.append((torch.from_numpy(g).to(dt), torch.from_numpy(r).to(dt)))
+        # the pivot sees only tiny differences: nearly every value captured
+        g = r + (1e-1 * rng.standard_normal(n)).astype(np.float32)
+        g[pos] = r[pos]
+        special.append((torch.from_numpy(g).to(dt), torch.from_numpy(r).to(dt)))
+        # NaN and a few Inf away from the pivot runs
+        away = np.setdiff1d(np.arange(n), pos)
+        g = r + (1e-2 * rng.standard_normal(n)).astype(np.float32)
+        g[rng.choice(away, 3, replace=False)] = np.nan
+        special.append((torch.from_numpy(g).to(dt), torch.from_numpy(r).to(dt)))
+        g = r + (1e-2 * rng.standard_normal(n)).astype(np.float32)
+        rr = r.copy()
+        inf_at = rng.choice(away, 40, replace=False)
+        rr[inf_at[:20]] = np.inf            # abs_diff inf, rel_diff NaN
+        g[inf_at[20:]] = -np.inf            # abs_diff inf, rel_diff inf
+        special.append((torch.from_numpy(g).to(dt), torch.from_numpy(rr).to(dt)))
+    # the segment ends in a partial vector whose values are all captured, in the last of a
+    # lane's four vectors of an fp32 item (n % 1024 > 4 * 193): that vector is finished
+    # while the wave's lane 0, whose vectors are all whole, is idle
+    for n in (100 * 1024 + 907, 99 * 1024 + 1023):
+        r = rng.standard_normal(n).astype(np.float32)
+        g = r + (1e-3 * rng.standard_normal(n)).astype(np.float32)
+        g[-3:] = r[-3:] + np.float32(10.0)
+        special.append((torch.from_numpy(g), torch.from_numpy(r)))
+    pairs = special + pairs
+    _say("capture batch", len(pairs))
+    recs = kv.verdict_records([(g.to(DEV), r.to(DEV)) for g, r in pairs], tolerance_policy=TOL)
+    for i, ((g, r), rec) in enumerate(zip(pairs, recs)):
+        probs = record_vs_oracle(rec, g, r, TOL) if i < len(special) else []
+        abs_d, rel_d, _, _ = tv.mismatch_parts(g, r, TOL)
+        for k, vals in (("p99_abs", abs_d), ("p99_rel", rel_d)):
+            want = tv.p99_meta(vals)
+            if not same_value(float(rec[k]), float(want)):
+                probs.append(f"{k}: device {rec[k]!r} != oracle {want!r}")
+        assert not probs, (i, tuple(g.shape), g.dtype, probs)
