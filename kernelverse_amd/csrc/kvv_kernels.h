@@ -1239,6 +1239,9 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
     uint64_t rare = 0;
     const bool capseg = (d.flags & kFlagCaptureElems) != 0;
     uint32_t cm[2] = {0u, 0u};  // capture segment: the lean slots whose abs / rel value is captured
+    // (the thresholds in registers: loads of them inside the loop would wait on its LDS atomics)
+    const uint32_t ck0 = uniform(d.cap_key[0]), ck1 = uniform(d.cap_key[1]);
+    const float crlo = __uint_as_float(uniform(__float_as_uint(d.cap_rel_lo)));
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (__ballot(((slow >> (u * V)) & 0xFu) != 0) == 0) continue;
@@ -1275,9 +1278,9 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
           acc.s[3] = fma(d64, d64, acc.s[3]);
           if (capseg) {
             // (a lean abs_diff is finite and nonzero)
-            const bool ca = key >= d.cap_key[0];
+            const bool ca = key >= ck0;
             bool cr = false;
-            if (!(ad < d.cap_rel_lo * den)) cr = fkey(ad / den) >= d.cap_key[1];
+            if (!(ad < crlo * den)) cr = fkey(ad / den) >= ck1;
             cm[0] |= (ca ? 1u : 0u) << p;
             cm[1] |= (cr ? 1u : 0u) << p;
           }

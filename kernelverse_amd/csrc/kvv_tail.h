@@ -675,6 +675,9 @@ __device__ inline bool small_keys(const float* v, int64_t count, const uint32_t 
   return has_nan;
 }
 
+__device__ inline bool range_keys(const float* v, uint32_t count, const uint32_t rank[2], uint32_t key[2],
+                                  SelectLds& L);
+
 // A group of at most kSmall samples, selected by one block.
 __device__ inline void select_small(const TailArgs& a, const SegDesc& d, int arr, int64_t count, SelectLds& L) {
   uint64_t rank64[2];
@@ -682,7 +685,7 @@ __device__ inline void select_small(const TailArgs& a, const SegDesc& d, int arr
   q99_ranks(count, rank64, wgt);
   const uint32_t rank[2] = {(uint32_t)rank64[0], (uint32_t)rank64[1]};
   uint32_t key[2];
-  const bool has_nan = small_keys(a.arr[arr] + d.sample_off, count, rank, key, L);
+  const bool has_nan = range_keys(a.arr[arr] + d.sample_off, (uint32_t)count, rank, key, L);
   finalize_group(a, d, arr, count, key, wgt, has_nan, L);
 }
 
@@ -883,13 +886,26 @@ __device__ inline bool range_keys(const float* v, uint32_t count, const uint32_t
     }
     for (int i = tid; i < 2 * 2048; i += kBlock) (&L.h[0][0])[i] = 0;
     __syncthreads();
+    // a lane's consecutive values of one bin are added once (repeated values,
+    // e.g. the zeros of mostly identical data, would serialise on one word)
+    uint32_t rb[2] = {0u, 0u}, rn[2] = {0u, 0u};
     visit([&](uint32_t kk) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        if ((t == 0 || !same) && lo[t] != hi[t] && kk >= lo[t] && kk <= hi[t])
-          atomicAdd(&L.h[t][(kk - lo[t]) >> shift[t]], 1u);
+        if ((t == 0 || !same) && lo[t] != hi[t] && kk >= lo[t] && kk <= hi[t]) {
+          const uint32_t bin = (kk - lo[t]) >> shift[t];
+          if (bin != rb[t]) {
+            if (rn[t]) atomicAdd(&L.h[t][rb[t]], rn[t]);
+            rb[t] = bin;
+            rn[t] = 0;
+          }
+          ++rn[t];
+        }
       }
     });
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      if (rn[t]) atomicAdd(&L.h[t][rb[t]], rn[t]);
     __syncthreads();
     uint32_t cA[8], cB[8], bin[2], below[2];
 #pragma unroll

@@ -210,7 +210,7 @@ def test_input_select_strided_samples(kv):
 def test_input_select_long_strided_pair(kv):
     """One pair of 50 M elements (10^6 strided samples, stride ~50) among 260
     smaller ones: the chunks step far-apart sample indices, and the sampled
-    sums of 31 chunks are folded in order."""
+    sums of its 31 chunks are folded in order."""
     rng = np.random.default_rng(13)
     big = _fp32_noise(50_000_000, rng)
     big[0][:: 77_777] += 0.25
