@@ -180,13 +180,13 @@ def cpu_baseline(pairs, policy=None, budget_s: float = 12.0):
 _F2 = 524288.0 / 262156.5
 PMC_TRAFFIC = {
     "c1": {"fetch_kib": 524479.7, "write_kib": 9091.1, "fetch_factor": 524288.0 / 262157.4, "write_factor": 1.0},
-    "c1/tolerant": {"fetch_kib": 524521.8, "write_kib": 23600.2, "fetch_factor": _F2, "write_factor": 1.0},
+    "c1/tolerant": {"fetch_kib": 524570.4, "write_kib": 23515.3, "fetch_factor": _F2, "write_factor": 1.0},
     "c0": {"fetch_kib": 4277.7, "write_kib": 8732.1, "fetch_factor": _F2, "write_factor": 1.0},
     "c2": {"fetch_kib": 262465.8, "write_kib": 9061.3, "fetch_factor": _F2, "write_factor": 1.0},
     "c3fp8": {"fetch_kib": 131273.0, "write_kib": 9060.4, "fetch_factor": _F2, "write_factor": 1.0},
     "c3int8": {"fetch_kib": 131256.1, "write_kib": 9063.4, "fetch_factor": _F2, "write_factor": 1.0},
     # c4: the whole batch call (every kernel of one kvv_verdict_batch), profiles/verdict_c4_batch_traffic.md
-    "c4": {"fetch_kib": 5478772.4, "write_kib": 117720.7, "fetch_factor": 524288.0 / 262157.4, "write_factor": 1.0},
+    "c4": {"fetch_kib": 2060041.4, "write_kib": 146645.6, "fetch_factor": 524288.0 / 262157.4, "write_factor": 1.0},
 }
 
 
