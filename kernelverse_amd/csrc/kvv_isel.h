@@ -239,22 +239,37 @@ static_assert(kPivotSamples == 16 * kBlock && kPivotRun == 64 && kSmall < kIselC
               "pivot values: 16 per thread, one run per wave and step, fewer than a capture segment's");
 
 // Capture thresholds.  A NaN among the pivot values (the p99 is then NaN)
-// captures the NaNs only.  cap_rel_lo bounds where rel_diff = abs_diff / den
-// can reach cap_key[1] without the division: a pair with abs_diff <
-// fl(cap_rel_lo * den) has fl(abs_diff / den) below the threshold value v,
-// since cap_rel_lo <= v * (1 - 2^-20) and every product stays a normal float
-// (v >= 2^-80, den >= 1e-12; larger v are capped at 2^127, past which only the
-// division tells).
+// captures the NaNs only.  cap_rel_lo and cap_rel_hi bound where rel_diff =
+// fl(abs_diff / den), den = fl(|ref| + 1e-12), reaches cap_key[1] without the
+// division (the threshold value v, u = 2^-24 the rounding unit):
+// * below: abs_diff < fl(cap_rel_lo * den) gives fl(abs_diff / den) < v,
+//   since cap_rel_lo <= v * (1 - 2^-20) and every product stays a normal float
+//   (v >= 2^-80, den >= 1e-12; larger v are capped at 2^127, past which only
+//   the division tells).  fl(cap_rel_lo * |ref|) is never above that product.
+// * above: abs_diff >= H = fl(cap_rel_hi * |ref| + cap_rel_hic), with
+//   cap_rel_hi = fl(v * (1 + 2^-20)) and cap_rel_hic = fl(cap_rel_hi * 1e-12),
+//   gives H >= cap_rel_hi * (|ref| + 1e-12) * (1 - u)^2 >= cap_rel_hi * den *
+//   (1 - u)^3, so abs_diff / den > v * (1 + 2^-20) * (1 - u)^4 > v and the
+//   rounded quotient is at least v.  Taken for 2^-80 <= v < 2^100 (products
+//   normal or, where they overflow, H infinite and the test false); else
+//   cap_rel_hi is +inf and only the division tells.
 __device__ inline void set_thresholds(SegDesc& d, uint32_t ka, bool nan_a, uint32_t kr, bool nan_r) {
   const uint32_t k0 = nan_a ? 0xFFFFFFFFu : ka, k1 = nan_r ? 0xFFFFFFFFu : kr;
   d.cap_key[0] = k0 > kZeroKey ? k0 : kZeroKey + 1u;
   d.cap_key[1] = k1 > kZeroKey ? k1 : kZeroKey + 1u;
   const float v = fkey_value(d.cap_key[1]);
-  float lo;
-  if (d.cap_key[1] == 0xFFFFFFFFu) lo = __builtin_inff();
-  else if (v < 0x1p-80f) lo = 0.0f;
-  else lo = fminf(v * (1.0f - 0x1p-20f), 0x1p127f);
+  float lo, hi = __builtin_inff();
+  if (d.cap_key[1] == 0xFFFFFFFFu) {
+    lo = __builtin_inff();
+  } else if (v < 0x1p-80f) {
+    lo = 0.0f;
+  } else {
+    lo = fminf(v * (1.0f - 0x1p-20f), 0x1p127f);
+    if (v < 0x1p100f) hi = v * (1.0f + 0x1p-20f);
+  }
   d.cap_rel_lo = lo;
+  d.cap_rel_hi = hi;
+  d.cap_rel_hic = hi * 1e-12f;
 }
 
 // Counts of bins [tid * 8, tid * 8 + 8) of both block histograms.

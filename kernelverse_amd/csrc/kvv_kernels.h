@@ -155,6 +155,8 @@ struct SegDesc {
   uint32_t* cap_state;    // the segment's input-select state words
   uint32_t cap_key[2];    // capture the nonzero values whose key is at least these (abs, rel)
   float cap_rel_lo;       // rel_diff can reach cap_key[1] only where abs_diff >= cap_rel_lo * den
+  float cap_rel_hi;       // rel_diff reaches cap_key[1] where abs_diff >= fma(cap_rel_hi, |ref|, cap_rel_hic)
+  float cap_rel_hic;
   int32_t isel_group;     // input-select: the segment's dtype group (its chunk work list and count)
   int32_t isel_gchunk0;   // input-select: the start of that group's region of the chunk work list
   int32_t isel_pad;
@@ -1193,34 +1195,67 @@ __device__ __forceinline__ bool phase_b_dense(const SegDesc& d, uint32_t R0, uin
 
 // Phase B in place for an fp32 item of mostly slow pairs under the isclose test
 // without near-zero diagnostics (e.g. every pair perturbed by noise): each lane
-// walks its own slots once and finishes every slow pair whose only outputs are
-// common ones, which are the abs key (argmax), the ULP bucket and the fp64
-// sums.  Such a pair is within tolerance, has a finite abs_diff, has values of
-// one sign, and has a rel_diff below the wave's rel-argmax bound.  For it,
-// slow_elem would change nothing else.  Its ULP bucket goes to copy lane % kRep
-// of the wave's replicated counters `rep` (no ballots, and at most four
-// increments of one element step meet at an address).
+// walks its own slots once and finishes every slow pair whose values have one
+// sign, other bits (a nonzero difference) and a finite abs_diff.  Such a "lean"
+// pair has no finite-pattern or NaN outputs; its ULP distance is the distance
+// of its codes.  Its ULP bucket goes to copy lane % kRep of the wave's
+// replicated counters `rep` (no ballots, and at most four increments of one
+// element step meet at an address); its abs key, fp64 sums and captures are
+// taken in registers.
 //
-// The other slow pairs are mismatches, non-finite values, opposite signs and
-// rel-argmax candidates.  They are returned as a mask for the queue and
-// slow_elem.  The lean pairs of a lane come in ascending index order and
-// precede the item's queued pairs, so a strict key comparison keeps the lowest
-// index of a tie.  The bound only rises, so a pair below it now stays below it.
-// Taken when every lane has at least 3/4 of its slots slow.  Otherwise `slow`
-// comes back unchanged.
+// Two conservative single-compare tests keep the division off the common path:
+// * tolerance: abs_diff <= fma(|gen|, rtol_lo, atol_lo) with both tolerances
+//   lowered by 2^-21 (lean_tol), which never exceeds the exact allowed bound
+//   fl(atol + fl(rtol * |gen|)): such a pair is close;
+// * rel bound: abs_diff < fl(thr * |ref|), never above fl(thr * den): such a
+//   pair cannot be the rel argmax.
+// A pair that fails either takes slow_elem's exact tests in place (the
+// mismatch counters, the rel argmax).  The capture of rel_diff is settled by
+// fl(cap_rel_lo * |ref|) below and fma(cap_rel_hi, |ref|, cap_rel_hic) above
+// (set_thresholds); the division is left to the thin band between.
+//
+// The other slow pairs (opposite signs, +0 against -0, non-finite values) are
+// returned as a mask for the queue and slow_elem.  The lean pairs of a lane
+// come in ascending index order and precede the item's queued pairs, so a
+// strict key comparison keeps the lowest index of a tie.  The bound only
+// rises, so a pair below it now stays below it.  Taken for a fully loaded item
+// (a bit-identical pair, which phase A finished, then has a zero difference
+// and is never lean) when every lane has at least 3/4 of its slots slow.
+// Otherwise `slow` comes back unchanged.
+struct LeanTol {
+  float rtol, atol;
+};
+
+// Tolerances for the lean form of the isclose test: fma(|g|, rtol_lo, atol_lo)
+// with x_lo = fl(x * (1 - 2^-21)) <= x * (1 - 2^-22) is at most (X + A) * (1 -
+// 2^-22) before its one rounding, where X = rtol * |g| and A = atol; the exact
+// bound fl(A + fl(X)) is at least (X + A) * (1 - 2^-24) - 2^-150.  For A >=
+// 2^-127 the first is the smaller, and for A = 0 rounding's monotonicity
+// orders them.  Tolerances outside [2^-100, 2^100] (zero aside) or a zero
+// tolerance (plain equality) give bounds below zero: no lean pair.
+__device__ __forceinline__ LeanTol lean_tol(const SegDesc& d) {
+  auto ok = [](float t) { return t == 0.0f || (t >= 0x1p-100f && t <= 0x1p100f); };
+  if (d.zero_tol || !ok(d.rtol) || !ok(d.atol)) return LeanTol{-1.0f, -1.0f};
+  return LeanTol{d.rtol * (1.0f - 0x1p-21f), d.atol * (1.0f - 0x1p-21f)};
+}
+
+// Absolute difference of two codes (one instruction).
+__device__ __forceinline__ uint32_t abs_diff_u32(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_sad_u32 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 template <int DT, int MODE>
-__device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, uint64_t slow, StageP stage,
-                                                 Acc& acc, KVV_LDS uint32_t* rep, uint32_t* wc) {
+__device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, uint64_t slow, uint32_t full,
+                                                 StageP stage, Acc& acc, KVV_LDS uint32_t* rep, uint32_t* wc) {
   constexpr int V = VecIO<DT>::V;
   if constexpr (DT != KVV_F32 || MODE != KVV_MODE_ISCLOSE) {
     return slow;
   } else {
-    if (__ballot((uint32_t)__popcll(slow) * 4u < 3u * (uint32_t)VecIO<DT>::NE)) return slow;
+    if (__ballot((uint32_t)__popcll(slow) * 4u < 3u * (uint32_t)VecIO<DT>::NE || full != (1u << kUnroll) - 1))
+      return slow;
     const int lane = lane_id();
-    // close == (g == r) under a zero tolerance: an allowed bound of -inf
-    const bool zt = d.zero_tol != 0;
-    const float atol = zt ? -__builtin_inff() : d.atol;
-    const float rtol = zt ? 0.0f : d.rtol;
     float thr = acc.rel_thr;
     if (__ballot(!(thr > -__builtin_inff()))) {
       // no bound yet (the run's first pairs): the largest finite rel_diff of the
@@ -1235,13 +1270,22 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
         thr = t > thr ? t : thr;
       }
     }
-    KVV_LDS uint32_t* const mine = rep + (lane & (kRep - 1));
-    uint64_t rare = 0;
+    const LeanTol lt = lean_tol(d);
+    const bool zt = d.zero_tol != 0;
+    // the ULP counters by leading zeros of the distance: row j - 17 for bucket
+    // 32 - j, bucket 15 (distances of 2^14 and more) in row 0
+    KVV_LDS uint32_t* const mine = rep + (lane & (kRep - 1)) - 17 * kRep;
+    // the lane's largest lean abs_diff (its bits; abs_diff >= 0) and its slot
+    uint32_t best = acc.gabs_k > kZeroKey ? acc.gabs_k & 0x7FFFFFFFu : 0u;
+    int bslot = -1;
+    uint32_t leanm = 0;
     const bool capseg = (d.flags & kFlagCaptureElems) != 0;
     uint32_t cm[2] = {0u, 0u};  // capture segment: the lean slots whose abs / rel value is captured
     // (the thresholds in registers: loads of them inside the loop would wait on its LDS atomics)
-    const uint32_t ck0 = uniform(d.cap_key[0]), ck1 = uniform(d.cap_key[1]);
+    const uint32_t ca0 = uniform(d.cap_key[0]) & 0x7FFFFFFFu, ck1 = uniform(d.cap_key[1]);
     const float crlo = __uint_as_float(uniform(__float_as_uint(d.cap_rel_lo)));
+    const float crhi = __uint_as_float(uniform(__float_as_uint(d.cap_rel_hi)));
+    const float crhc = __uint_as_float(uniform(__float_as_uint(d.cap_rel_hic)));
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (__ballot(((slow >> (u * V)) & 0xFu) != 0) == 0) continue;
@@ -1252,24 +1296,40 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int p = u * 4 + e;
-        const bool act = ((slow >> p) & 1u) != 0;
         const float g = __uint_as_float(gw[e]), r = __uint_as_float(rw[e]);
         const float ad = fabsf(g - r);
-        const float allowed = atol + fabsf(rtol * g);
-        const bool close = g == r || ad <= allowed;
-        const float den = fabsf(r) + 1e-12f;
-        const bool lean = close && __builtin_isfinite(ad) && (int32_t)(gw[e] ^ rw[e]) >= 0 && ad < thr * den;
-        rare |= (uint64_t)(act && !lean) << p;
-        if (act && lean) {
-          const uint32_t key = __float_as_uint(ad) | 0x80000000u;
-          if (key > acc.gabs_k) {
-            acc.gabs_k = key;
-            acc.gabs_i = R0 + (uint32_t)((u * 64 + lane) * V + e);
+        const uint32_t ab = __float_as_uint(ad);
+        // (one sign and other bits: a nonzero difference)
+        const bool lean = (int32_t)(gw[e] ^ rw[e]) > 0 && ad < __builtin_inff();
+        leanm |= (lean ? 1u : 0u) << p;
+        if (lean) {
+          const bool tol = ad <= fmaf(fabsf(g), lt.rtol, lt.atol);
+          const bool below = ad < thr * fabsf(r);
+          if (!(tol && below)) {
+            // a mismatch or a rel-argmax candidate (slow_elem's tests, exactly)
+            const float rel = ad / (fabsf(r) + 1e-12f);
+            const uint32_t rk = fkey(rel);
+            const uint32_t idx = R0 + (uint32_t)((u * 64 + lane) * V + e);
+            if (!tol && (zt || !(ad <= d.atol + fabsf(d.rtol * g)))) {
+              ++acc.nmm;
+              acc.first_mm = idx < acc.first_mm ? idx : acc.first_mm;
+              acc.mm_abs = fkey(ad) > acc.mm_abs ? fkey(ad) : acc.mm_abs;
+              acc.mm_rel = rk > acc.mm_rel ? rk : acc.mm_rel;
+            }
+            if (!below && better32(rk, idx, acc.grel_k, acc.grel_i)) {
+              acc.grel_k = rk;
+              acc.grel_i = idx;
+              const float t = rel_threshold(rel);
+              thr = t > thr ? t : thr;
+            }
           }
-          // one sign: the ULP distance is the distance of the codes
-          const uint32_t a = gw[e] - rw[e], b = rw[e] - gw[e];
-          const int bl = 32 - __clz(a < b ? a : b);
-          atomicAdd((uint32_t*)(mine + (bl < kBuckets - 1 ? bl : kBuckets - 1) * kRep), 1u);
+          if (ab > best) {
+            best = ab;
+            bslot = p;
+          }
+          // one sign: the ULP distance is the distance of the codes (nonzero here)
+          const uint32_t lz = (uint32_t)__builtin_clz(abs_diff_u32(gw[e], rw[e]));
+          atomicAdd((uint32_t*)(mine + (lz > 17u ? lz : 17u) * kRep), 1u);
           const double g64 = (double)g, r64 = (double)r;
           const double d64 = g64 - r64;
           acc.s[0] = fma(g64, g64, acc.s[0]);
@@ -1277,21 +1337,25 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
           acc.s[2] = fma(g64, r64, acc.s[2]);
           acc.s[3] = fma(d64, d64, acc.s[3]);
           if (capseg) {
-            // (a lean abs_diff is finite and nonzero)
-            const bool ca = key >= ck0;
-            bool cr = false;
-            if (!(ad < crlo * den)) cr = fkey(ad / den) >= ck1;
-            cm[0] |= (ca ? 1u : 0u) << p;
-            cm[1] |= (cr ? 1u : 0u) << p;
+            const bool hi = ad >= fmaf(crhi, fabsf(r), crhc);
+            cm[0] |= (ab >= ca0 ? 1u : 0u) << p;
+            cm[1] |= (hi ? 1u : 0u) << p;
+            if (!hi && !(ad < crlo * fabsf(r)) && fkey(ad / (fabsf(r) + 1e-12f)) >= ck1) cm[1] |= 1u << p;
           }
         }
       }
     }
+    acc.rel_thr = thr;
+    if (bslot >= 0) {
+      acc.gabs_k = best | kZeroKey;
+      acc.gabs_i = R0 + (uint32_t)((((bslot >> 2) * 64 + lane) * V) + (bslot & 3));
+    }
+    const uint64_t rare = slow & ~(uint64_t)leanm;
     if (capseg) {
       // the captured values of the lean pairs, lane by lane in slot order, from
       // the stage, after the run's captures so far; the lean pairs not captured
       // are nonzero values below the threshold
-      const uint32_t nl = (uint32_t)__popcll(slow & ~rare);
+      const uint32_t nl = (uint32_t)__popc(leanm);
       const uint32_t c0 = (uint32_t)__popc(cm[0]), c1 = (uint32_t)__popc(cm[1]);
       const uint32_t pk = c0 | (c1 << 16);  // (a wave adds at most 1024 to each half)
       const uint32_t incl = wave_incl_scan(pk);
@@ -1300,7 +1364,8 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
       if (tot | nb) {
         const uint32_t base = wc[WC_CBASE], f0 = wc[WC_CFILL], f1 = wc[WC_CFILL + 1];
         const uint32_t ex = incl - pk;
-        uint32_t at[2] = {base + f0 + (ex & 0xFFFFu), base + f1 + (ex >> 16)};
+        float* pa = d.cap_buf[0] + base + f0 + (ex & 0xFFFFu);
+        float* pr = d.cap_buf[1] + base + f1 + (ex >> 16);
 #pragma unroll
         for (int x = 0; x < 2; ++x) {
           for (uint32_t mk = cm[x]; mk; mk &= mk - 1) {
@@ -1308,7 +1373,7 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
             const float g = stage_elem<float>(stage, (2 * u) * 64 + lane, e);
             const float r = stage_elem<float>(stage, (2 * u + 1) * 64 + lane, e);
             const float ad = fabsf(g - r);
-            d.cap_buf[x][at[x]++] = x == 0 ? ad : ad / (fabsf(r) + 1e-12f);
+            if (x == 0) *pa++ = ad; else *pr++ = ad / (fabsf(r) + 1e-12f);
           }
         }
         if (lane == 0) {
@@ -1330,14 +1395,15 @@ __device__ __forceinline__ void fold_rep(KVV_LDS uint32_t* rep, uint32_t* wc) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane < kBuckets) {
+  // row i counts bucket 15 - i (phase_b_lean)
+  if (lane < kBuckets - 1) {
     uint32_t t = 0;
 #pragma unroll
     for (int c = 0; c < kRep; ++c) {
       t += rep[lane * kRep + c];
       rep[lane * kRep + c] = 0;
     }
-    wc[LC_HIST0 + lane] += t;
+    wc[LC_HIST0 + (kBuckets - 1) - lane] += t;
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -2210,7 +2276,7 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
         // what is left for the queue after an in-place pass over an item of mostly slow pairs
         uint64_t left = slow;
         if (__ballot(slow != 0)) {
-          if (kLean && !(d.flags & kFlagNearAny)) left = phase_b_lean<DT, MODE>(d, R0, slow, stage, acc, rep, wc);
+          if (kLean && !(d.flags & kFlagNearAny)) left = phase_b_lean<DT, MODE>(d, R0, slow, full_now, stage, acc, rep, wc);
           else if (phase_b_dense<DT, MODE>(d, R0, slow, stage, acc, wc)) left = 0;
         }
         if (__ballot(left != 0)) {

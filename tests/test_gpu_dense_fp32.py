@@ -1,11 +1,13 @@
 """fp32 pairs that differ at (nearly) every element, against the CPU oracle (needs an MI355X).
 
 Such items take the scan's in-place dense path: each lane finishes its pairs
-that are within tolerance, finite, of one sign and below the rel-argmax bound
-itself, and queues the rest (mismatches, NaN/Inf, sign changes, rel-argmax
-candidates) for the full per-element treatment.  Every case here mixes the two
-kinds inside items, in single calls and in batches, and checks every exact
-field (ULP histogram, argmax indices, counts), the sums and the metas.
+of one sign with a finite, nonzero difference itself (mismatches and rel-argmax
+candidates through the exact tests, the others through one-compare bounds),
+and queues the rest (NaN/Inf, sign changes, +0 against -0) for the full
+per-element treatment.  Every case here mixes the kinds inside items, in
+single calls and in batches, and checks every exact field (ULP histogram,
+argmax indices, counts), the sums and the metas; the tolerance-boundary cases
+put abs_diff within a few ULPs of the allowed bound.
 """
 
 import sys
@@ -98,6 +100,31 @@ def _cases():
     g[700_001] += np.float32(0.5)
     g[300_003] += np.float32(0.5)
     out.append(("abs_ties", g, r, {"FP32": {"atol": 1.0, "rtol": 0.0}}))
+    # abs_diff right at the allowed bound fl(atol + fl(rtol * |g|)) and a few ULPs either side: g on a
+    # grid of 2^-13 in [1, 2) (either sign) makes that bound exact, r = g - bound, then r moves by k ULPs.
+    # Pairs between the lowered in-place bound and the exact one take the exact test.
+    for nm, atol, rtol in (("tol_boundary", 2.0 ** -10, 2.0 ** -10), ("tol_boundary_rtol_only", 0.0, 2.0 ** -7)):
+        mag = (np.float32(1.0) + rng.integers(0, 1 << 13, N).astype(np.float32) * np.float32(2.0 ** -13))
+        bound = (np.float32(atol) + mag * np.float32(rtol)).astype(np.float32)
+        rm = (mag - bound).astype(np.float32)
+        k = rng.integers(-3, 4, N).astype(np.float32)
+        rm = (rm + k * np.float32(2.0 ** -23)).astype(np.float32)
+        sign = np.where(rng.random(N) < 0.5, np.float32(1), np.float32(-1))
+        g, r = (sign * mag).astype(np.float32), (sign * rm).astype(np.float32)
+        allowed = (np.float32(atol) + np.abs(np.float32(rtol) * g)).astype(np.float32)
+        ad = np.abs(g - r)
+        assert (ad == allowed).sum() > 100_000 and (ad > allowed).sum() > 100_000
+        out.append((nm, g, r, {"FP32": {"atol": atol, "rtol": rtol}}))
+    # an atol below the in-place test's range (every pair takes the exact test)
+    g, r = _noise(rng, N)
+    out.append(("tiny_atol", g, r, {"FP32": {"atol": 1e-35, "rtol": 1e-5}}))
+    # rel_diff ties: the largest rel_diff first appears halfway and then every 1000 elements; the lowest
+    # index wins (lanes, waves and items apart)
+    i = np.arange(N)
+    r = (np.float32(2.5) + (i % 1000).astype(np.float32) * np.float32(0.5)).astype(np.float32)
+    r[(i >= N // 2) & (i % 1000 == 0)] = np.float32(2.0)
+    g = (r + np.float32(0.5)).astype(np.float32)
+    out.append(("rel_ties", g, r, {"FP32": {"atol": 1.0, "rtol": 0.0}}))
     return [(nm, torch.from_numpy(np.ascontiguousarray(a)), torch.from_numpy(np.ascontiguousarray(b)), tol)
             for nm, a, b, tol in out]
 
