@@ -298,12 +298,14 @@ struct WsLayout {
   size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample,
       near_cm, ent, near_wave, ent_fill, wave_range, near_psum, table, chunk_seg, isel_state, isel_seg, isel_chunk,
       isel_sums, fb_segs, fb_counts, cap_runs, cap_chunks, subtab,
-      submm, total;
+      submm, starts, total;
 };
 
 // Work-list counts: the input-select passes' chunk lists (one per scan group),
 // their segment list, then the capture pass's chunk lists (one per scan group).
 constexpr int kMaxGroups = 15 * 2 * 3;
+// wave ranges kept per batch group (a grid of at most 4096 blocks, and one end)
+constexpr int64_t kGroupStarts = 4096 * kWaves + 1;
 
 // Near-zero entries of a single fp16/bf16 pair (kFlagNearEntries), 8 bytes each,
 // split evenly over the main pass's waves.  A wave's share is an eighth of its
@@ -336,7 +338,7 @@ int64_t run_slot_bound(int64_t item_count) {
 
 WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int64_t nslots, int64_t chunks,
                           int64_t items, const NearMode& near, bool batch, int64_t nisel = 0, int64_t isel_chunks = 0,
-                          int rounds = 1) {
+                          int rounds = 1, int64_t ngroups = 0) {
   WsLayout L{};
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -377,6 +379,7 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
   }
   if (batch) {
     L.table = take((size_t)nseg * sizeof(SegDesc));
+    L.starts = take((size_t)ngroups * kGroupStarts * 8);  // the main-pass launches' wave ranges
     L.chunk_seg = take((size_t)chunks * 8);
     L.isel_seg = take((size_t)nisel * 4);
     L.isel_chunk = take((size_t)isel_chunks * 8);  // the input-select passes' chunk work lists
@@ -569,19 +572,39 @@ int plan_single(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, S
 // kernel ends with the slowest).  Shares in proportion to the rates, refined
 // once from the per-round end times they gave, let the rounds finish together.
 constexpr double kRoundRate3[3] = {1.18, 1.0, 0.79};
+// The same for batch launches, whose items are mostly bound by instruction
+// issue (e.g. fp32 pairs that differ everywhere): the scan's oldest waves are
+// issued first.  Measured with equal shares on the C4 batch (per-wave clocks):
+// the rounds' waves ended at 575 / 641 / 764 us (fp32) and 179 / 196 / 219 us
+// (bf16) on average; the fp32 rates refined once from the shares below (645 /
+// 668 / 718 us at 1.10 / 1.0 / 0.86).
+constexpr double kBatchRoundRate3[3] = {1.10, 1.0, 0.86};
+constexpr double kBatchRoundRateF32[3] = {1.14, 1.0, 0.80};
 
-// Splits a single-segment grid's items over its dispatch rounds (a.rounds = 1:
-// one share for every wave).
-void plan_rounds(ScanArgs& a, ScanFn scan, int64_t grid) {
+// Relative cost of a batch item by what its segment asks of the main pass, in
+// items of a capture segment (least squares over per-wave clocks of the C4
+// batch: per item and per segment, fp32 / bf16): a strided-sample segment's
+// items (no capture: 0.74 / 0.68), a small segment's (its samples written:
+// 1.05 / 1.55), and each segment's start and end (its first load and run
+// record, the partial last vector: 2.3 / 2.6).
+struct ItemCost {
+  double strided, small, segment;
+};
+constexpr ItemCost kItemCostF32{0.74, 1.05, 2.3};
+constexpr ItemCost kItemCost16{0.68, 1.55, 2.6};
+
+// Splits a grid's a.items items over its dispatch rounds at the given rates
+// (a.rounds = 1: one share for every wave).
+void plan_rounds(ScanArgs& a, ScanFn scan, int64_t grid, const double* rate = kRoundRate3) {
   a.rounds = 1;
   const int64_t cus = device_cus();
   if (cus <= 0 || blocks_target(scan) != 3 * cus || grid <= 2 * cus) return;
   const int64_t nb[3] = {cus, cus, grid - 2 * cus};
   double wsum = 0.0;
-  for (int r = 0; r < 3; ++r) wsum += kRoundRate3[r] * (double)nb[r];
+  for (int r = 0; r < 3; ++r) wsum += rate[r] * (double)nb[r];
   int64_t first = 0;
   for (int r = 0; r < 3; ++r) {
-    const int64_t n = r < 2 ? (int64_t)((double)a.items * kRoundRate3[r] * (double)nb[r] / wsum) : a.items - first;
+    const int64_t n = r < 2 ? (int64_t)((double)a.items * rate[r] * (double)nb[r] / wsum) : a.items - first;
     const int64_t waves = nb[r] * kWaves;
     a.round_first[r] = first;
     a.round_ipw[r] = n > 0 ? (n + waves - 1) / waves : 0;
@@ -590,6 +613,74 @@ void plan_rounds(ScanArgs& a, ScanFn scan, int64_t grid) {
   a.round_first[3] = a.items;
   a.rounds = 3;
   a.round_blocks = (int32_t)cus;
+}
+
+// The wave ranges of a batch group's main-pass launch (grid blocks over items
+// [item_lo, item_lo + items) of segments [seg_lo, seg_hi)): each wave's share
+// of the group's cost (ItemCost) in proportion to its dispatch round's rate;
+// every range holds at least one item while items remain (the ranges after
+// the last item are empty).  Fills st[0 .. grid * kWaves] (relative to
+// item_lo) and each segment's run count and first range starting inside it.
+void plan_wave_ranges(std::vector<SegDesc>& table, int seg_lo, int seg_hi, int64_t item_lo, int64_t items,
+                      int64_t grid, ScanFn scan, const ItemCost& ic, const double* rates, int64_t* st) {
+  const int64_t nw = grid * kWaves;
+  auto cost_of = [&](const SegDesc& d) {
+    if (d.m <= kSmall) return ic.small;
+    if ((d.flags & kFlagInputSelect) && !(d.flags & kFlagCaptureElems)) return ic.strided;
+    return 1.0;
+  };
+  double total = 0.0;
+  for (int s = seg_lo; s < seg_hi; ++s)
+    if (table[s].item_count > 0) total += ic.segment + cost_of(table[s]) * (double)table[s].item_count;
+  // wave weights: dispatch rounds of one block per CU (equal weights when the
+  // grid does not fill three rounds)
+  const int64_t cus = device_cus();
+  const bool rounds = cus > 0 && blocks_target(scan) == 3 * cus && grid > 2 * cus;
+  auto weight = [&](int64_t k) {
+    if (!rounds) return 1.0;
+    const int64_t r = k / (cus * kWaves);
+    return rates[r < 2 ? r : 2];
+  };
+  double wsum = 0.0;
+  for (int64_t k = 0; k < nw; ++k) wsum += weight(k);
+  st[0] = 0;
+  int s = seg_lo;
+  int64_t seg_first = 0;  // the first item of segment s (relative)
+  double before = 0.0;    // the cost of the segments before s
+  double wcum = 0.0;
+  for (int64_t k = 1; k < nw; ++k) {
+    wcum += weight(k - 1);
+    const double t = total * wcum / wsum;
+    while (s < seg_hi) {
+      const SegDesc& d = table[s];
+      const double whole = d.item_count > 0 ? ic.segment + cost_of(d) * (double)d.item_count : 0.0;
+      if (before + whole > t) break;
+      before += whole;
+      seg_first += d.item_count;
+      ++s;
+    }
+    int64_t i = items;
+    if (s < seg_hi) {
+      const SegDesc& d = table[s];
+      const double rem = t - before - ic.segment;
+      int64_t j = rem <= 0.0 ? 0 : (int64_t)std::ceil(rem / cost_of(d));
+      if (j > d.item_count) j = d.item_count;
+      i = seg_first + j;
+    }
+    if (i <= st[k - 1]) i = st[k - 1] + 1;
+    if (i > items) i = items;
+    st[k] = i;
+  }
+  st[nw] = items;
+  // runs: the segment's first item and each range start strictly inside it
+  for (int q = seg_lo; q < seg_hi; ++q) {
+    SegDesc& d = table[q];
+    const int64_t b = d.item_begin - item_lo, e = b + d.item_count;
+    const int64_t k0 = std::upper_bound(st, st + nw + 1, b) - st;
+    const int64_t k1 = std::lower_bound(st, st + nw + 1, e) - st;
+    d.run_k0 = k0;
+    d.run_n = d.item_count > 0 ? 1 + (k1 > k0 ? k1 - k0 : 0) : 0;
+  }
 }
 
 // The main-pass launch of a single pair: kernel, items per wave, grid, the
@@ -737,8 +828,8 @@ int run_single(const SegDesc& d0, kvv_result* out, void* ws, size_t ws_bytes, hi
   // slots left clear by the previous call on this workspace need no clearing launch
   const bool slots_clear = take_kept(ws, L.slots, L.slot_bytes) && kept && main_hist;
   // one run record per block: its waves fold theirs (a single-segment launch)
-  d.run_base = 0;
-  d.run_ipb = g.ipw * kWaves;
+  d.run_n = g.grid;
+  d.run_k0 = 0;
   if (d.item_count > 0) {
     ScanArgs a = g.rounds;
     a.seg0 = d;
@@ -850,12 +941,14 @@ struct BatchPlan {
     int dt, mode, kind;
     int seg_lo, seg_hi;
     int64_t item_lo, items, ipb;
+    int64_t grid;  // the main-pass launch: blocks, and its wave ranges at starts[g * kGroupStarts]
     int64_t ick_lo, ick_n;  // this group's input-select chunks in isel_chunk
     int64_t isel_lo, isel_n;  // this group's input-select segments in isel_seg
   };
   std::vector<int32_t> isel_seg;      // input-select segments
   std::vector<int32_t> isel_chunk;    // (segment, chunk of the segment) pairs, grouped like the scans
   std::vector<Group> groups;
+  std::vector<int64_t> starts;  // kGroupStarts per group: wave k of its launch owns [starts[k], starts[k + 1])
   bool stream_groups = false;  // large groups selected one block each (tail level 4)
   int rounds = 1;              // select rounds per chunk block (every segment of the batch)
   int64_t items = 0, samples = 0, chunks = 0, nslots = 0, run_slots = 0;
@@ -927,7 +1020,7 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     bp.near = bp.near || (d.flags & KVV_FLAG_NEAR_ZERO);
     if (bp.groups.empty() || bp.groups.back().dt != d.dtype || bp.groups.back().mode != d.mode ||
         bp.groups.back().kind != kinds[i]) {
-      bp.groups.push_back({d.dtype, d.mode, kinds[i], s, s + 1, d.item_begin, d.item_count, 1, 0, 0,
+      bp.groups.push_back({d.dtype, d.mode, kinds[i], s, s + 1, d.item_begin, d.item_count, 1, 0, 0, 0,
                            (int64_t)bp.isel_seg.size(), 0});
     } else {
       bp.groups.back().seg_hi = s + 1;
@@ -941,15 +1034,22 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
     }
     bp.table.push_back(d);
   }
-  for (auto& gr : bp.groups) {
-    const int64_t target = blocks_target(scan_fn(gr.dt, gr.mode, gr.kind, true)) * kWaves;  // waves
-    gr.ipb = gr.items > 0 ? (gr.items + target - 1) / target : 1;  // items per wave
-    if ((uint64_t)gr.ipb * (uint64_t)item_elems_for(gr.dt) >= (1ull << 32))
+  bp.starts.assign(bp.groups.size() * (size_t)kGroupStarts, 0);
+  for (size_t g = 0; g < bp.groups.size(); ++g) {
+    auto& gr = bp.groups[g];
+    const ScanFn scan = scan_fn(gr.dt, gr.mode, gr.kind, true);
+    const int64_t target = blocks_target(scan) * kWaves;  // waves
+    gr.ipb = gr.items > 0 ? (gr.items + target - 1) / target : 1;  // items per wave, equal shares
+    gr.grid = gr.items > 0 ? (gr.items + gr.ipb * kWaves - 1) / (gr.ipb * kWaves) : 0;
+    if (gr.grid * kWaves + 1 > kGroupStarts) return fail(KVV_E_UNSUPPORTED, "batch group grid too large");
+    int64_t* st = bp.starts.data() + g * kGroupStarts;
+    plan_wave_ranges(bp.table, gr.seg_lo, gr.seg_hi, gr.item_lo, gr.items, gr.grid, scan,
+                     gr.dt == KVV_F32 ? kItemCostF32 : kItemCost16,
+                     gr.dt == KVV_F32 && gr.mode == KVV_MODE_ISCLOSE ? kBatchRoundRateF32 : kBatchRoundRate3, st);
+    int64_t max_ipw = 0;
+    for (int64_t k = 0; k < gr.grid * kWaves; ++k) max_ipw = st[k + 1] - st[k] > max_ipw ? st[k + 1] - st[k] : max_ipw;
+    if ((uint64_t)max_ipw * (uint64_t)item_elems_for(gr.dt) >= (1ull << 32))
       return fail(KVV_E_UNSUPPORTED, "batch group too large for 32-bit per-wave counts");
-    for (int s = gr.seg_lo; s < gr.seg_hi; ++s) {
-      bp.table[s].run_base = gr.item_lo;
-      bp.table[s].run_ipb = gr.ipb;
-    }
   }
   bp.items = item;
   bp.samples = sample;
@@ -995,7 +1095,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   NearMode near;
   near.exact = bp.near;
   const WsLayout L = workspace_layout(bp.run_slots, bp.samples, nseg, bp.nslots, bp.chunks, bp.items, near, true,
-                                      nisel, isel_chunks, bp.rounds);
+                                      nisel, isel_chunks, bp.rounds, (int64_t)bp.groups.size());
   int rc = check_ws(L, ws, ws_bytes, out);
   if (rc) return rc;
   SegDesc* dtable = at<SegDesc>(ws, L.table);
@@ -1009,6 +1109,9 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     d.cap_state = istate + (size_t)d.isel_slot * kIselStateWords;
   }
   KVV_HIP(hipMemcpyAsync(dtable, bp.table.data(), nseg * sizeof(SegDesc), hipMemcpyHostToDevice, st));
+  int64_t* dstarts = at<int64_t>(ws, L.starts);
+  if (!bp.starts.empty())
+    KVV_HIP(hipMemcpyAsync(dstarts, bp.starts.data(), bp.starts.size() * 8, hipMemcpyHostToDevice, st));
   if (bp.chunks) KVV_HIP(hipMemcpyAsync(dchunk, bp.chunk_seg.data(), bp.chunks * 8, hipMemcpyHostToDevice, st));
   int32_t* disel = at<int32_t>(ws, L.isel_seg);
   int2* dichunk = at<int2>(ws, L.isel_chunk);
@@ -1091,6 +1194,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     ScanFn scan = scan_fn(gr.dt, gr.mode, gr.kind, true);
     if (!scan) return fail(KVV_E_INVALID, "no kernel for dtype");
     ScanArgs a{};
+    a.starts = dstarts + (&gr - bp.groups.data()) * kGroupStarts;
     a.table = dtable + gr.seg_lo;
     a.nseg = gr.seg_hi - gr.seg_lo;
     a.item_lo = gr.item_lo;
@@ -1108,8 +1212,8 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
       a.zero_n4 = (int64_t)((L.isel_state - L.slots) / 16);
       zeroed = true;
     }
-    const int64_t grid = (gr.items + gr.ipb * kWaves - 1) / (gr.ipb * kWaves);
-    hipLaunchKernelGGL(scan, dim3((unsigned)grid), dim3(kBlock), 0, st, a);
+    // (the grid keeps the equal shares' size: three blocks per CU)
+    hipLaunchKernelGGL(scan, dim3((unsigned)gr.grid), dim3(kBlock), 0, st, a);
     KVV_HIP(hipGetLastError());
   }
   if (nisel) {
@@ -1214,7 +1318,8 @@ int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_te
   kvv::NearMode near;
   near.exact = bp.near;
   *bytes = kvv::workspace_layout(bp.run_slots, bp.samples, (int64_t)bp.table.size(), bp.nslots, bp.chunks, bp.items,
-                                 near, true, (int64_t)bp.isel_seg.size(), (int64_t)bp.isel_chunk.size() / 2, bp.rounds)
+                                 near, true, (int64_t)bp.isel_seg.size(), (int64_t)bp.isel_chunk.size() / 2, bp.rounds,
+                                 (int64_t)bp.groups.size())
                .total;
   return KVV_OK;
 }

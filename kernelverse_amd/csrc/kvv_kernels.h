@@ -125,8 +125,11 @@ struct SegDesc {
   int64_t sample_off;     // offset into the sample arrays
   int64_t chunk_begin;    // first select chunk of this segment (per array)
   int64_t chunk_count;    // select chunks per array (sized for m)
-  int64_t run_base;       // first item of the scan launch holding this segment
-  int64_t run_ipb;        // items per block of that launch
+  // The runs of this segment (a run: the part of one wave's item range, in a
+  // batch, or of one block's, for a single pair, inside the segment): how
+  // many, and the first wave range that starts inside it (batch).
+  int64_t run_n;
+  int64_t run_k0;
   uint64_t s_div, s_mod;  // (n-1) = s_div*(m-1) + s_mod: sample i sits at i*s_div + floor(i*s_mod/(m-1))
   uint32_t s_magic;       // floor(t/(m-1)) = mulhi(t, s_magic) >> s_shift for t < 64*(m-1)
   uint32_t s_shift;
@@ -187,6 +190,7 @@ struct ScanArgs {
   int64_t item_lo;         // items of this launch: [item_lo, item_lo + items)
   int64_t items;
   int64_t items_per_wave;  // each wave of the grid owns this many consecutive items
+  const int64_t* starts;   // batch: wave k owns items [starts[k], starts[k + 1]) (from item_lo)
   // single-segment launches filling the device in `rounds` dispatch rounds of
   // `round_blocks` blocks (rounds > 1): round r's waves own round_ipw[r] items
   // each, from round_first[r] on (round_first[rounds] == items)
@@ -1218,10 +1222,11 @@ __device__ __forceinline__ bool phase_b_dense(const SegDesc& d, uint32_t R0, uin
 // returned as a mask for the queue and slow_elem.  The lean pairs of a lane
 // come in ascending index order and precede the item's queued pairs, so a
 // strict key comparison keeps the lowest index of a tie.  The bound only
-// rises, so a pair below it now stays below it.  Taken for a fully loaded item
-// (a bit-identical pair, which phase A finished, then has a zero difference
-// and is never lean) when every lane has at least 3/4 of its slots slow.
-// Otherwise `slow` comes back unchanged.
+// rises, so a pair below it now stays below it.  Only the slots of fully loaded
+// vectors are walked (vec_tail takes a partial one's elements; a bit-identical
+// pair, which phase A finished, has a zero difference and is never lean).
+// Taken when every lane has at least 3/4 of those slots slow.  Otherwise
+// `slow` comes back unchanged.
 struct LeanTol {
   float rtol, atol;
 };
@@ -1253,8 +1258,8 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
   if constexpr (DT != KVV_F32 || MODE != KVV_MODE_ISCLOSE) {
     return slow;
   } else {
-    if (__ballot((uint32_t)__popcll(slow) * 4u < 3u * (uint32_t)VecIO<DT>::NE || full != (1u << kUnroll) - 1))
-      return slow;
+    // (a lane's slots: those of its fully loaded vectors; the others are vec_tail's)
+    if (__ballot((uint32_t)__popcll(slow) * 4u < 3u * (uint32_t)V * (uint32_t)__popc(full))) return slow;
     const int lane = lane_id();
     float thr = acc.rel_thr;
     if (__ballot(!(thr > -__builtin_inff()))) {
@@ -1299,8 +1304,8 @@ __device__ __forceinline__ uint64_t phase_b_lean(const SegDesc& d, uint32_t R0, 
         const float g = __uint_as_float(gw[e]), r = __uint_as_float(rw[e]);
         const float ad = fabsf(g - r);
         const uint32_t ab = __float_as_uint(ad);
-        // (one sign and other bits: a nonzero difference)
-        const bool lean = (int32_t)(gw[e] ^ rw[e]) > 0 && ad < __builtin_inff();
+        // (a loaded vector; one sign and other bits: a nonzero difference)
+        const bool lean = ((full >> u) & 1u) && (int32_t)(gw[e] ^ rw[e]) > 0 && ad < __builtin_inff();
         leanm |= (lean ? 1u : 0u) << p;
         if (lean) {
           const bool tol = ad <= fmaf(fabsf(g), lt.rtol, lt.atol);
@@ -1880,12 +1885,11 @@ __device__ __forceinline__ void scan_item_scalar(const SegDesc& d, int64_t L0, i
 }
 
 // ------------------------------------------------------------ run records
-// Run slot of the run that starts at item `it` of segment d: runs start at the
-// segment's first item and at every wave-range start inside it.
-__device__ __forceinline__ int64_t run_slot(const SegDesc& d, int64_t it) {
-  if (it == d.item_begin) return d.run_slot0;
-  const int64_t b_first = (d.item_begin - d.run_base) / d.run_ipb + 1;
-  return d.run_slot0 + (it - d.run_base) / d.run_ipb - b_first + 1;
+// Run slot of the run that starts at item `it` of segment d, in batch wave
+// range k: runs start at the segment's first item and at every wave range
+// that starts inside it (the launch's ranges are nonempty until its items end).
+__device__ __forceinline__ int64_t run_slot(const SegDesc& d, int64_t it, int64_t k) {
+  return it == d.item_begin ? d.run_slot0 : d.run_slot0 + 1 + (k - d.run_k0);
 }
 
 // Reduces the wave's accumulators and LDS counters into the run's columns (lane
@@ -2165,7 +2169,12 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
   // each wave owns a contiguous range of items; the waves of a block never wait
   // for each other
   int64_t i0, i1;
-  if (!BATCH && a.rounds > 1) {
+  if (BATCH) {
+    // the host's wave ranges (shares weighted by item cost and dispatch round)
+    const int64_t k = (int64_t)blockIdx.x * kWaves + w;
+    i0 = a.item_lo + a.starts[k];
+    i1 = a.item_lo + a.starts[k + 1];
+  } else if (a.rounds > 1) {
     // the grid is dispatched one block per CU at a time, and earlier rounds'
     // waves are served faster: each round's waves get a share of the items in
     // proportion to its rate
@@ -2316,14 +2325,14 @@ __global__ __launch_bounds__(kBlock, BATCH ? 3 : 1) void scan_kernel(ScanArgs a)
         const uint32_t b = wc[WC_BELOW + lane];
         if (b) atomicAdd(d.cap_state + IS_BELOW + lane, b);
       }
-      if (lane == 0) a.cap_runs[run_slot(d, run_start)] = make_uint4(wc[WC_CBASE], f0, f1, 0u);
+      if (lane == 0) a.cap_runs[run_slot(d, run_start, wave_id)] = make_uint4(wc[WC_CBASE], f0, f1, 0u);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       if (lane < 4) wc[WC_BELOW + lane] = 0;
     }
     if constexpr (BATCH) {
-      flush_run(acc, wc, ColSink{&a.runs, run_slot(d, run_start)}, base);
+      flush_run(acc, wc, ColSink{&a.runs, run_slot(d, run_start, wave_id)}, base);
       if (it >= i1) break;
       while (it >= ctable[s].item_begin + ctable[s].item_count) ++s;
       s = (int)uniform((uint32_t)s);

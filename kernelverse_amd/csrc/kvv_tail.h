@@ -115,14 +115,7 @@ __device__ __forceinline__ void role_split(int64_t nruns, int& f, int& p, int64_
   if (f >= F) j0 = j1 = 0;
 }
 
-__device__ __forceinline__ int64_t segment_runs(const SegDesc& d) {
-  if (d.item_count <= 0) return 0;
-  const int64_t rel0 = d.item_begin - d.run_base;                    // >= 0
-  const int64_t b_first = rel0 / d.run_ipb + 1;                       // first block start after item_begin
-  const int64_t rel_end = d.item_begin + d.item_count - d.run_base;  // exclusive
-  const int64_t b_end = (rel_end + d.run_ipb - 1) / d.run_ipb;       // block starts < rel_end
-  return 1 + (b_end > b_first ? b_end - b_first : 0);
-}
+__device__ __forceinline__ int64_t segment_runs(const SegDesc& d) { return d.item_count > 0 ? d.run_n : 0; }
 
 // Folds a u32 column part [j0, j1) (sum or max), 4 slots per load, 8 loads in flight.
 template <bool MAX>

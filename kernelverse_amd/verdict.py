@@ -240,7 +240,7 @@ class _Job:
     """One tensor pair on its way to the device, with what the meta builder needs."""
 
     __slots__ = ("gen", "ref", "path", "policy", "tolerance", "near_thresholds", "correctness_policy", "kpolicy",
-                 "record", "is_float", "active", "tol_text")
+                 "record", "is_float", "active", "tol_text", "pkey")
 
     def __init__(self, gen, ref, path, tolerance_policy, correctness_policy, max_samples, fp8_errors=None):
         self.gen, self.ref, self.path = gen, ref, path
@@ -248,9 +248,10 @@ class _Job:
         self.policy = _dtype_policy(ref, tolerance_policy)
         kp = _lib.KvvPolicy()
         kp.max_samples = int(max_samples)
+        mad = rtol = atol = 0
         if "max_abs_diff" in self.policy:
             kp.mode = _lib.MODE_MAX_ABS_DIFF
-            kp.max_abs_diff = int(self.policy["max_abs_diff"])
+            kp.max_abs_diff = mad = int(self.policy["max_abs_diff"])
             if not -2**31 <= kp.max_abs_diff < 2**31:
                 raise RuntimeError(f"value cannot be converted to type int32_t without overflow")
             self.tolerance = {"max_abs_diff": int(self.policy["max_abs_diff"])}
@@ -261,6 +262,7 @@ class _Job:
             kp.rtol, kp.atol = rtol, atol
             self.tolerance = {"rtol": rtol, "atol": atol}
         self.near_thresholds = None
+        nz = None
         if (ref.dtype in (torch.float16, torch.bfloat16) and is_tolerant_policy(correctness_policy)):
             th = thresholds_for_dtype(correctness_policy, _dtype_name(ref))
             if th.get("near_zero_abs") is not None and th.get("max_near_zero_bad_abs") is not None:
@@ -268,6 +270,9 @@ class _Job:
                 kp.flags |= _lib.FLAG_NEAR_ZERO
                 kp.near_zero_abs = float(th["near_zero_abs"])
                 kp.near_zero_bad_abs = float(th["max_near_zero_bad_abs"])
+                nz = (float(th["near_zero_abs"]), float(th["max_near_zero_bad_abs"]))
+        # the policy's part of the single-pair plan key (the values kpolicy was built from)
+        self.pkey = (kp.mode, rtol, atol, mad, nz, int(max_samples))
         if ref.dtype in _ISFINITE_ERRORS and (FP8_REFERENCE_ERRORS if fp8_errors is None else fp8_errors):
             raise NotImplementedError(_ISFINITE_ERRORS[ref.dtype])
         if _COMPLEX_REAL.get(ref.dtype, ref.dtype) not in _DTYPE_CODES:
@@ -368,7 +373,7 @@ class _Buffers:
     pointers set per call) and the workspace size, so a repeated call plans nothing
     on the host."""
 
-    __slots__ = ("lock", "ws", "out", "kept", "stream", "handle", "plans", "ws_bytes", "ws_ptr", "out_ptr")
+    __slots__ = ("lock", "ws", "out", "kept", "stream", "handle", "plans", "ws_bytes", "ws_ptr", "out_ptr", "out_rec")
 
     def __init__(self, stream):
         self.lock = threading.Lock()
@@ -379,6 +384,7 @@ class _Buffers:
         self.handle = stream.cuda_stream
         self.plans: "OrderedDict[tuple, tuple]" = OrderedDict()
         self.ws_bytes = self.ws_ptr = self.out_ptr = 0
+        self.out_rec = None  # the first record's bytes in `out`, as a ctypes view
 
 
 _MAX_STREAMS = 8
@@ -416,7 +422,7 @@ def _stream_buffers(dev: torch.device) -> _Buffers:
                 ob = _BUFFERS[old]
                 if ob.lock.acquire(blocking=False):
                     try:
-                        ob.ws = ob.out = None
+                        ob.ws = ob.out = ob.out_rec = None
                         ob.plans.clear()
                         del _BUFFERS[old]
                     finally:
@@ -429,7 +435,7 @@ def release_buffers() -> None:
     with _BUFFERS_LOCK:
         for b in _BUFFERS.values():
             with b.lock:
-                b.ws = b.out = None
+                b.ws = b.out = b.out_rec = None
                 b.plans.clear()
         _BUFFERS.clear()
         _LAST[0] = None
@@ -447,6 +453,7 @@ def _ensure(buf: _Buffers, dev: torch.device, ws_bytes: int, records: int) -> No
         # the records are written by the kernels straight into pinned host memory
         buf.out = torch.empty(max(rec_size * records, 64 * rec_size), dtype=torch.uint8, pin_memory=True)
         buf.out_ptr = buf.out.data_ptr()
+        buf.out_rec = (ctypes.c_char * rec_size).from_address(buf.out_ptr)
 
 
 def _device_of(job: _Job) -> torch.device:
@@ -487,8 +494,7 @@ def _launch_single(job: _Job) -> None:
         buf = _stream_buffers(_cuda_device(ri))
         kp = job.kpolicy
         gp, rp = g.data_ptr(), r.data_ptr()
-        key = (g.dtype, g.shape, g.stride(), r.stride(), (gp & 15) == 0, (rp & 15) == 0, kp.mode, kp.flags, kp.rtol,
-               kp.atol, kp.max_abs_diff, kp.near_zero_abs, kp.near_zero_bad_abs, kp.max_samples)
+        key = (job.pkey, g.dtype, g.shape, g.stride(), r.stride(), (gp & 15) == 0, (rp & 15) == 0)
         with buf.lock:
             plan = buf.plans.get(key)
             if plan is None:
@@ -518,7 +524,7 @@ def _launch_single(job: _Job) -> None:
             job.tol_text = f"{job.tolerance}"
             buf.stream.synchronize()
             buf.kept = True
-            job.record = _lib.KvvResult.from_buffer_copy(ctypes.string_at(buf.out_ptr, _REC_SIZE))
+            job.record = _lib.KvvResult.from_buffer_copy(buf.out_rec)
     finally:
         if ctx is not None:
             ctx.__exit__(None, None, None)
