@@ -1220,7 +1220,7 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     // p99 of the input-select segments: the capture segments' selection among
     // their captured values; then, for the other input-select segments and for
     // capture segments that missed, histograms, target bins, gather, final select
-    hipLaunchKernelGGL(isel_cap_final_kernel, dim3((unsigned)nisel), dim3(kBlock), 0, st, ia);
+    hipLaunchKernelGGL(isel_cap_final_kernel, dim3((unsigned)(2 * nisel)), dim3(kBlock), 0, st, ia);
     KVV_HIP(hipGetLastError());
     // (the passes loop over their work lists, which may be short: at most kIselWorkBlocks blocks)
     IselArgs wl = ia;

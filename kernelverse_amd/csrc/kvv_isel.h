@@ -462,11 +462,11 @@ __global__ __launch_bounds__(kBlock) void isel_gather_kernel(IselArgs a) {
     const float rel = adf / den;
     const uint32_t ka = fkey(adf) >> 21, kr = fkey(rel) >> 21;
     const bool cnt = act && adf != 0.0f;
-    stage_append(stage[w][0], fa, cnt && !nan0 && (ka == p00 || ka == p01), adf, &st[IS_FILL], ba);
-    stage_append(stage[w][1], fr, cnt && !nan1 && (kr == p10 || kr == p11), rel, &st[IS_FILL + 1], br);
+    stage_append(stage[w][0], fa, cnt && !nan0 && (ka == p00 || ka == p01), adf, &st[IS_GFILL], ba);
+    stage_append(stage[w][1], fr, cnt && !nan1 && (kr == p10 || kr == p11), rel, &st[IS_GFILL + 1], br);
   });
-  if (fa) stage_flush(stage[w][0], fa, &st[IS_FILL], ba);
-  if (fr) stage_flush(stage[w][1], fr, &st[IS_FILL + 1], br);
+  if (fa) stage_flush(stage[w][0], fa, &st[IS_GFILL], ba);
+  if (fr) stage_flush(stage[w][1], fr, &st[IS_GFILL + 1], br);
   }
 }
 
@@ -602,10 +602,14 @@ __device__ inline void cap_compact(const IselArgs& a, const SegDesc& d, int64_t 
   }
 }
 
+// Two blocks per segment: block 2s + x selects array x (both blocks place the
+// order statistics from the same counts, so they agree on a miss; the x = 0
+// block then hands the segment to the input-select passes).
 __global__ __launch_bounds__(kBlock) void isel_cap_final_kernel(IselArgs a) {
   __shared__ SelectLds L;
   const int tid = threadIdx.x;
-  const int seg = a.segs[blockIdx.x];
+  const int x = (int)(blockIdx.x & 1u);
+  const int seg = a.segs[blockIdx.x >> 1];
   const SegDesc& d = a.table[seg];
   if (!(d.flags & kFlagCapture)) return;
   uint32_t* st = a.state + (size_t)d.isel_slot * kIselStateWords;
@@ -630,9 +634,12 @@ __global__ __launch_bounds__(kBlock) void isel_cap_final_kernel(IselArgs a) {
   const CapRanks c0 = cap_ranks(d, cap[0], st[IS_BELOW], nan[0], rank64);
   const CapRanks c1 = cap_ranks(d, cap[1], st[IS_BELOW + 1], nan[1], rank64);
   if (st[IS_CNEG] != 0 || c0.miss || c1.miss) {
-    // the input-select passes take the segment over, from cleared histograms and counts
+    // the input-select passes take the segment over, from cleared histograms
+    // and counts (not the words either block reads above)
+    if (x != 0) return;
     __syncthreads();
-    for (int i = tid; i <= IS_BASE + 3; i += kBlock) st[i] = 0;
+    for (int i = tid; i <= IS_BASE + 3; i += kBlock)
+      if (i != IS_FILL && i != IS_FILL + 1) st[i] = 0;
     if (tid == 0) {
       a.fb_segs[atomicAdd(a.fb_scount, 1u)] = seg;
       const uint32_t nck = (uint32_t)((d.m + isel_chunk_len(d) - 1) / isel_chunk_len(d));
@@ -641,23 +648,17 @@ __global__ __launch_bounds__(kBlock) void isel_cap_final_kernel(IselArgs a) {
     }
     return;
   }
-#pragma unroll 1
-  for (int x = 0; x < 2; ++x) {
-    const bool need0 = x == 0 ? c0.need[0] : c1.need[0], need1 = x == 0 ? c0.need[1] : c1.need[1];
-    const uint32_t rk0 = x == 0 ? c0.rk[0] : c1.rk[0], rk1 = x == 0 ? c0.rk[1] : c1.rk[1];
-    const uint32_t cx = x == 0 ? cap[0] : cap[1];
-    uint32_t key[2] = {kZeroKey, kZeroKey};
-    if (need0 || need1) {
-      if (elems) cap_compact(a, d, nruns, x);
-      const uint32_t r2[2] = {need0 ? rk0 : rk1, need1 ? rk1 : rk0};
-      uint32_t k[2];
-      range_keys(a.buf[x] + d.sample_off, cx, r2, k, L);
-      if (need0) key[0] = k[0];
-      if (need1) key[1] = k[1];
-    }
-    if (tid == 0) store_p99(a.res[d.out_index], x, key, wgt, x == 0 ? nan[0] : nan[1]);
-    __syncthreads();
+  const CapRanks& c = x == 0 ? c0 : c1;
+  uint32_t key[2] = {kZeroKey, kZeroKey};
+  if (c.need[0] || c.need[1]) {
+    if (elems) cap_compact(a, d, nruns, x);
+    const uint32_t r2[2] = {c.need[0] ? c.rk[0] : c.rk[1], c.need[1] ? c.rk[1] : c.rk[0]};
+    uint32_t k[2];
+    range_keys(a.buf[x] + d.sample_off, cap[x], r2, k, L);
+    if (c.need[0]) key[0] = k[0];
+    if (c.need[1]) key[1] = k[1];
   }
+  if (tid == 0) store_p99(a.res[d.out_index], x, key, wgt, nan[x]);
 }
 
 __global__ __launch_bounds__(kBlock) void isel_find_kernel(IselArgs a) {
@@ -714,7 +715,7 @@ __global__ __launch_bounds__(kBlock) void isel_final_kernel(IselArgs a) {
     if (!nan) {
       const uint32_t p[2] = {st[IS_PFX + 2 * x], st[IS_PFX + 2 * x + 1]};
       const uint32_t b[2] = {st[IS_BASE + 2 * x], st[IS_BASE + 2 * x + 1]};
-      const uint32_t filled = st[IS_FILL + x];
+      const uint32_t filled = st[IS_GFILL + x];
       // The appended values are those of the target bins (one, or two adjacent
       // non-empty ones) without the zeros, which are the smallest values of the
       // zero bin.  Rank of each order statistic among the appended values:

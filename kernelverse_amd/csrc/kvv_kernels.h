@@ -56,7 +56,7 @@ constexpr uint32_t kFlagCaptureElems = 0x08000000u;
 enum IselWord {
   IS_HIST = 0,                 // [2][2048] top-digit histograms of abs_diff, rel_diff (zeros aside)
   IS_ZEROS = 2 * 2048,         // exact zeros (abs_diff == rel_diff == +0)
-  IS_FILL,                     // [2] values appended (input-select gather) or captured, per array
+  IS_FILL,                     // [2] values captured (the capture pass), per array
   IS_NAN = IS_FILL + 2,        // [2] the array holds a NaN
   IS_PFX = IS_NAN + 2,         // [2][2] bin of each order statistic
   IS_BASE = IS_PFX + 4,        // [2][2] values below each of those bins
@@ -66,9 +66,10 @@ enum IselWord {
                                // below the zeros, which the counts do not place: the segment falls back
   IS_FALLBACK,                 // kFlagCapture: an order statistic lies below the thresholds, so the
                                // input-select passes select this segment instead
+  IS_GFILL,                    // [2] values appended by the input-select gather, per array
   kIselStateWords = 4160       // 16,640 bytes: a multiple of 256
 };
-static_assert(IS_FALLBACK < kIselStateWords && (kIselStateWords * 4) % 256 == 0, "input-select state");
+static_assert(IS_GFILL + 1 < kIselStateWords && (kIselStateWords * 4) % 256 == 0, "input-select state");
 constexpr int64_t kIselChunk = 1 << 17;        // elements per input-select chunk (every element a sample)
 constexpr int64_t kIselChunkSampled = 1 << 15;  // samples per chunk at strided positions (element loads)
 // Per (large segment, array) slot: level-0 histogram (256), its kH0Copies
