@@ -496,10 +496,17 @@ __global__ __launch_bounds__(kBlock) void isel_capture_kernel(IselArgs a) {
     bool nan0 = false, nan1 = false, neg = false;
     double sg = 0.0, sr = 0.0, sx = 0.0;
     using E = Elem<DT>;
+    const float crlo = d->cap_rel_lo;
     unit_pass<DT, MODE>(*d, e0, e1, [&](float adf, float den, bool act, typename E::T gc, typename E::T rc) {
-      const float rel = adf / den;
       const bool nz = act && !(adf == 0.0f);
-      const bool ca = nz && fkey(adf) >= k0, cr = nz && fkey(rel) >= k1;
+      const bool ca = nz && fkey(adf) >= k0;
+      // rel_diff is divided out only where it can reach its threshold (set_thresholds)
+      float rel = 0.0f;
+      bool cr = false;
+      if (nz && !(adf < crlo * den)) {
+        rel = adf / den;
+        cr = fkey(rel) >= k1;
+      }
       b0 += nz && !ca ? 1u : 0u;
       b1 += nz && !cr ? 1u : 0u;
       nan0 = nan0 || (ca && adf != adf);
