@@ -424,7 +424,8 @@ struct NearLaunch {
 // level; then select level 1 and the final read-off of every array.
 int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchunk, int nseg, int64_t total_chunks,
                 int64_t nslots, const NearMode& nm, const WsLayout& L, void* ws, kvv_result* out, hipStream_t st,
-                const std::vector<NearLaunch>& nears, bool stream_groups = false, int rounds = 1) {
+                const std::vector<NearLaunch>& nears, bool stream_groups = false, int rounds = 1,
+                int64_t max_runs = -1) {
   const bool near = nm.any();
   TailArgs t{};
   if (seg0) t.seg0 = *seg0;
@@ -435,6 +436,9 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   t.res = out;
   t.runs = run_cols(L, ws);
   t.reduce_roles = nm.exact ? 6 : 5;
+  // a batch whose segments have at most 64 runs each: a wave folds each segment
+  const bool wave_fold = dtable != nullptr && !nm.any() && max_runs >= 0 && max_runs <= 64;
+  if (wave_fold) t.reduce_roles = 0;
   t.arr[0] = at<float>(ws, L.sample_abs);
   t.arr[1] = at<float>(ws, L.sample_rel);
   t.arr[2] = near ? at<float>(ws, L.near_sample) : nullptr;
@@ -497,7 +501,8 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   }
   // a single pair whose main pass did select level 0 of abs/rel starts at level 1 there
   const bool main_hist = seg0 && (seg0->flags & kFlagMainHist);
-  int rc = launch(nseg * t.reduce_roles, main_hist ? 3 : 0, 0, nm.entries ? 3 : 2);
+  int rc = launch(wave_fold ? (nseg + kWaves - 1) / kWaves : nseg * t.reduce_roles, main_hist ? 3 : 0, 0,
+                  nm.entries ? 3 : 2);
   if (rc) return rc;
   if (stream_groups) {
     rc = launch(0, 4, 0, 2);
@@ -1245,8 +1250,10 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
       KVV_HIP(hipGetLastError());
     }
   }
+  int64_t max_runs = 0;
+  for (const auto& d : bp.table) max_runs = d.run_n > max_runs ? d.run_n : max_runs;
   return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, near, L, ws, out, st, nears,
-                     bp.stream_groups, bp.rounds);
+                     bp.stream_groups, bp.rounds, max_runs);
 }
 
 }  // namespace

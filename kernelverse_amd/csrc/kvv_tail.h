@@ -34,7 +34,7 @@ struct TailArgs {
   const int64_t* chunk_seg;   // batch: owning segment of each select chunk
   int32_t nseg;
   int32_t reduce_blocks;      // leading blocks that fold run records (reduce_roles per segment), 0 for none
-  int32_t reduce_roles;       // 5, or 6 with the near-zero prefix
+  int32_t reduce_roles;       // 5, or 6 with the near-zero prefix; 0: one wave per segment (reduce_segment_wave)
   int32_t level;              // select level of the launch: 0 (with the fold and small groups), 1, 2 = final
   int32_t arr_lo;             // select blocks cover arrays [arr_lo, arr_lo + narr)
   int32_t narr;
@@ -355,6 +355,121 @@ __device__ inline void reduce_sums(const TailArgs& a, const SegDesc& d, int64_t 
     o.rel_l2 = rn == 0.0 ? (dn == 0.0 ? 0.0 : __builtin_inf()) : dn / rn;
     o.cosine = cosine_of(sum(2), sum(0), sum(1));
   }
+}
+
+// The fold of a batch segment of at most 64 runs by one wave (lane k reads run
+// k of every column): the outputs of the count, extrema and sum roles above,
+// from wave reductions (the f64 sums in a fixed DPP tree: reproducible).
+// Batches without near-zero diagnostics only.
+template <bool BATCH>
+__device__ inline void reduce_segment_wave(const TailArgs& a, int seg) {
+  const SegDesc& d = BATCH ? a.table[seg] : a.seg0;
+  const int64_t nruns = segment_runs(d);
+  const int lane = lane_id();
+  const bool in = lane < nruns;
+  const size_t at = (size_t)d.run_slot0 + (size_t)(in ? lane : 0);
+  const size_t stride = a.runs.stride;
+  uint32_t cu[kColU32];
+#pragma unroll
+  for (int c = 0; c < kColU32; ++c) cu[c] = in ? a.runs.u32[(size_t)c * stride + at] : 0u;
+  uint64_t cl[kColU64];
+#pragma unroll
+  for (int c = 0; c < kColU64; ++c) cl[c] = in ? a.runs.u64[(size_t)c * stride + at] : 0u;
+  uint64_t cnt[kColU32];
+#pragma unroll
+  for (int c = 0; c < kColU32; ++c) {
+    if (c == CU_GABSK || c == CU_GRELK) continue;
+    cnt[c] = (c == CU_MMABS || c == CU_MMREL) ? wave_max((uint64_t)cu[c]) : wave_sum((uint64_t)cu[c]);
+  }
+  uint64_t fmm = in ? cl[CL_FIRSTMM] : kNone, fviol = in ? cl[CL_FIRSTVIOL] : kNone;
+  fmm = wave_min(fmm);
+  fviol = wave_min(fviol);
+  uint32_t ka = cu[CU_GABSK], kr = cu[CU_GRELK];
+  uint64_t ia = in ? cl[CL_GABSI] : kNone, ir = in ? cl[CL_GRELI] : kNone;
+  wave_argmax(ka, ia);
+  wave_argmax(kr, ir);
+  double sm[7];
+#pragma unroll
+  for (int i = 0; i < 7; ++i) sm[i] = wave_sum(in ? __longlong_as_double((long long)cl[CL_S0 + i]) : 0.0);
+  if (lane != 0) return;
+  kvv_result& o = a.res[d.out_index];
+  const double qnan = __builtin_nan("");
+  const bool imode = d.mode == KVV_MODE_MAX_ABS_DIFF;
+  // counts (as reduce_counts)
+  o.finite_violations = (int64_t)cnt[LC_VIOL];
+  o.nan_gen = (int64_t)cnt[LC_NAN_G];
+  o.nan_ref = (int64_t)cnt[LC_NAN_R];
+  o.posinf_gen = (int64_t)cnt[LC_PINF_G];
+  o.posinf_ref = (int64_t)cnt[LC_PINF_R];
+  o.neginf_gen = (int64_t)cnt[LC_NINF_G];
+  o.neginf_ref = (int64_t)cnt[LC_NINF_R];
+  o.nan_pairs = (int64_t)cnt[LC_NANPAIR];
+  const int64_t nz = (int64_t)cnt[LC_NEAR];
+  o.near_zero_count = nz;
+  o.far_count = d.n - nz;
+  o.far_mismatch_count = (int64_t)cnt[LC_FARMM];
+  o.near_zero_bad_count = (int64_t)cnt[LC_NEARBAD];
+  const int64_t nm = nz < d.max_samples ? nz : d.max_samples;
+  o.near_zero_sample_count = nm;
+  if (a.near_cm) {
+    a.near_cm[2 * seg] = (uint64_t)nz;
+    a.near_cm[2 * seg + 1] = (uint64_t)nm;
+  }
+  if (!(d.flags & kFlagNearAny) || nm == 0) o.near_zero_p99_abs = o.near_zero_mean_abs = qnan;
+  for (int b = 0; b < kBuckets; ++b) o.ulp_hist[b] = cnt[LC_HIST0 + b];
+  o.numel = d.n;
+  const uint64_t mm = cnt[CU_MISM];
+  o.mismatch_count = (int64_t)mm;
+  o.mismatch_max_abs = mm ? (imode ? (double)ikey_value((uint32_t)cnt[CU_MMABS]) : (double)fkey_value((uint32_t)cnt[CU_MMABS]))
+                          : 0.0;
+  o.mismatch_max_rel = mm ? (double)fkey_value((uint32_t)cnt[CU_MMREL]) : 0.0;
+  o.sample_count = d.m;
+  if (d.m == 0) o.p99_abs = o.p99_rel = qnan;
+  o.status = 0;
+  o.reserved = 0;
+  // extrema (as reduce_extrema)
+  o.first_mismatch_index = fmm == kNone ? -1 : (int64_t)fmm;
+  o.first_finite_violation = fviol == kNone ? -1 : (int64_t)fviol;
+  if (d.n == 0) {
+    o.max_abs = 0.0;
+    o.max_abs_index = -1;
+    o.max_rel = 0.0;
+    o.max_rel_index = -1;
+  } else {
+    o.max_abs = imode ? (double)ikey_value(ka) : (double)fkey_value(ka);
+    o.max_abs_index = (int64_t)ia;
+    o.max_rel = (double)fkey_value(kr);
+    o.max_rel_index = (int64_t)ir;
+  }
+  // sums (as reduce_sums)
+  double sg = sm[4], sr = sm[5], sx = sm[6];
+  if (d.flags & kFlagCaptureElems) {
+    sg = sm[0];
+    sr = sm[1];
+    sx = sm[2];
+  } else if (d.flags & kFlagInputSelect) {
+    sg = sr = sx = 0.0;
+    const int64_t nck = (d.m + isel_chunk_len(d) - 1) / isel_chunk_len(d);
+    for (int64_t c = 0; c < nck; ++c) {
+      const double* p = a.isel_sums + (size_t)(d.isel_chunk0 + c) * 3;
+      sg += p[0];
+      sr += p[1];
+      sx += p[2];
+    }
+  }
+  o.sample_sum_gg = sg;
+  o.sample_sum_rr = sr;
+  o.sample_sum_gr = sx;
+  o.sample_cosine = cosine_of(sx, sg, sr);
+  const double gn = sqrt(sg), rn = sqrt(sr);
+  o.sample_norm_ratio = (gn == 0.0 && rn == 0.0) ? 1.0 : (gn == 0.0 ? 0.0 : (rn == 0.0 ? __builtin_inf() : gn / rn));
+  o.sum_gg = sm[0];
+  o.sum_rr = sm[1];
+  o.sum_gr = sm[2];
+  o.sum_dd = sm[3];
+  const double dn = sqrt(sm[3]), rn2 = sqrt(sm[1]);
+  o.rel_l2 = rn2 == 0.0 ? (dn == 0.0 ? 0.0 : __builtin_inf()) : dn / rn2;
+  o.cosine = cosine_of(sm[2], sm[0], sm[1]);
 }
 
 // Near-zero: exclusive prefix of the per-item counts, in item order.
@@ -1658,7 +1773,13 @@ __global__ __launch_bounds__(kBlock) void tail_kernel(TailArgs a) {
   constexpr bool kFirst = LEVEL == 0 || LEVEL == 3;
   const int64_t b = blockIdx.x;
   if (kFirst && b < a.reduce_blocks) {
-    reduce_segment<BATCH>(a, (int)(b / a.reduce_roles), (int)(b % a.reduce_roles), lds.r);
+    if (a.reduce_roles == 0) {
+      // (batches of few runs per segment: a wave per segment)
+      const int seg = (int)b * kWaves + (int)(threadIdx.x >> 6);
+      if (seg < a.nseg) reduce_segment_wave<BATCH>(a, seg);
+    } else {
+      reduce_segment<BATCH>(a, (int)(b / a.reduce_roles), (int)(b % a.reduce_roles), lds.r);
+    }
     return;
   }
   const int64_t sb = b - a.reduce_blocks;
