@@ -180,6 +180,93 @@ __device__ __forceinline__ void sample_pass(const SegDesc& d, int64_t i0, int64_
   }
 }
 
+// The strided samples of a segment with n - 1 <= (17/16)(m - 1) (a segment a
+// little past the sample cap: nearly every element a sample), elements of 1 or
+// 2 bytes (whose element loads fill few bytes of a cache line each; wider
+// elements measured faster with them), 16-byte vector access: windows of
+// kStageSamples samples, whose
+// elements the block first stages in LDS (`wg`, `wr`: kStageElems each) with
+// vector loads; each thread then reads its samples from there.  Otherwise as
+// sample_pass (the same samples, in the same order per thread).
+constexpr int kStageSamples = kIselSampleUnroll * kBlock;
+constexpr int kStageElems = 2304;  // >= kStageSamples * 17/16 + 32: a window's elements and vector slack
+template <int DT>
+__device__ __forceinline__ bool staged_ok(const SegDesc& d) {
+  return sizeof(typename Elem<DT>::T) <= 2 && d.vec && d.m < d.n && 16 * (d.n - 1) <= 17 * (d.m - 1);
+}
+template <int DT, int MODE, typename F>
+__device__ __forceinline__ void sample_pass_staged(const SegDesc& d, int64_t i0, int64_t i1, F&& f, uint4* wg,
+                                                   uint4* wr) {
+  using T = typename Elem<DT>::T;
+  constexpr int V = VecIO<DT>::V;
+  typedef const __attribute__((address_space(1))) u32x4* G4;
+  typedef const __attribute__((address_space(1))) T* GT;
+  const G4 g4 = (G4)d.g;
+  const G4 r4 = (G4)d.r;
+  const int tid = threadIdx.x;
+  const uint32_t den = (uint32_t)(d.m - 1);  // m <= 2^24
+  const double inv_den = 1.0 / (double)den;
+  const uint64_t step_t = (uint64_t)kBlock * d.s_mod;
+  const uint32_t step_q = (uint32_t)(step_t / den), step_r = (uint32_t)(step_t % den);
+  const int64_t step_idx = (int64_t)kBlock * (int64_t)d.s_div + step_q;
+  int64_t idx = sample_index(d, i0 + tid, inv_den);
+  uint32_t rem = (uint32_t)(((uint64_t)(i0 + tid) * d.s_mod) % den);
+  const T* sg = reinterpret_cast<const T*>(wg);
+  const T* sr = reinterpret_cast<const T*>(wr);
+  const int64_t nfull = d.n / V;  // vectors wholly inside the tensor
+#pragma unroll 1
+  for (int64_t s0 = i0; s0 < i1; s0 += kStageSamples) {
+    const int64_t s1 = s0 + kStageSamples < i1 ? s0 + kStageSamples : i1;
+    // the window: the vectors from the one holding the first sample to the one holding the last
+    const int64_t w0 = sample_index(d, s0, inv_den) / V;
+    const int64_t w1 = sample_index(d, s1 - 1, inv_den) / V + 1;
+    for (int64_t j = w0 + tid; j < w1; j += kBlock) {
+      uint4 x, y;
+      if (j < nfull) {
+        const u32x4 a = __builtin_nontemporal_load(g4 + j), b = __builtin_nontemporal_load(r4 + j);
+        x = make_uint4(a.x, a.y, a.z, a.w);
+        y = make_uint4(b.x, b.y, b.z, b.w);
+      } else {
+        // the tensor's partial last vector: its elements one by one
+        T eg[V], er[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const int64_t k = j * V + e;
+          eg[e] = k < d.n ? ((GT)d.g)[k] : (T)0;
+          er[e] = k < d.n ? ((GT)d.r)[k] : (T)0;
+        }
+        __builtin_memcpy(&x, eg, 16);
+        __builtin_memcpy(&y, er, 16);
+      }
+      wg[j - w0] = x;
+      wr[j - w0] = y;
+    }
+    __syncthreads();
+    const int64_t e0 = w0 * V;
+    T gc[kIselSampleUnroll], rc[kIselSampleUnroll];
+#pragma unroll
+    for (int u = 0; u < kIselSampleUnroll; ++u) {
+      const int64_t i = s0 + u * kBlock + tid;
+      gc[u] = rc[u] = (T)0;
+      if (i < s1) {
+        gc[u] = sg[idx - e0];
+        rc[u] = sr[idx - e0];
+      }
+      rem += step_r;
+      const bool carry = rem >= den;
+      rem -= carry ? den : 0u;
+      idx += step_idx + (carry ? 1 : 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kIselSampleUnroll; ++u) {
+      float adf, dn;
+      diff_parts<DT, MODE>(gc[u], rc[u], adf, dn);
+      f(adf, dn, s0 + u * kBlock + tid < s1, gc[u], rc[u]);
+    }
+    __syncthreads();  // (the next window overwrites the stage)
+  }
+}
+
 // Calls f over the block's chunk: contiguous elements when every element is a
 // sample, else the strided sample positions.
 template <int DT, int MODE, typename F>
@@ -479,6 +566,8 @@ __global__ __launch_bounds__(kBlock) void isel_gather_kernel(IselArgs a) {
 template <int DT, int MODE>
 __global__ __launch_bounds__(kBlock) void isel_capture_kernel(IselArgs a) {
   __shared__ float stage[kWaves][2][kIselStage];
+  // a window of staged elements (sample_pass_staged: elements of at most 2 bytes)
+  __shared__ uint4 win[2][sizeof(typename Elem<DT>::T) <= 2 ? kStageElems * 2 / 16 : 1];
   __shared__ uint32_t nb[kWaves][2];
   __shared__ double ss[kWaves][3];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -497,7 +586,7 @@ __global__ __launch_bounds__(kBlock) void isel_capture_kernel(IselArgs a) {
     double sg = 0.0, sr = 0.0, sx = 0.0;
     using E = Elem<DT>;
     const float crlo = d->cap_rel_lo;
-    unit_pass<DT, MODE>(*d, e0, e1, [&](float adf, float den, bool act, typename E::T gc, typename E::T rc) {
+    auto capture = [&](float adf, float den, bool act, typename E::T gc, typename E::T rc) {
       const bool nz = act && !(adf == 0.0f);
       const bool ca = nz && fkey(adf) >= k0;
       // rel_diff is divided out only where it can reach its threshold (set_thresholds)
@@ -519,7 +608,9 @@ __global__ __launch_bounds__(kBlock) void isel_capture_kernel(IselArgs a) {
       sg = fma(g64, g64, sg);
       sr = fma(r64, r64, sr);
       sx = fma(g64, r64, sx);
-    });
+    };
+    if (staged_ok<DT>(*d)) sample_pass_staged<DT, MODE>(*d, e0, e1, capture, win[0], win[1]);
+    else unit_pass<DT, MODE>(*d, e0, e1, capture);
     if (fa) stage_flush(stage[w][0], fa, &st[IS_FILL], ba);
     if (fr) stage_flush(stage[w][1], fr, &st[IS_FILL + 1], br);
     if (__ballot(nan0) && lane == 0) st[IS_CNAN] = 1u;
