@@ -628,7 +628,7 @@ def _meta_from_record(job: _Job) -> Tuple[bool, List[str], Dict[str, Any]]:
         meta["norm_ratio"] = _norm_ratio_value(rec)
     count = rec.mismatch_count
     allclose = count == 0
-    meta["mismatch_rate"] = round((count / numel) if numel else 0.0, 4)
+    meta["mismatch_rate"] = _round4(count / numel) if count else 0.0
     meta["p99_abs"] = None if numel == 0 else rec.p99_abs
     meta["p99_rel"] = None if numel == 0 else rec.p99_rel
     meta["allclose_pass"] = allclose
@@ -669,6 +669,23 @@ def _meta_from_record(job: _Job) -> Tuple[bool, List[str], Dict[str, Any]]:
     return False, [detail], meta
 
 
+def _round4(x: float) -> float:
+    """round(x, 4), exactly, without its decimal conversion where it is not needed.
+
+    round(x, 4) is the double nearest to k / 10^4, k the integer nearest to x * 10^4
+    (exactly).  fl(x * 10^4) is within half an ulp of the exact product, so where it
+    lies clearly away from a half-integer, floor(fl + 0.5) is that k, and k / 10000.0
+    (both exact doubles, k < 2^53) is the nearest double to k / 10^4.  Near a
+    half-integer, and for non-finite or huge x, the built-in takes over."""
+    y = x * 10000.0
+    if -4.0e15 < y < 4.0e15:
+        k = math.floor(y + 0.5)
+        t = y - k
+        if -0.4999 < t < 0.4999:
+            return k / 10000.0 if k else math.copysign(0.0, x)
+    return round(x, 4)
+
+
 def _rounded_or_convention(cos: float, gg: float, rr: float) -> float:
     """GCR:364-372: exact 1.0 / 0.0 for zero norms, else round(cosine, 4).  (A norm is the square root of
     a sum of squares, which is >= 0, -0.0 or NaN: the norm is zero exactly when the sum is.)"""
@@ -678,7 +695,7 @@ def _rounded_or_convention(cos: float, gg: float, rr: float) -> float:
         return 1.0
     if g_zero or r_zero:
         return 0.0
-    return round(float(cos), 4)
+    return _round4(float(cos))
 
 
 def _norm_ratio_value(rec) -> float:
@@ -691,7 +708,7 @@ def _norm_ratio_value(rec) -> float:
         return 0.0
     if r_zero:
         return float("inf")
-    return round(float(rec.sample_norm_ratio), 4)
+    return _round4(float(rec.sample_norm_ratio))
 
 
 def _near_zero_meta(job: _Job, meta: Dict[str, Any], numel: int) -> None:
@@ -705,8 +722,8 @@ def _near_zero_meta(job: _Job, meta: Dict[str, Any], numel: int) -> None:
     far = rec.far_count
     far_mm = rec.far_mismatch_count
     meta["near_zero_abs"] = float(th["near_zero_abs"])
-    meta["near_zero_rate"] = round((near / numel) if numel else 0.0, 4)
-    meta["far_mismatch_rate"] = round((far_mm / far) if far else 0.0, 4)
+    meta["near_zero_rate"] = _round4(near / numel) if near else 0.0
+    meta["far_mismatch_rate"] = _round4(far_mm / far) if far_mm else 0.0
     if near == 0:
         meta["near_zero_p99_abs"] = None
         meta["near_zero_mean_abs"] = None
@@ -714,7 +731,7 @@ def _near_zero_meta(job: _Job, meta: Dict[str, Any], numel: int) -> None:
         return
     meta["near_zero_p99_abs"] = rec.near_zero_p99_abs
     meta["near_zero_mean_abs"] = rec.near_zero_mean_abs
-    meta["near_zero_bad_rate"] = round(rec.near_zero_bad_count / near, 4)
+    meta["near_zero_bad_rate"] = _round4(rec.near_zero_bad_count / near)
     meta["near_zero_abs_pass"] = bool(
         meta.get("finite_pass")
         and far_mm == 0

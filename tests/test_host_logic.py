@@ -124,3 +124,29 @@ def test_trial_without_gpu_raises():
             language="hip", correctness_shape={"n": 16}, generated_model_class=trial_models.ScaleAdd,
             reference_model_class=trial_models.ScaleAdd, generate_inputs_fn=trial_models.generate_inputs,
             backend=None, device="cpu", input_seed=1, param_seed=2, tolerance_policy=None, correctness_policy=None)
+
+
+def test_round4_matches_builtin_round():
+    """verdict._round4 is round(x, 4) bit for bit (signed zeros, NaN and infinities included), on random
+    values of every magnitude and on values a few ulps either side of the ties k / 10^4 + 5e-5."""
+    import math
+    import random
+    from kernelverse_amd.verdict import _round4
+    rng = random.Random(20261202)
+    vals = [0.0, -0.0, 1.0, -1.0, 0.99995, 0.00005, -0.00005, 1e-300, -1e-300, 5e-5, 1.5e-4, 2.5e-4,
+            math.inf, -math.inf, math.nan, 1e15, -1e15, 4e11, 4.1e11, 1e300]
+    for _ in range(20000):
+        e = rng.uniform(-12, 12)
+        vals.append(rng.choice((1, -1)) * 10 ** e)
+        vals.append(rng.random())
+    for _ in range(20000):
+        k = rng.randint(-10**7, 10**7)
+        t = (k + 0.5) / 10000.0
+        for steps in range(-3, 4):
+            x = t
+            for _ in range(abs(steps)):
+                x = math.nextafter(x, math.inf if steps > 0 else -math.inf)
+            vals.append(x)
+    for x in vals:
+        a, b = _round4(x), round(x, 4)
+        assert (a != a and b != b) or (a == b and math.copysign(1.0, a) == math.copysign(1.0, b)), (x, a, b)
