@@ -581,10 +581,11 @@ constexpr double kRoundRate3[3] = {1.18, 1.0, 0.79};
 // issue (e.g. fp32 pairs that differ everywhere): the scan's oldest waves are
 // issued first.  Measured with equal shares on the C4 batch (per-wave clocks):
 // the rounds' waves ended at 575 / 641 / 764 us (fp32) and 179 / 196 / 219 us
-// (bf16) on average; the fp32 rates refined once from the shares below (645 /
-// 668 / 718 us at 1.10 / 1.0 / 0.86).
-constexpr double kBatchRoundRate3[3] = {1.10, 1.0, 0.86};
-constexpr double kBatchRoundRateF32[3] = {1.14, 1.0, 0.80};
+// (bf16) on average; refined from the ends the cost-weighted shares then gave
+// (fp32 676 / 690 / 701 us at 1.14 / 1.0 / 0.80, bf16 205 / 209 / 213 us at
+// 1.10 / 1.0 / 0.86).
+constexpr double kBatchRoundRate3[3] = {1.12, 1.0, 0.84};
+constexpr double kBatchRoundRateF32[3] = {1.16, 1.0, 0.78};
 
 // Relative cost of a batch item by what its segment asks of the main pass, in
 // items of a capture segment (least squares over per-wave clocks of the C4
