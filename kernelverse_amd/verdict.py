@@ -245,43 +245,78 @@ class _Job:
     def __init__(self, gen, ref, path, tolerance_policy, correctness_policy, max_samples, fp8_errors=None):
         self.gen, self.ref, self.path = gen, ref, path
         self.correctness_policy = correctness_policy
-        self.policy = _dtype_policy(ref, tolerance_policy)
-        kp = _lib.KvvPolicy()
-        kp.max_samples = int(max_samples)
+        dt = ref.dtype
+        self.policy = pol = _dtype_policy(ref, tolerance_policy)
+        ms = int(max_samples)
         mad = rtol = atol = 0
-        if "max_abs_diff" in self.policy:
-            kp.mode = _lib.MODE_MAX_ABS_DIFF
-            kp.max_abs_diff = mad = int(self.policy["max_abs_diff"])
-            if not -2**31 <= kp.max_abs_diff < 2**31:
+        if "max_abs_diff" in pol:
+            mode = _lib.MODE_MAX_ABS_DIFF
+            mad = int(pol["max_abs_diff"])
+            if not -2**31 <= mad < 2**31:
                 raise RuntimeError(f"value cannot be converted to type int32_t without overflow")
-            self.tolerance = {"max_abs_diff": int(self.policy["max_abs_diff"])}
+            self.tolerance = {"max_abs_diff": mad}
         else:
-            rtol = float(self.policy["rtol"])
-            atol = float(self.policy["atol"])
-            kp.mode = _lib.MODE_ISCLOSE
-            kp.rtol, kp.atol = rtol, atol
+            rtol = float(pol["rtol"])
+            atol = float(pol["atol"])
+            mode = _lib.MODE_ISCLOSE
             self.tolerance = {"rtol": rtol, "atol": atol}
         self.near_thresholds = None
         nz = None
-        if (ref.dtype in (torch.float16, torch.bfloat16) and is_tolerant_policy(correctness_policy)):
+        if dt in _HALF_DTYPES and is_tolerant_policy(correctness_policy):
             th = thresholds_for_dtype(correctness_policy, _dtype_name(ref))
             if th.get("near_zero_abs") is not None and th.get("max_near_zero_bad_abs") is not None:
                 self.near_thresholds = th
-                kp.flags |= _lib.FLAG_NEAR_ZERO
-                kp.near_zero_abs = float(th["near_zero_abs"])
-                kp.near_zero_bad_abs = float(th["max_near_zero_bad_abs"])
                 nz = (float(th["near_zero_abs"]), float(th["max_near_zero_bad_abs"]))
-        # the policy's part of the single-pair plan key (the values kpolicy was built from)
-        self.pkey = (kp.mode, rtol, atol, mad, nz, int(max_samples))
-        if ref.dtype in _ISFINITE_ERRORS and (FP8_REFERENCE_ERRORS if fp8_errors is None else fp8_errors):
-            raise NotImplementedError(_ISFINITE_ERRORS[ref.dtype])
-        if _COMPLEX_REAL.get(ref.dtype, ref.dtype) not in _DTYPE_CODES:
-            raise TypeError(f"verdict does not support dtype {ref.dtype}")
-        self.kpolicy = kp
+        # the policy's part of the single-pair plan key (the values kpolicy is built from)
+        self.pkey = pkey = (mode, rtol, atol, mad, nz, ms)
+        info = _DTYPE_INFO.get(dt)
+        if info is None:
+            info = _dtype_info(dt)
+        if info[0] is not None and (FP8_REFERENCE_ERRORS if fp8_errors is None else fp8_errors):
+            raise NotImplementedError(info[0])
+        if not info[1]:
+            raise TypeError(f"verdict does not support dtype {dt}")
+        tmpl = _KP_TEMPLATES.get(pkey)
+        if tmpl is None:
+            tmpl = _kp_template(pkey)
+        self.kpolicy = _lib.KvvPolicy.from_buffer_copy(tmpl)
         self.record = None
         self.tol_text = None
-        self.is_float = torch.is_floating_point(ref)
+        self.is_float = info[2]
         self.active = policy_name(correctness_policy)
+
+
+_HALF_DTYPES = (torch.float16, torch.bfloat16)
+_DTYPE_INFO: Dict[Any, Tuple[Optional[str], bool, bool]] = {}
+_KP_TEMPLATES: Dict[tuple, bytes] = {}
+
+
+def _dtype_info(dt) -> Tuple[Optional[str], bool, bool]:
+    """Per dtype: the isfinite error the reference raises for it (or None), whether the library
+    supports it, whether it is a floating type."""
+    info = (_ISFINITE_ERRORS.get(dt), _COMPLEX_REAL.get(dt, dt) in _DTYPE_CODES, dt.is_floating_point)
+    _DTYPE_INFO[dt] = info
+    return info
+
+
+def _kp_template(pkey: tuple) -> bytes:
+    """The C-ABI policy of a job's policy key, as bytes (a fresh KvvPolicy is copied from them per job)."""
+    mode, rtol, atol, mad, nz, ms = pkey
+    kp = _lib.KvvPolicy()
+    kp.max_samples = ms
+    kp.mode = mode
+    if mode == _lib.MODE_MAX_ABS_DIFF:
+        kp.max_abs_diff = mad
+    else:
+        kp.rtol, kp.atol = rtol, atol
+    if nz is not None:
+        kp.flags |= _lib.FLAG_NEAR_ZERO
+        kp.near_zero_abs, kp.near_zero_bad_abs = nz
+    tmpl = bytes(kp)
+    if len(_KP_TEMPLATES) >= 256:
+        _KP_TEMPLATES.clear()
+    _KP_TEMPLATES[pkey] = tmpl
+    return tmpl
 
 
 def _device_for(*tensors) -> torch.device:
