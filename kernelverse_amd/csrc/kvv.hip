@@ -296,7 +296,7 @@ int plan_segment(const kvv_tensor* g, const kvv_tensor* r, const kvv_policy* p, 
 struct WsLayout {
   int64_t run_stride;
   size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample,
-      near_cm, ent, near_wave, ent_fill, wave_range, near_psum, table, chunk_seg, isel_state, isel_seg, isel_chunk,
+      near_cm, ent, near_wave, ent_fill, wave_range, near_psum, table, chunk_seg, isel_state, isel_seg,
       isel_sums, fb_segs, fb_counts, cap_runs, cap_chunks, subtab,
       submm, starts, total;
 };
@@ -382,9 +382,8 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
     L.starts = take((size_t)ngroups * kGroupStarts * 8);  // the main-pass launches' wave ranges
     L.chunk_seg = take((size_t)chunks * 8);
     L.isel_seg = take((size_t)nisel * 4);
-    L.isel_chunk = take((size_t)isel_chunks * 8);  // the input-select passes' chunk work lists
     L.isel_sums = take((size_t)isel_chunks * 3 * 8);
-    L.fb_segs = take((size_t)nisel * 4);           // ... and their segment work list
+    L.fb_segs = take((size_t)nisel * 4);           // the fallback's segment work list
     L.fb_counts = take((size_t)(2 * kMaxGroups + 1) * 4);
     L.cap_runs = take((size_t)run_slots * 16);
     L.cap_chunks = take((size_t)isel_chunks * 8);  // the capture pass's chunk work lists
@@ -425,7 +424,7 @@ struct NearLaunch {
 int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchunk, int nseg, int64_t total_chunks,
                 int64_t nslots, const NearMode& nm, const WsLayout& L, void* ws, kvv_result* out, hipStream_t st,
                 const std::vector<NearLaunch>& nears, bool stream_groups = false, int rounds = 1,
-                int64_t max_runs = -1) {
+                int64_t max_runs = -1, bool stream_ar = true) {
   const bool near = nm.any();
   TailArgs t{};
   if (seg0) t.seg0 = *seg0;
@@ -504,7 +503,7 @@ int launch_tail(const SegDesc* seg0, const SegDesc* dtable, const int64_t* dchun
   int rc = launch(wave_fold ? (nseg + kWaves - 1) / kWaves : nseg * t.reduce_roles, main_hist ? 3 : 0, 0,
                   nm.entries ? 3 : 2);
   if (rc) return rc;
-  if (stream_groups) {
+  if (stream_groups && stream_ar) {
     rc = launch(0, 4, 0, 2);
     if (rc) return rc;
   }
@@ -959,8 +958,8 @@ struct BatchPlan {
   int rounds = 1;              // select rounds per chunk block (every segment of the batch)
   int64_t items = 0, samples = 0, chunks = 0, nslots = 0, run_slots = 0;
   bool near = false;
-  // run-time work lists of the input-select and capture passes (host copies, filled by run_batch)
-  std::vector<int32_t> work_chunks, work_segs, cap_work;
+  // run-time work lists of the fallback and capture passes (host copies, filled by run_batch)
+  std::vector<int32_t> work_segs, cap_work;
   std::vector<uint32_t> work_counts;
 };
 
@@ -1065,7 +1064,6 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   if (bp.groups.size() > (size_t)kMaxGroups) return fail(KVV_E_INVALID, "too many scan groups");
   for (auto& gr : bp.groups) {
     gr.ick_lo = (int64_t)bp.isel_chunk.size() / 2;
-    for (int s = gr.seg_lo; s < gr.seg_hi; ++s) bp.table[s].isel_gchunk0 = (int32_t)gr.ick_lo;
     for (int pass = 0; pass < 2; ++pass) {
       for (int s = gr.seg_lo; s < gr.seg_hi; ++s) {
         const SegDesc& d = bp.table[s];
@@ -1120,17 +1118,15 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     KVV_HIP(hipMemcpyAsync(dstarts, bp.starts.data(), bp.starts.size() * 8, hipMemcpyHostToDevice, st));
   if (bp.chunks) KVV_HIP(hipMemcpyAsync(dchunk, bp.chunk_seg.data(), bp.chunks * 8, hipMemcpyHostToDevice, st));
   int32_t* disel = at<int32_t>(ws, L.isel_seg);
-  int2* dichunk = at<int2>(ws, L.isel_chunk);
   int32_t* dfbseg = at<int32_t>(ws, L.fb_segs);
   uint32_t* dcounts = at<uint32_t>(ws, L.fb_counts);
   int2* dcapchunk = at<int2>(ws, L.cap_chunks);
   const int ngroups = (int)bp.groups.size();
   if (nisel) {
-    // work lists: the input-select passes' start with the segments that do not
-    // capture (none at present), to which the capture final adds those that
-    // fall back; the capture pass's hold the chunks of the capture segments
-    // with strided samples
-    bp.work_chunks.assign((size_t)isel_chunks * 2, 0);
+    // work lists: the fallback's starts with the segments that do not capture
+    // (none at present), to which the capture final adds those that miss; the
+    // capture pass's hold the chunks of the capture segments with strided
+    // samples
     bp.cap_work.assign((size_t)isel_chunks * 2, 0);
     bp.work_segs.clear();
     bp.work_counts.assign((size_t)2 * ngroups + 1, 0u);
@@ -1139,19 +1135,17 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
       for (int64_t k = gr.ick_lo; k < gr.ick_lo + gr.ick_n; ++k) {
         const int32_t s = bp.isel_chunk[2 * k];
         const uint32_t f = bp.table[s].flags;
-        std::vector<int32_t>& list = (f & kFlagCapture) ? bp.cap_work : bp.work_chunks;
-        uint32_t& cnt = bp.work_counts[(f & kFlagCapture) ? ngroups + 1 + g : g];
-        if ((f & kFlagCapture) && (f & kFlagCaptureElems)) continue;  // captured by the main pass
+        if (!(f & kFlagCapture) || (f & kFlagCaptureElems)) continue;  // not captured, or by the main pass
+        uint32_t& cnt = bp.work_counts[ngroups + 1 + g];
         const int64_t at_k = gr.ick_lo + cnt++;
-        list[2 * at_k] = s;
-        list[2 * at_k + 1] = bp.isel_chunk[2 * k + 1];
+        bp.cap_work[2 * at_k] = s;
+        bp.cap_work[2 * at_k + 1] = bp.isel_chunk[2 * k + 1];
       }
     }
     for (int32_t s : bp.isel_seg)
       if (!(bp.table[s].flags & kFlagCapture)) bp.work_segs.push_back(s);
     bp.work_counts[ngroups] = (uint32_t)bp.work_segs.size();
     KVV_HIP(hipMemcpyAsync(disel, bp.isel_seg.data(), nisel * 4, hipMemcpyHostToDevice, st));
-    KVV_HIP(hipMemcpyAsync(dichunk, bp.work_chunks.data(), isel_chunks * 8, hipMemcpyHostToDevice, st));
     KVV_HIP(hipMemcpyAsync(dcapchunk, bp.cap_work.data(), isel_chunks * 8, hipMemcpyHostToDevice, st));
     if (!bp.work_segs.empty())
       KVV_HIP(hipMemcpyAsync(dfbseg, bp.work_segs.data(), bp.work_segs.size() * 4, hipMemcpyHostToDevice, st));
@@ -1166,8 +1160,6 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   ia.buf[1] = at<float>(ws, L.sample_rel);
   ia.res = out;
   ia.cap_runs = at<uint4>(ws, L.cap_runs);
-  ia.fb_chunks = dichunk;
-  ia.fb_ccount = dcounts;
   ia.fb_segs = dfbseg;
   ia.fb_scount = dcounts + ngroups;
   // input-select segments: their state is cleared, and the capture thresholds
@@ -1224,37 +1216,36 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   }
   if (nisel) {
     // p99 of the input-select segments: the capture segments' selection among
-    // their captured values; then, for the other input-select segments and for
-    // capture segments that missed, histograms, target bins, gather, final select
+    // their captured values; then the fallback, one launch per group, for the
+    // other input-select segments and the capture segments that missed (its
+    // blocks loop over the list, which is empty unless a capture missed)
     hipLaunchKernelGGL(isel_cap_final_kernel, dim3((unsigned)(2 * nisel)), dim3(kBlock), 0, st, ia);
     KVV_HIP(hipGetLastError());
-    // (the passes loop over their work lists, which may be short: at most kIselWorkBlocks blocks)
     IselArgs wl = ia;
     wl.segs = dfbseg;
     wl.nsegs = dcounts + ngroups;
-    for (int pass = 0; pass < 2; ++pass) {
-      for (int g = 0; g < ngroups; ++g) {
-        const auto& gr = bp.groups[g];
-        if (gr.ick_n == 0) continue;
-        IselFn fn = isel_fn(gr.dt, pass);
-        if (!fn) return fail(KVV_E_INVALID, "no input-select kernel for dtype");
-        IselArgs x = wl;
-        x.chunks = dichunk + gr.ick_lo;
-        x.nchunks = dcounts + g;
-        const int64_t grid = gr.ick_n < kIselWorkBlocks ? gr.ick_n : kIselWorkBlocks;
-        hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(kBlock), 0, st, x);
-        KVV_HIP(hipGetLastError());
-      }
-      const int64_t sgrid = nisel < kIselWorkBlocks ? nisel : kIselWorkBlocks;
-      if (pass == 0) hipLaunchKernelGGL(isel_find_kernel, dim3((unsigned)sgrid), dim3(kBlock), 0, st, wl);
-      else hipLaunchKernelGGL(isel_final_kernel, dim3((unsigned)sgrid), dim3(kBlock), 0, st, wl);
+    const int64_t fgrid = nisel < kIselWorkBlocks ? nisel : kIselWorkBlocks;
+    for (int g = 0; g < ngroups; ++g) {
+      const auto& gr = bp.groups[g];
+      if (gr.isel_n == 0) continue;
+      IselFn fn = isel_fn(gr.dt, 0);
+      if (!fn) return fail(KVV_E_INVALID, "no input-select kernel for dtype");
+      IselArgs x = wl;
+      x.group = g;
+      hipLaunchKernelGGL(fn, dim3((unsigned)fgrid), dim3(kBlock), 0, st, x);
       KVV_HIP(hipGetLastError());
     }
   }
   int64_t max_runs = 0;
-  for (const auto& d : bp.table) max_runs = d.run_n > max_runs ? d.run_n : max_runs;
+  // abs/rel groups that the one-block stream select takes (large, with sample
+  // arrays, not selected from the inputs): none, and its launch is left out
+  bool stream_ar = false;
+  for (const auto& d : bp.table) {
+    max_runs = d.run_n > max_runs ? d.run_n : max_runs;
+    stream_ar = stream_ar || (d.chunk_count > 0 && d.m > kSmall && !(d.flags & kFlagInputSelect));
+  }
   return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, near, L, ws, out, st, nears,
-                     bp.stream_groups, bp.rounds, max_runs);
+                     bp.stream_groups, bp.rounds, max_runs, stream_ar);
 }
 
 }  // namespace

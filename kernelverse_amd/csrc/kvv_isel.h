@@ -6,28 +6,24 @@
 // Used by batch launches with many large groups (C4-like batches), for
 // contiguous segments: the main pass then writes no sample arrays for them
 // (8 bytes per sample, more than a bf16 pair's own 4) and walks no sample
-// positions, and the selection reads the samples twice instead of the sample
-// arrays three times, spread over chunks instead of one block per group.
-// Four launches after the main pass:
+// positions.  Most segments capture their order statistics (the capture path
+// below); a segment whose capture misses is selected from its inputs by
+// isel_fallback_kernel, one block per segment, in four steps:
 //
-//   isel_hist_kernel    one block per chunk of samples: 11-bit
-//                       histograms of the top key digit (bits 31..21) of
-//                       abs_diff and rel_diff, added into the segment's global
-//                       histograms (nonzero bins only); exact zeros (identical
-//                       pairs) are only counted.  The block also sums g^2,
-//                       r^2 and g*r over its samples (the sampled cosine and
-//                       norm ratio, GCR:351-393), which the run fold adds up
-//                       in chunk order;
-//   isel_find_kernel    one block per segment: the bins of the two order
-//                       statistics of each array and the count below them;
-//   isel_gather_kernel  one block per chunk: the values that fall in those bins
-//                       (zeros aside) are appended, through a per-wave LDS
-//                       stage, to the segment's sample region, whose space the
-//                       workspace holds anyway;
-//   isel_final_kernel   one block per segment: the order statistics among the
-//                       zeros and the appended values (in LDS when at most
-//                       kSmall were appended, else by streaming digit passes),
-//                       interpolated like torch.quantile.
+//   hist    per chunk of samples: 11-bit histograms of the top key digit
+//           (bits 31..21) of abs_diff and rel_diff, added into the segment's
+//           histograms (nonzero bins only); exact zeros (identical pairs) are
+//           only counted.  The chunk's sums of g^2, r^2 and g*r over its
+//           samples (the sampled cosine and norm ratio, GCR:351-393) are left
+//           for the run fold, which adds them up in chunk order;
+//   find    the bins of the two order statistics of each array and the count
+//           below them;
+//   gather  per chunk: the values that fall in those bins (zeros aside) are
+//           appended, through a per-wave LDS stage, to the segment's sample
+//           region, whose space the workspace holds anyway;
+//   final   the order statistics among the zeros and the appended values (in
+//           LDS when at most kSmall were appended, else by streaming digit
+//           passes), interpolated like torch.quantile.
 //
 // abs_diff and rel_diff are computed exactly as the main pass's samples are
 // (sample_pair), so the result equals the selection over sample arrays.
@@ -45,12 +41,10 @@ struct IselArgs {
   float* buf[2];           // the sample arrays: space for the appended abs_diff, rel_diff
   kvv_result* res;
   const uint4* cap_runs;   // capture final: the run records of the main pass
-  // capture final: the work lists of the input-select passes, to which it adds the segments that fall back
-  // (chunks: a region per dtype group from SegDesc::isel_gchunk0, counted in fb_ccount[isel_group])
-  int2* fb_chunks;
-  uint32_t* fb_ccount;
+  // capture final: the fallback's segment list, to which it adds the segments that miss
   int32_t* fb_segs;
   uint32_t* fb_scount;
+  int32_t group;           // fallback launch: the dtype group whose segments it takes
 };
 
 // abs_diff and the rel_diff denominator of one pair, as elem_test / sample_pair
@@ -307,14 +301,15 @@ constexpr int kIselWorkBlocks = 1024;
 //                          part of the segment's sample region (from the run's
 //                          first sample on); the others
 //                          are counted (IS_BELOW); each run leaves a record;
-//   isel_cap_final_kernel  one block per segment: the runs' captured values
-//                          are moved together, then an order statistic of
-//                          rank t lies among the zeros (t < zeros), the values
-//                          below the thresholds (missed) or the captured ones
-//                          (rank t - zeros - below there).  If either array
-//                          misses one, the segment is added to the work lists
-//                          of the input-select passes, which select it from
-//                          its inputs.
+//   isel_cap_final_kernel  one block per segment and array: the runs'
+//                          captured values are moved together, then an order
+//                          statistic of rank t lies among the zeros
+//                          (t < zeros), the values below the thresholds
+//                          (missed) or the captured ones (rank
+//                          t - zeros - below there).  If either array misses
+//                          one, the segment is added to the fallback's list,
+//                          and isel_fallback_kernel selects it from its
+//                          inputs.
 //
 // The threshold rank leaves 88 of the 4096 pivot values above it: 1 % of them
 // (41) plus six standard deviations of that count (6.4 each) and a margin, so
@@ -440,33 +435,35 @@ __global__ __launch_bounds__(kBlock) void isel_pivot_kernel(IselArgs a) {
   if (tid == 0) set_thresholds(d, zero_a ? kZeroKey : pfx[0], na, zero_r ? kZeroKey : pfx[1], nr);
 }
 
+// LDS of the fallback's histogram step: bins 2048 + lane take the adds of a
+// lane without a counted value (no branch, no shared word).
+struct HistLds {
+  uint32_t h[2][2048 + 64];
+  uint32_t zs[kWaves];
+  double ss[kWaves][3];
+};
+
+// Fallback step 1, one chunk (samples e0..e1 of d, batch-wide chunk gchunk):
+// its top-digit histograms added into the segment's, its zeros counted, its
+// sampled sums stored.  Called by all threads of the block.
 template <int DT, int MODE>
-__global__ __launch_bounds__(kBlock) void isel_hist_kernel(IselArgs a) {
-  // bins 2048 + lane: a lane without a counted value adds there (no branch, no shared word)
-  __shared__ uint32_t h[2][2048 + 64];
-  __shared__ uint32_t zs[kWaves];
-  __shared__ double ss[kWaves][3];
+__device__ inline void isel_hist_chunk(const IselArgs& a, const SegDesc& d, int64_t e0, int64_t e1, int64_t gchunk,
+                                       HistLds& H) {
   const int tid = threadIdx.x, lane = tid & 63;
-  const uint32_t nwork = *a.nchunks;
-#pragma unroll 1
-  for (uint32_t b = blockIdx.x; b < nwork; b += gridDim.x) {
-  const SegDesc* d;
-  int64_t e0, e1, gchunk;
-  chunk_range(a, b, d, e0, e1, gchunk);
-  uint32_t* st = a.state + (size_t)d->isel_slot * kIselStateWords;
-  for (int i = tid; i < 2 * (2048 + 64); i += kBlock) (&h[0][0])[i] = 0;
+  uint32_t* st = a.state + (size_t)d.isel_slot * kIselStateWords;
+  for (int i = tid; i < 2 * (2048 + 64); i += kBlock) (&H.h[0][0])[i] = 0;
   __syncthreads();
   using E = Elem<DT>;
   uint32_t zeros = 0;
   double sg = 0.0, sr = 0.0, sx = 0.0;
-  unit_pass<DT, MODE>(*d, e0, e1, [&](float adf, float den, bool act, typename E::T gc, typename E::T rc) {
+  unit_pass<DT, MODE>(d, e0, e1, [&](float adf, float den, bool act, typename E::T gc, typename E::T rc) {
     const bool z = adf == 0.0f;
     zeros += act && z ? 1u : 0u;
     const bool cnt = act && !z;
     const uint32_t ba = cnt ? fkey(adf) >> 21 : 2048u + lane;
     const uint32_t br = cnt ? fkey(adf / den) >> 21 : 2048u + lane;
-    atomicAdd(&h[0][ba], 1u);
-    atomicAdd(&h[1][br], 1u);
+    atomicAdd(&H.h[0][ba], 1u);
+    atomicAdd(&H.h[1][br], 1u);
     // inactive lanes hold zero codes, which add 0
     const double g64 = E::f64(gc), r64 = E::f64(rc);
     sg = fma(g64, g64, sg);
@@ -474,33 +471,32 @@ __global__ __launch_bounds__(kBlock) void isel_hist_kernel(IselArgs a) {
     sx = fma(g64, r64, sx);
   });
   zeros = wave_sum(zeros);
-  if (lane == 0) zs[tid >> 6] = zeros;
+  if (lane == 0) H.zs[tid >> 6] = zeros;
   // the chunk's sampled sums, in a fixed order (bit-reproducible)
   sg = wave_sum(sg);
   sr = wave_sum(sr);
   sx = wave_sum(sx);
   if (lane == 0) {
-    ss[tid >> 6][0] = sg;
-    ss[tid >> 6][1] = sr;
-    ss[tid >> 6][2] = sx;
+    H.ss[tid >> 6][0] = sg;
+    H.ss[tid >> 6][1] = sr;
+    H.ss[tid >> 6][2] = sx;
   }
   __syncthreads();
   if (tid < 3) {
     double t = 0.0;
-    for (int w = 0; w < kWaves; ++w) t += ss[w][tid];
+    for (int w = 0; w < kWaves; ++w) t += H.ss[w][tid];
     a.sums[(size_t)gchunk * 3 + tid] = t;
   }
   for (int i = tid; i < 2 * 2048; i += kBlock) {
-    const uint32_t c = h[i >> 11][i & 2047];
+    const uint32_t c = H.h[i >> 11][i & 2047];
     if (c) atomicAdd(&st[IS_HIST + i], c);
   }
   if (tid == 0) {
     uint32_t t = 0;
-    for (int w = 0; w < kWaves; ++w) t += zs[w];
+    for (int w = 0; w < kWaves; ++w) t += H.zs[w];
     if (t) atomicAdd(&st[IS_ZEROS], t);
   }
   __syncthreads();
-  }
 }
 
 // Writes the wave's LDS stage out to buf, at space reserved in the segment's
@@ -526,26 +522,22 @@ __device__ __forceinline__ void stage_append(float* stage, uint32_t& fill, bool 
   fill += (uint32_t)__popcll(b);
 }
 
+// Fallback step 3, one chunk: its values in the target bins appended to the
+// segment's sample region.  Called by all threads of the block; each wave's
+// stage is its own and written out at the end of the chunk.
 template <int DT, int MODE>
-__global__ __launch_bounds__(kBlock) void isel_gather_kernel(IselArgs a) {
-  __shared__ float stage[kWaves][2][kIselStage];
+__device__ inline void isel_gather_chunk(const IselArgs& a, const SegDesc& d, int64_t e0, int64_t e1,
+                                         float (&stage)[kWaves][2][kIselStage]) {
   const int w = threadIdx.x >> 6;
-  const uint32_t nwork = *a.nchunks;
-#pragma unroll 1
-  for (uint32_t b = blockIdx.x; b < nwork; b += gridDim.x) {
-  // (each wave's stage is its own and written out at the end of the chunk: no barrier between chunks)
-  const SegDesc* d;
-  int64_t e0, e1, gchunk;
-  chunk_range(a, b, d, e0, e1, gchunk);
-  uint32_t* st = a.state + (size_t)d->isel_slot * kIselStateWords;
+  uint32_t* st = a.state + (size_t)d.isel_slot * kIselStateWords;
   const bool nan0 = st[IS_NAN] != 0, nan1 = st[IS_NAN + 1] != 0;
-  if (nan0 && nan1) continue;
+  if (nan0 && nan1) return;
   const uint32_t p00 = st[IS_PFX], p01 = st[IS_PFX + 1], p10 = st[IS_PFX + 2], p11 = st[IS_PFX + 3];
-  float* ba = a.buf[0] + d->sample_off;
-  float* br = a.buf[1] + d->sample_off;
+  float* ba = a.buf[0] + d.sample_off;
+  float* br = a.buf[1] + d.sample_off;
   uint32_t fa = 0, fr = 0;
   using T = typename Elem<DT>::T;
-  unit_pass<DT, MODE>(*d, e0, e1, [&](float adf, float den, bool act, T, T) {
+  unit_pass<DT, MODE>(d, e0, e1, [&](float adf, float den, bool act, T, T) {
     const float rel = adf / den;
     const uint32_t ka = fkey(adf) >> 21, kr = fkey(rel) >> 21;
     const bool cnt = act && adf != 0.0f;
@@ -554,15 +546,15 @@ __global__ __launch_bounds__(kBlock) void isel_gather_kernel(IselArgs a) {
   });
   if (fa) stage_flush(stage[w][0], fa, &st[IS_GFILL], ba);
   if (fr) stage_flush(stage[w][1], fr, &st[IS_GFILL + 1], br);
-  }
 }
 
 // The capture pass of the capture segments with strided samples, one block
 // per chunk of their samples: the sampled values at or above the pivot
 // thresholds are appended (through per-wave LDS stages) to the segment's
 // sample region, counted in IS_FILL; the nonzero ones below are counted in
-// IS_BELOW; and the chunk's sampled sums are left as isel_hist_kernel leaves
-// them.  (Dense capture segments are captured by the main pass.)
+// IS_BELOW; and the chunk's sampled sums are left as the fallback's
+// histogram step leaves them.  (Dense capture segments are captured by the
+// main pass.)
 template <int DT, int MODE>
 __global__ __launch_bounds__(kBlock) void isel_capture_kernel(IselArgs a) {
   __shared__ float stage[kWaves][2][kIselStage];
@@ -732,18 +724,13 @@ __global__ __launch_bounds__(kBlock) void isel_cap_final_kernel(IselArgs a) {
   const CapRanks c0 = cap_ranks(d, cap[0], st[IS_BELOW], nan[0], rank64);
   const CapRanks c1 = cap_ranks(d, cap[1], st[IS_BELOW + 1], nan[1], rank64);
   if (st[IS_CNEG] != 0 || c0.miss || c1.miss) {
-    // the input-select passes take the segment over, from cleared histograms
-    // and counts (not the words either block reads above)
+    // the fallback takes the segment over, from cleared histograms and counts
+    // (not the words either block reads above)
     if (x != 0) return;
     __syncthreads();
     for (int i = tid; i <= IS_BASE + 3; i += kBlock)
       if (i != IS_FILL && i != IS_FILL + 1) st[i] = 0;
-    if (tid == 0) {
-      a.fb_segs[atomicAdd(a.fb_scount, 1u)] = seg;
-      const uint32_t nck = (uint32_t)((d.m + isel_chunk_len(d) - 1) / isel_chunk_len(d));
-      const uint32_t at = atomicAdd(&a.fb_ccount[d.isel_group], nck);
-      for (uint32_t ck = 0; ck < nck; ++ck) a.fb_chunks[d.isel_gchunk0 + at + ck] = make_int2(seg, (int)ck);
-    }
+    if (tid == 0) a.fb_segs[atomicAdd(a.fb_scount, 1u)] = seg;
     return;
   }
   const CapRanks& c = x == 0 ? c0 : c1;
@@ -759,13 +746,13 @@ __global__ __launch_bounds__(kBlock) void isel_cap_final_kernel(IselArgs a) {
   if (tid == 0) store_p99(a.res[d.out_index], x, key, wgt, nan[x]);
 }
 
-__global__ __launch_bounds__(kBlock) void isel_find_kernel(IselArgs a) {
-  __shared__ SelectLds L;
+#endif  // KVV_COMMON_KERNELS
+
+// ------------------------------------------------------------ fallback
+// Fallback step 2: the bins of both order statistics of each array and the
+// count below them.  Called by all threads of the block.
+__device__ inline void isel_find_seg(const IselArgs& a, const SegDesc& d, SelectLds& L) {
   const int tid = threadIdx.x;
-  const uint32_t nwork = *a.nsegs;
-#pragma unroll 1
-  for (uint32_t wi = blockIdx.x; wi < nwork; wi += gridDim.x) {
-  const SegDesc& d = a.table[a.segs[wi]];
   uint32_t* st = a.state + (size_t)d.isel_slot * kIselStateWords;
   uint64_t rank64[2];
   float wgt;
@@ -791,16 +778,12 @@ __global__ __launch_bounds__(kBlock) void isel_find_kernel(IselArgs a) {
     }
     __syncthreads();
   }
-  }
 }
 
-__global__ __launch_bounds__(kBlock) void isel_final_kernel(IselArgs a) {
-  __shared__ SelectLds L;
+// Fallback step 4: the order statistics among the zeros and the appended
+// values, interpolated like torch.quantile.  Called by all threads.
+__device__ inline void isel_final_seg(const IselArgs& a, const SegDesc& d, SelectLds& L) {
   const int tid = threadIdx.x;
-  const uint32_t nwork = *a.nsegs;
-#pragma unroll 1
-  for (uint32_t wi = blockIdx.x; wi < nwork; wi += gridDim.x) {
-  const SegDesc& d = a.table[a.segs[wi]];
   const uint32_t* st = a.state + (size_t)d.isel_slot * kIselStateWords;
   uint64_t rank64[2];
   float wgt;
@@ -846,6 +829,53 @@ __global__ __launch_bounds__(kBlock) void isel_final_kernel(IselArgs a) {
     if (tid == 0) store_p99(a.res[d.out_index], x, key, wgt, nan);
     __syncthreads();
   }
+}
+
+// The block's writes to global memory (state words, appended values) reach the
+// block's later reads: the steps of one segment run in one block.
+__device__ __forceinline__ void fallback_step_sync() {
+  __threadfence();
+  __syncthreads();
+  __threadfence();
+}
+
+union FallbackLds {
+  HistLds h;
+  float stage[kWaves][2][kIselStage];
+  SelectLds s;
+};
+
+// The fallback of one dtype group's segments (a.group) on the list a.segs
+// (a.nsegs long: the input-select segments that do not capture, then those
+// whose capture missed): one block per segment, block-strided over the list,
+// taking the four steps over the segment's chunks in turn.  Launched once per
+// group after the capture final; its blocks find the list empty unless a
+// capture missed.
+template <int DT, int MODE>
+__global__ __launch_bounds__(kBlock) void isel_fallback_kernel(IselArgs a) {
+  __shared__ FallbackLds U;
+  const uint32_t nwork = *a.nsegs;
+#pragma unroll 1
+  for (uint32_t wi = blockIdx.x; wi < nwork; wi += gridDim.x) {
+    const SegDesc& d = a.table[a.segs[wi]];
+    if (d.isel_group != a.group) continue;
+    const int64_t len = isel_chunk_len(d);
+    const int64_t nck = (d.m + len - 1) / len;
+#pragma unroll 1
+    for (int64_t ck = 0; ck < nck; ++ck) {
+      const int64_t e0 = ck * len, e1 = e0 + len < d.m ? e0 + len : d.m;
+      isel_hist_chunk<DT, MODE>(a, d, e0, e1, (int64_t)d.isel_chunk0 + ck, U.h);
+    }
+    fallback_step_sync();
+    isel_find_seg(a, d, U.s);
+    fallback_step_sync();
+#pragma unroll 1
+    for (int64_t ck = 0; ck < nck; ++ck) {
+      const int64_t e0 = ck * len, e1 = e0 + len < d.m ? e0 + len : d.m;
+      isel_gather_chunk<DT, MODE>(a, d, e0, e1, U.stage);
+    }
+    fallback_step_sync();
+    isel_final_seg(a, d, U.s);
+    fallback_step_sync();
   }
 }
-#endif  // KVV_COMMON_KERNELS

@@ -161,9 +161,8 @@ struct SegDesc {
   float cap_rel_lo;       // rel_diff can reach cap_key[1] only where abs_diff >= cap_rel_lo * den
   float cap_rel_hi;       // rel_diff reaches cap_key[1] where abs_diff >= fma(cap_rel_hi, |ref|, cap_rel_hic)
   float cap_rel_hic;
-  int32_t isel_group;     // input-select: the segment's dtype group (its chunk work list and count)
-  int32_t isel_gchunk0;   // input-select: the start of that group's region of the chunk work list
-  int32_t isel_pad;
+  int32_t isel_group;     // input-select: the segment's dtype group (which fallback launch takes it)
+  int32_t isel_pad[2];
 };
 
 // Samples per input-select chunk of segment d.

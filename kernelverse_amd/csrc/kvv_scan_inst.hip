@@ -56,13 +56,13 @@ NearFn KVV_NEAR_FN(KVV_DT)(int mode) {
                                   : (NearFn)near_kernel<kDt, KVV_MODE_MAX_ABS_DIFF>;
 }
 
-// Input-select kernels that read the inputs (which: 0 histogram, 1 gather, 2
-// capture pivot, 3 capture pass of strided samples): contiguous segments only,
-// so the dtype's natural test.
+// Input-select kernels that read the inputs (which: 0 fallback, 2 capture
+// pivot, 3 capture pass of strided samples): contiguous segments only, so the
+// dtype's natural test.
 IselFn KVV_ISEL_FN(KVV_DT)(int which) {
   if (which == 2) return (IselFn)isel_pivot_kernel<kDt, kNative>;
   if (which == 3) return (IselFn)isel_capture_kernel<kDt, kNative>;
-  return which == 1 ? (IselFn)isel_gather_kernel<kDt, kNative> : (IselFn)isel_hist_kernel<kDt, kNative>;
+  return which == 0 ? (IselFn)isel_fallback_kernel<kDt, kNative> : nullptr;
 }
 
 }  // namespace kvv

@@ -107,8 +107,8 @@ def test_workspace_grows_with_samples_and_near_zero():
 def test_many_group_batch_reserves_input_select_state():
     """A batch with more large contiguous pairs than the device has CUs selects
     their p99 from the inputs: its workspace holds 16,640 bytes of state per
-    such pair (plus the segment list, two chunk work lists, the per-chunk
-    sampled sums and the segment work list), which the same batch with
+    such pair (plus the segment list, the capture pass's chunk work list, the
+    per-chunk sampled sums and the fallback's segment list), which the same batch with
     transposed pairs (selected from sample arrays) does not."""
     lib = _lib.load()
     count = 300  # above any device's CU count (no device here: the planner assumes 256)
@@ -120,7 +120,7 @@ def test_many_group_batch_reserves_input_select_state():
     assert lib.kvv_batch_workspace_size(count, contig, contig, pols, ctypes.byref(a)) == 0
     assert lib.kvv_batch_workspace_size(count, transposed, transposed, pols, ctypes.byref(b)) == 0
     state = count * 16_640
-    lists = 256 * (2 * -(-count * 4 // 256) + 2 * -(-count * 8 // 256) + -(-count * 24 // 256))  # one chunk per pair
+    lists = 256 * (2 * -(-count * 4 // 256) + -(-count * 8 // 256) + -(-count * 24 // 256))  # one chunk per pair
     assert a.value - b.value == state + lists
 
 
