@@ -298,7 +298,7 @@ struct WsLayout {
   size_t runs_u32, runs_u64, sample_abs, sample_rel, slots, slot_bytes, item_near, item_near_off, item_near_sum, near_sample,
       near_cm, ent, near_wave, ent_fill, wave_range, near_psum, table, chunk_seg, isel_state, isel_seg,
       isel_sums, fb_segs, fb_counts, cap_runs, cap_chunks, subtab,
-      submm, starts, total;
+      submm, starts, upload_end, total;
 };
 
 // Work-list counts: the input-select passes' chunk lists (one per scan group),
@@ -378,15 +378,17 @@ WsLayout workspace_layout(int64_t run_slots, int64_t samples, int64_t nseg, int6
     L.submm = take((size_t)kArrays * chunks * rounds * kSubMM * 4);
   }
   if (batch) {
+    // what the host writes, in one block [table, upload_end): one copy per call
     L.table = take((size_t)nseg * sizeof(SegDesc));
     L.starts = take((size_t)ngroups * kGroupStarts * 8);  // the main-pass launches' wave ranges
     L.chunk_seg = take((size_t)chunks * 8);
     L.isel_seg = take((size_t)nisel * 4);
-    L.isel_sums = take((size_t)isel_chunks * 3 * 8);
+    L.cap_chunks = take((size_t)isel_chunks * 8);  // the capture pass's chunk work lists
     L.fb_segs = take((size_t)nisel * 4);           // the fallback's segment work list
     L.fb_counts = take((size_t)(2 * kMaxGroups + 1) * 4);
+    L.upload_end = off;
+    L.isel_sums = take((size_t)isel_chunks * 3 * 8);
     L.cap_runs = take((size_t)run_slots * 16);
-    L.cap_chunks = take((size_t)isel_chunks * 8);  // the capture pass's chunk work lists
   }
   L.total = off + 256;
   return L;
@@ -1092,6 +1094,64 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
   return KVV_OK;
 }
 
+// ------------------------------------------------------------ batch uploads
+// What a batch call writes from the host (its table, wave ranges and work
+// lists) lies in one block of the workspace.  It goes over in one copy from a
+// pinned staging buffer per device, which the next call refills only after the
+// copy that read it has finished (its event): one DMA per call instead of one
+// per part from pageable memory (C4: five copies, 68 us of the call).  The
+// buffer is kept until the process ends.  A stream that is being captured
+// into a graph takes the parts as separate copies (a captured copy would read
+// the staging buffer when the graph runs).
+struct UploadPart {
+  size_t at;  // workspace offset
+  const void* src;
+  size_t bytes;
+};
+constexpr int kStageDevices = 64;
+struct Staging {
+  void* buf = nullptr;
+  size_t cap = 0;
+  hipEvent_t done = nullptr;
+  bool pending = false;
+};
+std::mutex g_stage_mu;
+Staging g_stage[kStageDevices];
+
+int upload_parts(const std::vector<UploadPart>& parts, size_t lo, size_t hi, void* ws, hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  KVV_HIP(hipStreamIsCapturing(st, &cs));
+  int dev = -1;
+  KVV_HIP(hipGetDevice(&dev));
+  if (cs != hipStreamCaptureStatusNone || dev < 0 || dev >= kStageDevices) {
+    for (const auto& u : parts)
+      if (u.bytes) KVV_HIP(hipMemcpyAsync((char*)ws + u.at, u.src, u.bytes, hipMemcpyHostToDevice, st));
+    return KVV_OK;
+  }
+  std::lock_guard<std::mutex> lock(g_stage_mu);
+  Staging& S = g_stage[dev];
+  if (S.pending) {
+    KVV_HIP(hipEventSynchronize(S.done));
+    S.pending = false;
+  }
+  const size_t need = hi - lo;
+  if (S.cap < need) {
+    if (S.buf) KVV_HIP(hipHostFree(S.buf));
+    S.buf = nullptr;
+    S.cap = 0;
+    const size_t c = need + need / 4 + 65536;
+    KVV_HIP(hipHostMalloc(&S.buf, c, hipHostMallocDefault));
+    S.cap = c;
+  }
+  if (!S.done) KVV_HIP(hipEventCreateWithFlags(&S.done, hipEventDisableTiming));
+  for (const auto& u : parts)
+    if (u.bytes) std::memcpy((char*)S.buf + (u.at - lo), u.src, u.bytes);
+  KVV_HIP(hipMemcpyAsync((char*)ws + lo, S.buf, need, hipMemcpyHostToDevice, st));
+  KVV_HIP(hipEventRecord(S.done, st));
+  S.pending = true;
+  return KVV_OK;
+}
+
 int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st) {
   const int nseg = (int)bp.table.size();
   if (nseg == 0) return KVV_OK;
@@ -1112,11 +1172,11 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     d.cap_buf[1] = at<float>(ws, L.sample_rel) + d.sample_off;
     d.cap_state = istate + (size_t)d.isel_slot * kIselStateWords;
   }
-  KVV_HIP(hipMemcpyAsync(dtable, bp.table.data(), nseg * sizeof(SegDesc), hipMemcpyHostToDevice, st));
+  std::vector<UploadPart> parts;
+  parts.push_back({L.table, bp.table.data(), nseg * sizeof(SegDesc)});
   int64_t* dstarts = at<int64_t>(ws, L.starts);
-  if (!bp.starts.empty())
-    KVV_HIP(hipMemcpyAsync(dstarts, bp.starts.data(), bp.starts.size() * 8, hipMemcpyHostToDevice, st));
-  if (bp.chunks) KVV_HIP(hipMemcpyAsync(dchunk, bp.chunk_seg.data(), bp.chunks * 8, hipMemcpyHostToDevice, st));
+  parts.push_back({L.starts, bp.starts.data(), bp.starts.size() * 8});
+  parts.push_back({L.chunk_seg, bp.chunk_seg.data(), (size_t)bp.chunks * 8});
   int32_t* disel = at<int32_t>(ws, L.isel_seg);
   int32_t* dfbseg = at<int32_t>(ws, L.fb_segs);
   uint32_t* dcounts = at<uint32_t>(ws, L.fb_counts);
@@ -1145,12 +1205,13 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     for (int32_t s : bp.isel_seg)
       if (!(bp.table[s].flags & kFlagCapture)) bp.work_segs.push_back(s);
     bp.work_counts[ngroups] = (uint32_t)bp.work_segs.size();
-    KVV_HIP(hipMemcpyAsync(disel, bp.isel_seg.data(), nisel * 4, hipMemcpyHostToDevice, st));
-    KVV_HIP(hipMemcpyAsync(dcapchunk, bp.cap_work.data(), isel_chunks * 8, hipMemcpyHostToDevice, st));
-    if (!bp.work_segs.empty())
-      KVV_HIP(hipMemcpyAsync(dfbseg, bp.work_segs.data(), bp.work_segs.size() * 4, hipMemcpyHostToDevice, st));
-    KVV_HIP(hipMemcpyAsync(dcounts, bp.work_counts.data(), (2 * ngroups + 1) * 4, hipMemcpyHostToDevice, st));
+    parts.push_back({L.isel_seg, bp.isel_seg.data(), (size_t)nisel * 4});
+    parts.push_back({L.cap_chunks, bp.cap_work.data(), (size_t)isel_chunks * 8});
+    parts.push_back({L.fb_segs, bp.work_segs.data(), bp.work_segs.size() * 4});
+    parts.push_back({L.fb_counts, bp.work_counts.data(), (size_t)(2 * ngroups + 1) * 4});
   }
+  rc = upload_parts(parts, L.table, L.upload_end, ws, st);
+  if (rc) return rc;
   IselArgs ia{};
   ia.table = dtable;
   ia.segs = disel;
