@@ -1152,6 +1152,21 @@ int upload_parts(const std::vector<UploadPart>& parts, size_t lo, size_t hi, voi
   return KVV_OK;
 }
 
+// ------------------------------------------------------------ side stream
+// A batch whose input-select segments fall in two or more dtype groups runs
+// the groups' pivot and capture launches on two streams: they touch disjoint
+// segments, and each launch is latency-bound, so one group's blocks use the
+// device time the other's leave idle.  One side stream per device (default
+// priority), forked from the caller's stream and joined back into it with
+// events before the main passes; a stream that is being captured keeps every
+// launch on itself.
+struct Side {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mu;
+Side g_side[kStageDevices];
+
 int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStream_t st) {
   const int nseg = (int)bp.table.size();
   if (nseg == 0) return KVV_OK;
@@ -1224,15 +1239,39 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   ia.fb_segs = dfbseg;
   ia.fb_scount = dcounts + ngroups;
   // input-select segments: their state is cleared, and the capture thresholds
-  // estimated, before the main pass (one block per segment, per dtype)
+  // estimated, before the main pass (one block per segment, per dtype); every
+  // other group's launches go to the side stream
+  int isel_groups = 0;
+  for (const auto& gr : bp.groups) isel_groups += gr.isel_n > 0 ? 1 : 0;
+  std::unique_lock<std::mutex> side_lock;
+  Side* side = nullptr;
+  if (isel_groups >= 2) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    KVV_HIP(hipStreamIsCapturing(st, &cs));
+    int dev = -1;
+    KVV_HIP(hipGetDevice(&dev));
+    if (cs == hipStreamCaptureStatusNone && dev >= 0 && dev < kStageDevices) {
+      side_lock = std::unique_lock<std::mutex>(g_side_mu);
+      side = &g_side[dev];
+      if (!side->s) {
+        KVV_HIP(hipStreamCreateWithFlags(&side->s, hipStreamNonBlocking));
+        KVV_HIP(hipEventCreateWithFlags(&side->fork, hipEventDisableTiming));
+        KVV_HIP(hipEventCreateWithFlags(&side->join, hipEventDisableTiming));
+      }
+      KVV_HIP(hipEventRecord(side->fork, st));
+      KVV_HIP(hipStreamWaitEvent(side->s, side->fork, 0));
+    }
+  }
+  int isel_k = 0;
   for (int g = 0; g < ngroups; ++g) {
     const auto& gr = bp.groups[g];
     if (gr.isel_n == 0) continue;
+    const hipStream_t sg = side && (isel_k++ & 1) ? side->s : st;
     IselFn fn = isel_fn(gr.dt, 2);
     if (!fn) return fail(KVV_E_INVALID, "no input-select kernel for dtype");
     IselArgs x = ia;
     x.segs = disel + gr.isel_lo;
-    hipLaunchKernelGGL(fn, dim3((unsigned)gr.isel_n), dim3(kBlock), 0, st, x);
+    hipLaunchKernelGGL(fn, dim3((unsigned)gr.isel_n), dim3(kBlock), 0, sg, x);
     KVV_HIP(hipGetLastError());
     // then the capture pass over the strided samples of the group's capture segments
     const int64_t ncap = bp.work_counts[ngroups + 1 + g];
@@ -1241,9 +1280,14 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
       IselArgs c = ia;
       c.chunks = dcapchunk + gr.ick_lo;
       c.nchunks = dcounts + ngroups + 1 + g;
-      hipLaunchKernelGGL(cf, dim3((unsigned)(ncap < kIselWorkBlocks ? ncap : kIselWorkBlocks)), dim3(kBlock), 0, st, c);
+      hipLaunchKernelGGL(cf, dim3((unsigned)(ncap < kIselWorkBlocks ? ncap : kIselWorkBlocks)), dim3(kBlock), 0, sg, c);
       KVV_HIP(hipGetLastError());
     }
+  }
+  if (side) {
+    KVV_HIP(hipEventRecord(side->join, side->s));
+    KVV_HIP(hipStreamWaitEvent(st, side->join, 0));
+    side_lock.unlock();
   }
   std::vector<NearLaunch> nears;
   bool zeroed = false;
