@@ -136,6 +136,8 @@ def _dtype_policy(tensor, tolerance_policy: Optional[Dict[str, Any]] = None):
 
 def _format_number(value: Any) -> str:
     """GCR:331-335."""
+    if type(value) is float:
+        return format(value, ".6g")
     try:
         return f"{float(value):.6g}"
     except (TypeError, ValueError):
@@ -664,8 +666,10 @@ def _meta_from_record(job: _Job) -> Tuple[bool, List[str], Dict[str, Any]]:
     count = rec.mismatch_count
     allclose = count == 0
     meta["mismatch_rate"] = _round4(count / numel) if count else 0.0
-    meta["p99_abs"] = None if numel == 0 else rec.p99_abs
-    meta["p99_rel"] = None if numel == 0 else rec.p99_rel
+    p99_abs = None if numel == 0 else rec.p99_abs
+    p99_rel = None if numel == 0 else rec.p99_rel
+    meta["p99_abs"] = p99_abs
+    meta["p99_rel"] = p99_rel
     meta["allclose_pass"] = allclose
     meta["normal_metric_pass"] = False
     meta["cosine_metric_pass"] = False
@@ -673,8 +677,10 @@ def _meta_from_record(job: _Job) -> Tuple[bool, List[str], Dict[str, Any]]:
     if is_float:
         meta["finite_pass"] = rec.finite_violations == 0
         _near_zero_meta(job, meta, numel)
-    meta["metric_pass"] = False if allclose else _evaluate_tensor_policy(job.ref, meta, job.correctness_policy)
-    meta["policy_pass"] = bool(allclose or meta["metric_pass"])
+    metric = False if allclose else _evaluate_tensor_policy(job.ref, meta, job.correctness_policy)
+    meta["metric_pass"] = metric
+    ok = bool(allclose or metric)
+    meta["policy_pass"] = ok
     if numel == 0 or count == 0:
         return True, [], meta
     if job.kpolicy.mode == _lib.MODE_MAX_ABS_DIFF:
@@ -687,19 +693,17 @@ def _meta_from_record(job: _Job) -> Tuple[bool, List[str], Dict[str, Any]]:
     ref = job.ref
     first = "()" if ref.dim() == 0 else _unravel(rec.first_mismatch_index, ref.shape)
     meta["first_mismatch_index"] = first
-    ok = bool(meta["policy_pass"])
     if ok:
         return True, [], meta
     # (the policy failed, so policy_pass and metric_pass are False)
+    fmt = _format_number
     detail = (
         f"{path}: policy={active}, policy_pass=False, allclose_pass=False, metric_pass=False, "
         f"normal_metric_pass={meta['normal_metric_pass']}, cosine_metric_pass={meta['cosine_metric_pass']}, "
         f"near_zero_abs_pass={meta.get('near_zero_abs_pass')}, {count}/{numel} elements mismatched, "
-        f"max_abs={_format_number(max_abs)}, max_rel={_format_number(max_rel)}, "
-        f"p99_abs={_format_number(meta['p99_abs'])}, p99_rel={_format_number(meta['p99_rel'])}, "
-        f"cosine_similarity={_format_number(meta['cosine_similarity'])}, "
-        f"norm_ratio={_format_number(meta['norm_ratio'])}, first_mismatch_index={first}, "
-        f"tolerance={job.tol_text if job.tol_text is not None else job.tolerance}"
+        f"max_abs={fmt(max_abs)}, max_rel={fmt(max_rel)}, p99_abs={fmt(p99_abs)}, p99_rel={fmt(p99_rel)}, "
+        f"cosine_similarity={fmt(meta['cosine_similarity'])}, norm_ratio={fmt(meta['norm_ratio'])}, "
+        f"first_mismatch_index={first}, tolerance={job.tol_text if job.tol_text is not None else job.tolerance}"
     )
     return False, [detail], meta
 
