@@ -963,13 +963,48 @@ struct BatchPlan {
   // run-time work lists of the fallback and capture passes (host copies, filled by run_batch)
   std::vector<int32_t> work_segs, cap_work;
   std::vector<uint32_t> work_counts;
+  // the planner's own per-pair scratch
+  std::vector<SegDesc> segs;
+  std::vector<int> order, kinds;
+  // Empties the plan for the next call; the vectors keep their memory, so a
+  // thread's repeated batches of one size allocate (and first-touch) nothing.
+  void reset() {
+    table.clear();
+    chunk_seg.clear();
+    isel_seg.clear();
+    isel_chunk.clear();
+    groups.clear();
+    starts.clear();
+    stream_groups = false;
+    rounds = 1;
+    items = samples = chunks = nslots = run_slots = 0;
+    near = false;
+    work_segs.clear();
+    cap_work.clear();
+    work_counts.clear();
+    segs.clear();
+    order.clear();
+    kinds.clear();
+  }
 };
+
+// The calling thread's plan, reused call after call.
+BatchPlan& thread_plan() {
+  static thread_local BatchPlan bp;
+  bp.reset();
+  return bp;
+}
 
 int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, const kvv_policy* pols, BatchPlan& bp) {
   if (count < 0) return fail(KVV_E_INVALID, "negative count");
   if (count > 0 && (!gens || !refs || !pols)) return fail(KVV_E_INVALID, "null batch arrays");
-  std::vector<SegDesc> segs((size_t)count);
-  std::vector<int> order((size_t)count), kinds((size_t)count);
+  std::vector<SegDesc>& segs = bp.segs;
+  std::vector<int>& order = bp.order;
+  std::vector<int>& kinds = bp.kinds;
+  segs.assign((size_t)count, SegDesc{});
+  order.assign((size_t)count, 0);
+  kinds.assign((size_t)count, 0);
+  bp.table.reserve((size_t)count);
   for (int i = 0; i < count; ++i) {
     int rc = plan_segment(&gens[i], &refs[i], &pols[i], segs[i]);
     if (rc) return fail(rc, "pair " + std::to_string(i) + ": " + g_err);
@@ -1416,7 +1451,7 @@ int kvv_verdict_noalloc(const kvv_tensor* gen, const kvv_tensor* ref, const kvv_
 int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs,
                              const kvv_policy* policies, size_t* bytes) {
   if (!bytes) return kvv::fail(KVV_E_INVALID, "null bytes pointer");
-  kvv::BatchPlan bp;
+  kvv::BatchPlan& bp = kvv::thread_plan();
   int rc = kvv::plan_batch(count, gens, refs, policies, bp);
   if (rc) return rc;
   kvv::NearMode near;
@@ -1430,7 +1465,7 @@ int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_te
 
 int kvv_verdict_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, const kvv_policy* policies,
                       kvv_result* out, void* workspace, size_t workspace_bytes, void* stream) {
-  kvv::BatchPlan bp;
+  kvv::BatchPlan& bp = kvv::thread_plan();
   int rc = kvv::plan_batch(count, gens, refs, policies, bp);
   if (rc) return rc;
   kvv::take_kept(workspace, 0, 0);  // a batch writes the workspace its own way
