@@ -207,9 +207,16 @@ KVV_API int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, cons
 
 /* A batch of independent verdicts -- one per pair, as the per-tensor
  * recursion of _compare_outputs (generated_correctness_runner.py:789-833)
- * produces -- in one main-pass launch with a segmented reduction.
- * gens/refs/policies are HOST arrays of `count` entries; out is a DEVICE
- * array of `count` results. */
+ * produces -- with one main-pass launch per (dtype, test, layout) group and a
+ * segmented reduction; each pair has its own policy (tolerances included).
+ * gens/refs/policies are HOST arrays of `count` entries; out is an array of
+ * `count` results in device memory or pinned host memory.  The call plans on
+ * the host and uploads its pair table with one copy from a pinned staging
+ * buffer; one dtype group's pivot and capture launches may run on a side
+ * stream joined back into `stream`.  The library keeps the staging buffer and
+ * the side stream per device until the process ends.  A stream that is being
+ * captured into a graph is refused (KVV_E_UNSUPPORTED): a replay would reuse
+ * a stale upload. */
 KVV_API int kvv_verdict_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs,
                       const kvv_policy* policies, kvv_result* out, void* workspace,
                       size_t workspace_bytes, void* stream);

@@ -1135,9 +1135,8 @@ int plan_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, co
 // pinned staging buffer per device, which the next call refills only after the
 // copy that read it has finished (its event): one DMA per call instead of one
 // per part from pageable memory (C4: five copies, 68 us of the call).  The
-// buffer is kept until the process ends.  A stream that is being captured
-// into a graph takes the parts as separate copies (a captured copy would read
-// the staging buffer when the graph runs).
+// buffer is kept until the process ends.  (A batch is never captured into a
+// graph: kvv_verdict_batch refuses a capturing stream.)
 struct UploadPart {
   size_t at;  // workspace offset
   const void* src;
@@ -1154,11 +1153,9 @@ std::mutex g_stage_mu;
 Staging g_stage[kStageDevices];
 
 int upload_parts(const std::vector<UploadPart>& parts, size_t lo, size_t hi, void* ws, hipStream_t st) {
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  KVV_HIP(hipStreamIsCapturing(st, &cs));
   int dev = -1;
   KVV_HIP(hipGetDevice(&dev));
-  if (cs != hipStreamCaptureStatusNone || dev < 0 || dev >= kStageDevices) {
+  if (dev < 0 || dev >= kStageDevices) {
     for (const auto& u : parts)
       if (u.bytes) KVV_HIP(hipMemcpyAsync((char*)ws + u.at, u.src, u.bytes, hipMemcpyHostToDevice, st));
     return KVV_OK;
@@ -1193,8 +1190,7 @@ int upload_parts(const std::vector<UploadPart>& parts, size_t lo, size_t hi, voi
 // segments, and each launch is latency-bound, so one group's blocks use the
 // device time the other's leave idle.  One side stream per device (default
 // priority), forked from the caller's stream and joined back into it with
-// events before the main passes; a stream that is being captured keeps every
-// launch on itself.
+// events before the main passes.
 struct Side {
   hipStream_t s = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
@@ -1281,11 +1277,9 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
   std::unique_lock<std::mutex> side_lock;
   Side* side = nullptr;
   if (isel_groups >= 2) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    KVV_HIP(hipStreamIsCapturing(st, &cs));
     int dev = -1;
     KVV_HIP(hipGetDevice(&dev));
-    if (cs == hipStreamCaptureStatusNone && dev >= 0 && dev < kStageDevices) {
+    if (dev >= 0 && dev < kStageDevices) {
       side_lock = std::unique_lock<std::mutex>(g_side_mu);
       side = &g_side[dev];
       if (!side->s) {
@@ -1465,6 +1459,13 @@ int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, const kvv_te
 
 int kvv_verdict_batch(int32_t count, const kvv_tensor* gens, const kvv_tensor* refs, const kvv_policy* policies,
                       kvv_result* out, void* workspace, size_t workspace_bytes, void* stream) {
+  // the call uploads its host-written table (and plans on the host): a graph
+  // would replay a stale upload
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs) != hipSuccess)
+    return kvv::fail(KVV_E_HIP, "hipStreamIsCapturing failed");
+  if (cs != hipStreamCaptureStatusNone)
+    return kvv::fail(KVV_E_UNSUPPORTED, "kvv_verdict_batch cannot be captured into a graph");
   kvv::BatchPlan& bp = kvv::thread_plan();
   int rc = kvv::plan_batch(count, gens, refs, policies, bp);
   if (rc) return rc;

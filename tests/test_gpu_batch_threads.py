@@ -81,3 +81,44 @@ def test_concurrent_batches_match_sequential_ones():
                 d = _diff(a, b)
                 assert not d, (k, it, i, d)
     verdict.release_buffers()
+
+
+def test_batch_refuses_a_capturing_stream():
+    """kvv_verdict_batch on a stream that is being captured into a graph returns
+    KVV_E_UNSUPPORTED and enqueues nothing (a replay would reuse a stale upload of
+    its pair table); the capture itself goes on and replays normally."""
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible: the gpu tests must run on the MI355X box")
+    import ctypes
+    from kernelverse_amd import _lib, verdict
+    lib = _lib.load()
+    pairs = _batch(73, count=8)
+    jobs = [verdict._Job(g, r, f"o{i}", None, None, verdict.MAX_SAMPLES) for i, (g, r) in enumerate(pairs)]
+    n = len(jobs)
+    views = [verdict._device_views(g, r) for g, r in pairs]
+    gts = (_lib.KvvTensor * n)(*[v[0] for v in views])
+    rts = (_lib.KvvTensor * n)(*[v[1] for v in views])
+    pols = (_lib.KvvPolicy * n)(*[j.kpolicy for j in jobs])
+    size = ctypes.c_size_t()
+    _lib.check(lib.kvv_batch_workspace_size(n, gts, rts, pols, ctypes.byref(size)), "kvv_batch_workspace_size")
+    ws = torch.empty(size.value, dtype=torch.uint8, device=DEV)
+    out = torch.zeros(n * ctypes.sizeof(_lib.KvvResult), dtype=torch.uint8, device=DEV)
+    x = torch.zeros(4, device=DEV)
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    _say("batch capture: kvv_verdict_batch inside a capture")
+    with torch.cuda.graph(graph):
+        rc = lib.kvv_verdict_batch(n, gts, rts, pols, out.data_ptr(), ws.data_ptr(), size.value,
+                                   torch.cuda.current_stream().cuda_stream)
+        x.add_(1.0)
+    assert rc == -4, rc  # KVV_E_UNSUPPORTED
+    assert b"captured" in lib.kvv_last_error()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(x.cpu(), torch.ones(4))
+    assert int(out.sum().item()) == 0  # nothing of the batch ran
+    # the same call outside a capture runs
+    _lib.check(lib.kvv_verdict_batch(n, gts, rts, pols, out.data_ptr(), ws.data_ptr(), size.value,
+                                     torch.cuda.current_stream().cuda_stream), "kvv_verdict_batch")
+    torch.cuda.synchronize()
+    assert int(out.sum().item()) != 0
