@@ -71,7 +71,7 @@ enum IselWord {
 };
 static_assert(IS_GFILL + 1 < kIselStateWords && (kIselStateWords * 4) % 256 == 0, "input-select state");
 constexpr int64_t kIselChunk = 1 << 17;        // elements per input-select chunk (every element a sample)
-constexpr int64_t kIselChunkSampled = 1 << 15;  // samples per chunk at strided positions (element loads)
+constexpr int64_t kIselChunkSampled = 1 << 14;  // samples per chunk at strided positions (element loads)
 // Per (large segment, array) slot: level-0 histogram (256), its kH0Copies
 // copies that the main pass's blocks add into (block b into copy b mod
 // kH0Copies: the bins every block touches, e.g. the zeros, would otherwise
