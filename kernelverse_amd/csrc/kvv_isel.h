@@ -293,9 +293,9 @@ constexpr int kIselWorkBlocks = 1024;
 //                          abs/rel keys of kPivotSamples values (kPivotRuns
 //                          runs of kPivotRun consecutive samples, spread over
 //                          the segment), and a lower bound of their order
-//                          statistic at kPivotRank from two histogram levels
-//                          (11 key bits each), which becomes the capture
-//                          threshold (cap_key);
+//                          statistic at kPivotRank from two 2048-bin
+//                          histogram passes over the range of their keys,
+//                          which becomes the capture threshold (cap_key);
 //   main pass              every nonzero sampled value whose key reaches its
 //                          threshold is written, compacted, into its run's
 //                          part of the segment's sample region (from the run's
@@ -403,13 +403,51 @@ __global__ __launch_bounds__(kBlock) void isel_pivot_kernel(IselArgs a) {
   // counts over the block: values at or below zero (their keys go first), NaNs
   uint32_t lo_a = block_sum_nan(low[0], L), lo_r = block_sum_nan(low[1], L);
   const bool na = block_sum_nan(nan[0], L) != 0, nr = block_sum_nan(nan[1], L) != 0;
-  // the order statistic at kPivotRank among the values above zero, by two 11-bit levels
+  // the order statistic at kPivotRank among the values above zero, by two
+  // passes of 2048 bins over the range of those values' keys (then over the
+  // range of the rank's bin): spread over the range, the adds of values that
+  // share their leading key bits do not meet in a few LDS words
   uint32_t resid[2] = {kPivotRank >= lo_a ? kPivotRank - lo_a : 0u, kPivotRank >= lo_r ? kPivotRank - lo_r : 0u};
   const bool zero_a = kPivotRank < lo_a, zero_r = kPivotRank < lo_r;
-  uint32_t pfx[2] = {0u, 0u};
+  uint32_t lo[2], hi[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const uint32_t kk = key[x][k];
+      if (kk > kZeroKey) {
+        mn = kk < mn ? kk : mn;
+        mx = kk > mx ? kk : mx;
+      }
+    }
+    mn = wave_min(mn);
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) {
+      L.sh[x * 8 + (tid >> 6)] = mn;
+      L.sh[x * 8 + 4 + (tid >> 6)] = mx;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    lo[x] = L.sh[x * 8];
+    hi[x] = L.sh[x * 8 + 4];
+    for (int w = 1; w < kWaves; ++w) {
+      lo[x] = L.sh[x * 8 + w] < lo[x] ? L.sh[x * 8 + w] : lo[x];
+      hi[x] = L.sh[x * 8 + 4 + w] > hi[x] ? L.sh[x * 8 + 4 + w] : hi[x];
+    }
+    if (lo[x] > hi[x]) lo[x] = hi[x] = kZeroKey + 1u;  // no value above zero (the rank is then a zero)
+  }
+  __syncthreads();
 #pragma unroll 1
   for (int lev = 0; lev < 2; ++lev) {
-    const int shift = lev == 0 ? 21 : 10;
+    int shift[2];
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const int bits = 32 - __clz(hi[x] - lo[x]);
+      shift[x] = bits > 11 ? bits - 11 : 0;
+    }
     for (int i = tid; i < 2 * 2048; i += kBlock) (&L.h[0][0])[i] = 0;
     __syncthreads();
 #pragma unroll
@@ -417,8 +455,7 @@ __global__ __launch_bounds__(kBlock) void isel_pivot_kernel(IselArgs a) {
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
         const uint32_t kk = key[x][k];
-        const bool in = kk > kZeroKey && (lev == 0 || (kk >> 21) == pfx[x]);
-        if (in) atomicAdd(&L.h[x][(kk >> shift) & 2047u], 1u);
+        if (kk > kZeroKey && kk >= lo[x] && kk <= hi[x]) atomicAdd(&L.h[x][(kk - lo[x]) >> shift[x]], 1u);
       }
     }
     __syncthreads();
@@ -427,12 +464,16 @@ __global__ __launch_bounds__(kBlock) void isel_pivot_kernel(IselArgs a) {
     block_find2<8>(cA, cB, false, resid, bin, below, L.sh);
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
-      pfx[x] = lev == 0 ? bin[x] : ((pfx[x] << 21) | (bin[x] << 10));
+      const uint64_t nlo = (uint64_t)lo[x] + ((uint64_t)bin[x] << shift[x]);
+      const uint64_t nhi = nlo + ((uint64_t)1 << shift[x]) - 1;
+      lo[x] = (uint32_t)nlo;
+      hi[x] = nhi < hi[x] ? (uint32_t)nhi : hi[x];
       resid[x] -= below[x];
     }
     __syncthreads();
   }
-  if (tid == 0) set_thresholds(d, zero_a ? kZeroKey : pfx[0], na, zero_r ? kZeroKey : pfx[1], nr);
+  // the lower end of the rank's final bin: a lower bound of the order statistic
+  if (tid == 0) set_thresholds(d, zero_a ? kZeroKey : lo[0], na, zero_r ? kZeroKey : lo[1], nr);
 }
 
 // LDS of the fallback's histogram step: bins 2048 + lane take the adds of a
