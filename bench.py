@@ -307,7 +307,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the verdict path has no multi-GPU mode "
-                                   "(see DESIGN.md for how it would shard)"}))
+                                   "(it would shard by contiguous index ranges, one process per GPU, merging the "
+                                   "per-rank records in rank order)"}))
         sys.exit(2)
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a ROCm GPU")
