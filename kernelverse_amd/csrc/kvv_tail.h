@@ -375,11 +375,15 @@ __device__ inline void reduce_segment_wave(const TailArgs& a, int seg) {
   uint64_t cl[kColU64];
 #pragma unroll
   for (int c = 0; c < kColU64; ++c) cl[c] = in ? a.runs.u64[(size_t)c * stride + at] : 0u;
+  // every count of a segment is at most its element count: below 2^32 the
+  // sums stay in 32-bit lanes (half the DPP moves of 64-bit ones)
+  const bool n32 = d.n < ((int64_t)1 << 32);
   uint64_t cnt[kColU32];
 #pragma unroll
   for (int c = 0; c < kColU32; ++c) {
     if (c == CU_GABSK || c == CU_GRELK) continue;
-    cnt[c] = (c == CU_MMABS || c == CU_MMREL) ? wave_max((uint64_t)cu[c]) : wave_sum((uint64_t)cu[c]);
+    if (c == CU_MMABS || c == CU_MMREL) cnt[c] = wave_max(cu[c]);
+    else cnt[c] = n32 ? (uint64_t)wave_sum(cu[c]) : wave_sum((uint64_t)cu[c]);
   }
   uint64_t fmm = in ? cl[CL_FIRSTMM] : kNone, fviol = in ? cl[CL_FIRSTVIOL] : kNone;
   fmm = wave_min(fmm);
