@@ -962,14 +962,18 @@ __device__ inline bool range_keys(const float* v, uint32_t count, const uint32_t
       }
     }
   };
-  uint32_t mn = 0xFFFFFFFFu, mx = 0u, nans = 0u;
+  uint32_t mn = 0xFFFFFFFFu, mx = 0u, nans = 0u, zeros = 0u;
   visit([&](uint32_t kk) {
     mn = kk < mn ? kk : mn;
     mx = kk > mx ? kk : mx;
     nans += kk == 0xFFFFFFFFu ? 1u : 0u;
+    zeros += kk == kZeroKey ? 1u : 0u;
   });
   key[0] = key[1] = 0u;
-  if (block_sum_nan(nans, L) != 0) return true;
+  // NaNs and exact zeros counted together (each at most the block's count, below 2^16 when
+  // the values are in registers; else only the NaN count is used)
+  const uint32_t nz = block_sum_nan(regs ? nans | (zeros << 16) : nans, L);
+  if ((regs ? nz & 0xFFFFu : nz) != 0) return true;
   mn = wave_min(mn);
   mx = wave_max(mx);
   if ((tid & 63) == 0) {
@@ -985,6 +989,11 @@ __device__ inline bool range_keys(const float* v, uint32_t count, const uint32_t
     mx = L.sh[w] > mx ? L.sh[w] : mx;
   }
   __syncthreads();
+  // both ranks among the exact zeros, the least values (the p99 of mostly identical pairs): no pass
+  if (regs && mn == kZeroKey && rank[1] < (nz >> 16)) {
+    key[0] = key[1] = kZeroKey;
+    return false;
+  }
   uint32_t lo[2] = {mn, mn}, hi[2] = {mx, mx}, resid[2] = {rank[0], rank[1]};
 #pragma unroll 1
   for (int pass = 0; pass < 4; ++pass) {
