@@ -212,8 +212,9 @@ KVV_API int kvv_batch_workspace_size(int32_t count, const kvv_tensor* gens, cons
  * gens/refs/policies are HOST arrays of `count` entries; out is an array of
  * `count` results in device memory or pinned host memory.  The call plans on
  * the host and uploads its pair table with one copy from a pinned staging
- * buffer; one dtype group's pivot and capture launches may run on a side
- * stream joined back into `stream`.  The library keeps the staging buffer and
+ * buffer; one dtype group's pivot and capture launches, and the launches
+ * after the main passes that the capture final does not feed, may run on a
+ * side stream joined back into `stream`.  The library keeps the staging buffer and
  * the side stream per device until the process ends.  A stream that is being
  * captured into a graph is refused (KVV_E_UNSUPPORTED): a replay would reuse
  * a stale upload. */

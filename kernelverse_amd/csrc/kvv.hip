@@ -1348,28 +1348,6 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     hipLaunchKernelGGL(scan, dim3((unsigned)gr.grid), dim3(kBlock), 0, st, a);
     KVV_HIP(hipGetLastError());
   }
-  if (nisel) {
-    // p99 of the input-select segments: the capture segments' selection among
-    // their captured values; then the fallback, one launch per group, for the
-    // other input-select segments and the capture segments that missed (its
-    // blocks loop over the list, which is empty unless a capture missed)
-    hipLaunchKernelGGL(isel_cap_final_kernel, dim3((unsigned)(2 * nisel)), dim3(kBlock), 0, st, ia);
-    KVV_HIP(hipGetLastError());
-    IselArgs wl = ia;
-    wl.segs = dfbseg;
-    wl.nsegs = dcounts + ngroups;
-    const int64_t fgrid = nisel < kIselWorkBlocks ? nisel : kIselWorkBlocks;
-    for (int g = 0; g < ngroups; ++g) {
-      const auto& gr = bp.groups[g];
-      if (gr.isel_n == 0) continue;
-      IselFn fn = isel_fn(gr.dt, 0);
-      if (!fn) return fail(KVV_E_INVALID, "no input-select kernel for dtype");
-      IselArgs x = wl;
-      x.group = g;
-      hipLaunchKernelGGL(fn, dim3((unsigned)fgrid), dim3(kBlock), 0, st, x);
-      KVV_HIP(hipGetLastError());
-    }
-  }
   int64_t max_runs = 0;
   // abs/rel groups that the one-block stream select takes (large, with sample
   // arrays, not selected from the inputs): none, and its launch is left out
@@ -1378,8 +1356,58 @@ int run_batch(BatchPlan& bp, kvv_result* out, void* ws, size_t ws_bytes, hipStre
     max_runs = d.run_n > max_runs ? d.run_n : max_runs;
     stream_ar = stream_ar || (d.chunk_count > 0 && d.m > kSmall && !(d.flags & kFlagInputSelect));
   }
-  return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, near, L, ws, out, st, nears,
-                     bp.stream_groups, bp.rounds, max_runs, stream_ar);
+  auto tail = [&](hipStream_t ts) {
+    return launch_tail(nullptr, dtable, dchunk, nseg, bp.chunks, bp.nslots, near, L, ws, out, ts, nears,
+                       bp.stream_groups, bp.rounds, max_runs, stream_ar);
+  };
+  if (!nisel) return tail(st);
+  // The tail launches (the run fold, the small groups' selects) need nothing of
+  // the capture final's or the fallback's when every input-select segment
+  // captures (the fallback then writes no chunk sums): they go to the side
+  // stream, beside those launches, and are joined back before the call ends.
+  std::unique_lock<std::mutex> tail_lock;
+  Side* tside = nullptr;
+  if (bp.work_segs.empty()) {
+    int dev = -1;
+    KVV_HIP(hipGetDevice(&dev));
+    if (dev >= 0 && dev < kStageDevices) {
+      tail_lock = std::unique_lock<std::mutex>(g_side_mu);
+      tside = &g_side[dev];
+      if (!tside->s) {
+        KVV_HIP(hipStreamCreateWithFlags(&tside->s, hipStreamNonBlocking));
+        KVV_HIP(hipEventCreateWithFlags(&tside->fork, hipEventDisableTiming));
+        KVV_HIP(hipEventCreateWithFlags(&tside->join, hipEventDisableTiming));
+      }
+      KVV_HIP(hipEventRecord(tside->fork, st));
+      KVV_HIP(hipStreamWaitEvent(tside->s, tside->fork, 0));
+      rc = tail(tside->s);
+      if (rc) return rc;
+      KVV_HIP(hipEventRecord(tside->join, tside->s));
+    }
+  }
+  // p99 of the input-select segments: the capture segments' selection among
+  // their captured values; then the fallback, one launch per group, for the
+  // other input-select segments and the capture segments that missed (its
+  // blocks loop over the list, which is empty unless a capture missed)
+  hipLaunchKernelGGL(isel_cap_final_kernel, dim3((unsigned)(2 * nisel)), dim3(kBlock), 0, st, ia);
+  KVV_HIP(hipGetLastError());
+  IselArgs wl = ia;
+  wl.segs = dfbseg;
+  wl.nsegs = dcounts + ngroups;
+  const int64_t fgrid = nisel < kIselWorkBlocks ? nisel : kIselWorkBlocks;
+  for (int g = 0; g < ngroups; ++g) {
+    const auto& gr = bp.groups[g];
+    if (gr.isel_n == 0) continue;
+    IselFn fn = isel_fn(gr.dt, 0);
+    if (!fn) return fail(KVV_E_INVALID, "no input-select kernel for dtype");
+    IselArgs x = wl;
+    x.group = g;
+    hipLaunchKernelGGL(fn, dim3((unsigned)fgrid), dim3(kBlock), 0, st, x);
+    KVV_HIP(hipGetLastError());
+  }
+  if (!tside) return tail(st);
+  KVV_HIP(hipStreamWaitEvent(st, tside->join, 0));
+  return KVV_OK;
 }
 
 }  // namespace

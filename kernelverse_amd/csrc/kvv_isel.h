@@ -15,7 +15,8 @@
 //           histograms (nonzero bins only); exact zeros (identical pairs) are
 //           only counted.  The chunk's sums of g^2, r^2 and g*r over its
 //           samples (the sampled cosine and norm ratio, GCR:351-393) are left
-//           for the run fold, which adds them up in chunk order;
+//           for the run fold, which adds them up in chunk order (a capture
+//           segment keeps the capture pass's);
 //   find    the bins of the two order statistics of each array and the count
 //           below them;
 //   gather  per chunk: the values that fall in those bins (zeros aside) are
@@ -523,7 +524,9 @@ __device__ inline void isel_hist_chunk(const IselArgs& a, const SegDesc& d, int6
     H.ss[tid >> 6][2] = sx;
   }
   __syncthreads();
-  if (tid < 3) {
+  // (a capture segment's chunk sums are the capture pass's: the run fold may be
+  // reading them while the fallback runs)
+  if (tid < 3 && !(d.flags & kFlagCapture)) {
     double t = 0.0;
     for (int w = 0; w < kWaves; ++w) t += H.ss[w][tid];
     a.sums[(size_t)gchunk * 3 + tid] = t;
