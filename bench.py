@@ -186,7 +186,7 @@ PMC_TRAFFIC = {
     "c3fp8": {"fetch_kib": 131273.0, "write_kib": 9060.4, "fetch_factor": _F2, "write_factor": 1.0},
     "c3int8": {"fetch_kib": 131256.1, "write_kib": 9063.4, "fetch_factor": _F2, "write_factor": 1.0},
     # c4: the whole batch call (every kernel of one kvv_verdict_batch), profiles/verdict_c4_batch_traffic.md
-    "c4": {"fetch_kib": 2071663.4, "write_kib": 148246.1, "fetch_factor": 524288.0 / 262157.0, "write_factor": 1.0},
+    "c4": {"fetch_kib": 2071718.9, "write_kib": 148259.7, "fetch_factor": 524288.0 / 262157.0, "write_factor": 1.0},
 }
 
 
